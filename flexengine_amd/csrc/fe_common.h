@@ -1,0 +1,164 @@
+// Shared device helpers for the gfx950 paged-attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "flexengine_amd.h"
+
+namespace fe {
+
+typedef _Float16 f16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// ---- wave-level helpers (wave64) -------------------------------------------
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+  return __shfl_xor(v, mask, kWave);
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Inclusive prefix sum across the 64 lanes.
+__device__ __forceinline__ int wave_scan_incl_i(int v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    int up = __shfl_up(v, d, kWave);
+    if (lane >= d) v += up;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int readlane_i(int v, int lane) {
+  return __builtin_amdgcn_readlane(v, lane);
+}
+
+// ---- 16-byte global accesses ------------------------------------------------
+
+__device__ __forceinline__ f16x8 ld16(const f16* p) {
+  return *reinterpret_cast<const f16x8*>(p);
+}
+__device__ __forceinline__ void st16(f16* p, f16x8 v) {
+  *reinterpret_cast<f16x8*>(p) = v;
+}
+
+// ---- MFMA wrappers ------------------------------------------------------------
+// v_mfma_f32_16x16x16_f16.  Operand layout for lane l (g = l/16, n = l%16):
+//   A: A[row n][k-slots of group g] (4 halves)   B: B[k-slots of group g][col n]
+//   C: C[row 4g+i][col n], i = 0..3
+// A and B use the same k-slots for a given (g, register), so any assignment of
+// reduction indices to slots is valid as long as both operands follow it.
+__device__ __forceinline__ f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f16x4 lo4(f16x8 v) { return f16x4{v[0], v[1], v[2], v[3]}; }
+__device__ __forceinline__ f16x4 hi4(f16x8 v) { return f16x4{v[4], v[5], v[6], v[7]}; }
+
+// ---- split-K partition ---------------------------------------------------------
+// The keys of every sequence are cut into 64-token "quads" (one 16-token tile
+// per wave of a 256-thread workgroup).  All sequences share one chunk size,
+// chosen on the device from the live context lengths so that the whole batch
+// yields about `target` pieces per KV head:
+//   quads_b = ceil(L_b / 64), chunk = max(1, ceil(sum_b quads_b / target)),
+//   splits_b = ceil(quads_b / chunk).
+// Pieces are numbered sequence-major; piece ids run over [0, sum_b splits_b) <=
+// target + batch.  Every function below is evaluated by a whole wave and
+// returns wave-uniform values.
+
+__device__ __forceinline__ int clamp_len(int L) { return L > 0 ? L : 0; }
+
+__device__ __forceinline__ int split_chunk_quads(const int32_t* ctx, int B, int target) {
+  const int lane = lane_id();
+  int total = 0;
+  for (int base = 0; base < B; base += kWave) {
+    const int b = base + lane;
+    const int L = b < B ? clamp_len(ctx[b]) : 0;
+    total += wave_sum_i((L + 63) >> 6);
+  }
+  const int chunk = (total + target - 1) / target;
+  return chunk > 0 ? chunk : 1;
+}
+
+struct Piece {
+  int b;         // sequence
+  int split;     // index of this piece within the sequence
+  int nsplit;    // pieces of this sequence
+  int L;         // context length of the sequence
+  int tok_begin; // first key position of the piece
+  int tok_end;   // one past the last key position of the piece
+};
+
+// Finds the piece with id `item`; false when item is past the last piece.
+__device__ __forceinline__ bool locate_piece(const int32_t* ctx, int B, int chunk,
+                                             int item, Piece& pc) {
+  const int lane = lane_id();
+  int carry = 0;
+  for (int base = 0; base < B; base += kWave) {
+    const int b = base + lane;
+    const int L = b < B ? clamp_len(ctx[b]) : 0;
+    const int nq = (L + 63) >> 6;
+    const int ns = (nq + chunk - 1) / chunk;
+    const int incl = wave_scan_incl_i(ns) + carry;
+    const int excl = incl - ns;
+    const unsigned long long hit = __ballot(b < B && item >= excl && item < incl);
+    if (hit) {
+      const int src = __builtin_ctzll(hit);
+      pc.b = base + src;
+      pc.L = readlane_i(L, src);
+      pc.nsplit = readlane_i(ns, src);
+      pc.split = item - readlane_i(excl, src);
+      pc.tok_begin = pc.split * chunk * 64;
+      const int e = (pc.split + 1) * chunk * 64;
+      pc.tok_end = e < pc.L ? e : pc.L;
+      return true;
+    }
+    carry = readlane_i(incl, kWave - 1);
+  }
+  return false;
+}
+
+// Number of pieces of sequence b and the id of its first piece.
+__device__ __forceinline__ void seq_pieces(const int32_t* ctx, int B, int chunk, int b,
+                                           int& nsplit, int& first) {
+  const int lane = lane_id();
+  int carry = 0;
+  nsplit = 0;
+  first = 0;
+  for (int base = 0; base < B; base += kWave) {
+    const int bb = base + lane;
+    const int L = bb < B ? clamp_len(ctx[bb]) : 0;
+    const int nq = (L + 63) >> 6;
+    const int ns = (nq + chunk - 1) / chunk;
+    const int incl = wave_scan_incl_i(ns) + carry;
+    if (b >= base && b < base + kWave) {
+      nsplit = readlane_i(ns, b - base);
+      first = readlane_i(incl - ns, b - base);
+      return;
+    }
+    carry = readlane_i(incl, kWave - 1);
+  }
+}
+
+}  // namespace fe
+
+#define FE_CHECK_ARG(cond)                 \
+  do {                                     \
+    if (!(cond)) return FE_ERR_INVALID_ARGUMENT; \
+  } while (0)
+
+#define FE_LAUNCH_STATUS() ((int)hipGetLastError())

@@ -1,0 +1,305 @@
+// Fused single-token paged decode attention for gfx950 (MI355X).
+//
+// Work decomposition
+//   grid = (pieces, kv_heads); one 256-thread workgroup (4 waves) per
+//   (piece of a sequence's keys, KV head).  The pieces come from the
+//   device-side split-K partition in fe_common.h, so every workgroup gets an
+//   equal share of keys whatever the context-length mix.  Within a workgroup
+//   wave w takes the 16-token tiles w, w+4, w+8, ... of the piece (tile engine:
+//   attn_core.h) and the four waves are merged through LDS at the end.  A
+//   sequence cut into several pieces writes fp32 partials plus a base-2
+//   log-sum-exp per query head, and decode_merge_kernel combines them.
+//
+// One wave serves all G = Hq/Hkv query heads of its KV head (the 16 MFMA
+// columns), so every K/V byte is read from HBM once per step; the reference's
+// Triton kernel reads it G times, once per query head
+// (src/flexengine/inference/kernels/paged_attention.py:99-139).
+#include "attn_core.h"
+
+using namespace fe;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kDefaultTarget = 512;
+constexpr int kMaxGroup = 16;
+
+struct DecodeArgs {
+  const f16* q;
+  f16* out;
+  const f16* k_new;
+  const f16* v_new;
+  f16* k_pool;
+  f16* v_pool;
+  const int32_t* tables;
+  const int32_t* ctx;
+  float* ws_o;    // [pieces, Hq, D]
+  float* ws_lse;  // [pieces, Hq]  (base 2)
+  int64_t q_stride;
+  int64_t new_stride;
+  int W, B, Hq, Hkv, G, BS, bs_log2, NB, target;
+  float scale_log2;  // softmax scale * log2(e)
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void paged_decode_kernel(const DecodeArgs a) {
+  using C = TileCfg<D>;
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int chunk = split_chunk_quads(a.ctx, a.B, a.target);
+  Piece pc;
+  if (!locate_piece(a.ctx, a.B, chunk, blockIdx.x, pc)) return;
+
+  const int h = blockIdx.y;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = lane_id();
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int G = a.G;
+  const int b = pc.b;
+
+  TileCore<D> core;
+  core.k_pool = a.k_pool;
+  core.v_pool = a.v_pool;
+  core.trow = a.tables + (int64_t)b * a.W;
+  core.rs = (int64_t)a.Hkv * D;
+  core.hoff = h * D;
+  core.W = a.W;
+  core.NB = a.NB;
+  core.BS = a.BS;
+  core.bs_log2 = a.bs_log2;
+  core.tok_end = pc.tok_end;
+  core.limit = pc.tok_end;
+  core.scale_log2 = a.scale_log2;
+  if (a.k_new != nullptr) {
+    core.knew_row = a.k_new + (int64_t)b * a.new_stride + (int64_t)h * D;
+    core.vnew_row = a.v_new + (int64_t)b * a.new_stride + (int64_t)h * D;
+    core.new_pos = pc.L - 1;
+  } else {
+    core.knew_row = nullptr;
+    core.vnew_row = nullptr;
+    core.new_pos = -1;
+  }
+  core.stage = smem + w * C::STAGE;
+
+  {
+    const int hq = h * G + (n < G ? n : G - 1);
+    const f16* qrow = a.q + (int64_t)b * a.q_stride + (int64_t)hq * D;
+#pragma unroll
+    for (int s = 0; s < C::NK; ++s) {
+      const f16x8 v = ld16(qrow + (4 * s + g) * 8);
+      core.qv[s] = n < G ? v : f16x8{};
+    }
+  }
+  core.init_acc();
+  core.run(pc.tok_begin / kTile + w, kWaves, (pc.tok_end + kTile - 1) / kTile);
+
+  // ---- combine the four waves ----
+  const float l_tot = core.l_total();
+  float* mO = reinterpret_cast<float*>(smem + kWaves * C::STAGE);  // [4][G][D]
+  float* mM = mO + kWaves * G * D;                                 // [4][16]
+  float* mL = mM + kWaves * kMaxGroup;                             // [4][16]
+  if (n < G) {
+#pragma unroll
+    for (int x = 0; x < C::NX; ++x)
+      *reinterpret_cast<f32x4*>(mO + (w * G + n) * D + 16 * x + 4 * g) = core.o[x];
+    if (g == 0) {
+      mM[w * kMaxGroup + n] = core.m_run;
+      mL[w * kMaxGroup + n] = l_tot;
+    }
+  }
+  __syncthreads();
+  const int item = blockIdx.x;
+  for (int e = threadIdx.x; e < G * D; e += kThreads) {
+    const int hh = e / D;
+    const int d = e - hh * D;
+    float M = kNegInf;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, mM[ww * kMaxGroup + hh]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float mw = mM[ww * kMaxGroup + hh];
+      const float sc = mw == kNegInf ? 0.f : exp2f(mw - M);
+      num += sc * mO[(ww * G + hh) * D + d];
+      den += sc * mL[ww * kMaxGroup + hh];
+    }
+    const float res = num / den;
+    const int hq = h * G + hh;
+    if (pc.nsplit == 1) {
+      a.out[((int64_t)b * a.Hq + hq) * D + d] = (f16)res;
+    } else {
+      a.ws_o[((int64_t)item * a.Hq + hq) * D + d] = res;
+      if (d == 0) a.ws_lse[(int64_t)item * a.Hq + hq] = M + log2f(den);
+    }
+  }
+}
+
+// Combines the pieces of every split sequence; writes zeros for inactive rows.
+template <int D>
+__global__ __launch_bounds__(kThreads) void decode_merge_kernel(const DecodeArgs a) {
+  const int b = blockIdx.x;
+  const int h = blockIdx.y;
+  const int G = a.G;
+  const int L = clamp_len(a.ctx[b]);
+  if (L == 0) {
+    for (int e = threadIdx.x; e < G * D; e += kThreads)
+      a.out[((int64_t)b * a.Hq + h * G) * D + e] = (f16)0.f;
+    return;
+  }
+  const int chunk = split_chunk_quads(a.ctx, a.B, a.target);
+  int ns, first;
+  seq_pieces(a.ctx, a.B, chunk, b, ns, first);
+  if (ns <= 1) return;
+  for (int e = threadIdx.x; e < G * D; e += kThreads) {
+    const int hh = e / D;
+    const int d = e - hh * D;
+    const int hq = h * G + hh;
+    float M = kNegInf;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, a.ws_lse[(int64_t)(first + s) * a.Hq + hq]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < ns; ++s) {
+      const float sc = exp2f(a.ws_lse[(int64_t)(first + s) * a.Hq + hq] - M);
+      num += sc * a.ws_o[((int64_t)(first + s) * a.Hq + hq) * D + d];
+      den += sc;
+    }
+    a.out[((int64_t)b * a.Hq + hq) * D + d] = (f16)(num / den);
+  }
+}
+
+// General LSE merge of S partial results (natural-log LSE at the boundary).
+__global__ __launch_bounds__(kThreads) void lse_merge_kernel(const float* __restrict__ po,
+                                                             const float* __restrict__ plse,
+                                                             int S, int R, int D, f16* out,
+                                                             float* out_lse) {
+  const int r = blockIdx.x;
+  float M = kNegInf;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, plse[(int64_t)s * R + r] * kLog2e);
+  if (M == kNegInf) {
+    for (int d = threadIdx.x; d < D; d += blockDim.x) out[(int64_t)r * D + d] = (f16)0.f;
+    if (out_lse && threadIdx.x == 0) out_lse[r] = kNegInf;
+    return;
+  }
+  float den = 0.f;
+  for (int s = 0; s < S; ++s) den += exp2f(plse[(int64_t)s * R + r] * kLog2e - M);
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float num = 0.f;
+    for (int s = 0; s < S; ++s)
+      num += exp2f(plse[(int64_t)s * R + r] * kLog2e - M) * po[((int64_t)s * R + r) * D + d];
+    out[(int64_t)r * D + d] = (f16)(num / den);
+  }
+  if (out_lse && threadIdx.x == 0) out_lse[r] = (M + log2f(den)) / kLog2e;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline int log2_exact(int x) {
+  if (x <= 0 || (x & (x - 1))) return -1;
+  int l = 0;
+  while ((1 << l) < x) ++l;
+  return l;
+}
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+inline size_t ws_o_bytes(int batch, int hq, int d, int target) {
+  return align256((size_t)(target + batch) * hq * d * sizeof(float));
+}
+inline size_t ws_lse_bytes(int batch, int hq, int target) {
+  return align256((size_t)(target + batch) * hq * sizeof(float));
+}
+
+template <int D>
+size_t decode_lds_bytes(int G) {
+  return (size_t)kWaves * TileCfg<D>::STAGE + (size_t)kWaves * G * D * sizeof(float) +
+         2 * kWaves * kMaxGroup * sizeof(float);
+}
+
+template <int D>
+int launch_decode(const DecodeArgs& a, hipStream_t stream) {
+  const dim3 grid(a.target + a.B, a.Hkv);
+  hipLaunchKernelGGL(paged_decode_kernel<D>, grid, dim3(kThreads), decode_lds_bytes<D>(a.G),
+                     stream, a);
+  int st = FE_LAUNCH_STATUS();
+  if (st != 0) return st;
+  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.B, a.Hkv), dim3(kThreads), 0, stream, a);
+  return FE_LAUNCH_STATUS();
+}
+
+}  // namespace
+
+extern "C" size_t fe_paged_decode_workspace_size(int batch, int num_q_heads, int head_dim,
+                                                 int target_splits) {
+  if (batch < 0 || num_q_heads <= 0 || head_dim <= 0) return 0;
+  const int target = target_splits > 0 ? target_splits : kDefaultTarget;
+  return ws_o_bytes(batch, num_q_heads, head_dim, target) +
+         ws_lse_bytes(batch, num_q_heads, target);
+}
+
+extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
+                               const void* k_new, const void* v_new, int64_t new_batch_stride,
+                               void* k_pool, void* v_pool, int num_blocks,
+                               const int32_t* block_tables, int table_stride,
+                               const int32_t* context_lens, void* workspace,
+                               size_t workspace_bytes, int batch, int num_q_heads, int kv_heads,
+                               int head_dim, int block_size, float scale, int target_splits,
+                               fe_stream_t stream) {
+  FE_CHECK_ARG(batch >= 0 && num_q_heads > 0 && kv_heads > 0 && num_blocks > 0 &&
+               table_stride > 0 && target_splits >= 0);
+  if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
+  FE_CHECK_ARG(num_q_heads % kv_heads == 0);
+  const int G = num_q_heads / kv_heads;
+  if (G > kMaxGroup) return FE_ERR_UNSUPPORTED;
+  const int bs_log2 = log2_exact(block_size);
+  if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
+  if (batch == 0) return FE_OK;
+  FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && context_lens);
+  FE_CHECK_ARG((k_new == nullptr) == (v_new == nullptr));
+  FE_CHECK_ARG(q_batch_stride % 8 == 0 && q_batch_stride >= (int64_t)num_q_heads * head_dim);
+  FE_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(k_pool) && aligned16(v_pool));
+  if (k_new) {
+    FE_CHECK_ARG(aligned16(k_new) && aligned16(v_new) && new_batch_stride % 8 == 0 &&
+                 new_batch_stride >= (int64_t)kv_heads * head_dim);
+  }
+  const int target = target_splits > 0 ? target_splits : kDefaultTarget;
+  const size_t need = fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, target);
+  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+    return FE_ERR_WORKSPACE;
+
+  DecodeArgs a;
+  a.q = (const f16*)q;
+  a.out = (f16*)out;
+  a.k_new = (const f16*)k_new;
+  a.v_new = (const f16*)v_new;
+  a.k_pool = (f16*)k_pool;
+  a.v_pool = (f16*)v_pool;
+  a.tables = block_tables;
+  a.ctx = context_lens;
+  a.ws_o = (float*)workspace;
+  a.ws_lse = (float*)((char*)workspace + ws_o_bytes(batch, num_q_heads, head_dim, target));
+  a.q_stride = q_batch_stride;
+  a.new_stride = new_batch_stride;
+  a.W = table_stride;
+  a.B = batch;
+  a.Hq = num_q_heads;
+  a.Hkv = kv_heads;
+  a.G = G;
+  a.BS = block_size;
+  a.bs_log2 = bs_log2;
+  a.NB = num_blocks;
+  a.target = target;
+  a.scale_log2 = scale * kLog2e;
+  if (head_dim == 64) return launch_decode<64>(a, (hipStream_t)stream);
+  return launch_decode<128>(a, (hipStream_t)stream);
+}
+
+extern "C" int fe_lse_merge(const float* part_out, const float* part_lse, int num_splits,
+                            int rows, int head_dim, void* out, float* out_lse,
+                            fe_stream_t stream) {
+  FE_CHECK_ARG(num_splits > 0 && rows >= 0 && head_dim > 0);
+  if (rows == 0) return FE_OK;
+  FE_CHECK_ARG(part_out && part_lse && out);
+  const int threads = head_dim >= 256 ? 256 : (head_dim >= 128 ? 128 : 64);
+  hipLaunchKernelGGL(lse_merge_kernel, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
+                     part_out, part_lse, num_splits, rows, head_dim, (f16*)out, out_lse);
+  return FE_LAUNCH_STATUS();
+}

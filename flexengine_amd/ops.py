@@ -1,0 +1,247 @@
+"""Tensor-level wrappers around the C ABI (device memory and streams from PyTorch).
+
+Every function validates shapes, dtypes and devices on the host, then makes one
+asynchronous call into libfe_paged.so on the current HIP stream.  None of them
+synchronises the host or allocates inside the library, so all of them may be
+captured into a HIP graph (torch.cuda.graph) as long as the caller provides
+the workspace / output buffers or lets them come from the graph pool.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from flexengine_amd import _lib
+
+FP16 = torch.float16
+
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            "flexengine_amd kernels run on a ROCm GPU only; got tensors on " + str(dev)
+        )
+    for t in tensors[1:]:
+        if t is not None and t.device != dev:
+            raise ValueError(f"all tensors must be on {dev}; got {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _check_pool(k_pool: torch.Tensor, v_pool: torch.Tensor) -> tuple[int, int, int, int]:
+    if k_pool.shape != v_pool.shape or k_pool.ndim != 4:
+        raise ValueError("K/V pools must both be [num_blocks, block_size, kv_heads, head_dim]")
+    if k_pool.dtype != FP16 or v_pool.dtype != FP16:
+        raise ValueError("K/V pools must be float16")
+    if not (k_pool.is_contiguous() and v_pool.is_contiguous()):
+        raise ValueError("K/V pools must be contiguous")
+    nb, bs, hkv, d = k_pool.shape
+    return nb, bs, hkv, d
+
+
+def _int32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.int32:
+        raise ValueError(f"{name} must be int32 (convert once with .to(torch.int32))")
+    return t.contiguous()
+
+
+# ---------------------------------------------------------------------------------------
+# KV page write / gather
+# ---------------------------------------------------------------------------------------
+
+def write_kv(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+             slot_block: torch.Tensor, slot_offset: torch.Tensor) -> None:
+    """k_pool[slot_block[t], slot_offset[t]] = k_new[t] (and v); negative blocks are skipped."""
+    dev = _require_gpu(k_new, v_new, k_pool, v_pool, slot_block, slot_offset)
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
+    if k_new.shape != v_new.shape or k_new.ndim != 3 or tuple(k_new.shape[1:]) != (hkv, d):
+        raise ValueError("K/V shapes must be [tokens, kv_heads, head_dim]")
+    if k_new.dtype != FP16 or v_new.dtype != FP16:
+        raise ValueError("wrong KV dtype")
+    if k_new.stride() != v_new.stride() or k_new.stride(2) != 1 or k_new.stride(1) != d:
+        raise ValueError("new K/V rows must have contiguous heads and equal strides")
+    t = k_new.shape[0]
+    slot_block, slot_offset = _int32(slot_block, "slot_block"), _int32(slot_offset, "slot_offset")
+    if slot_block.shape != (t,) or slot_offset.shape != (t,):
+        raise ValueError("slot arrays must be [tokens]")
+    _lib.call("fe_write_kv", k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0),
+              k_pool.data_ptr(), v_pool.data_ptr(), nb, slot_block.data_ptr(),
+              slot_offset.data_ptr(), t, hkv, d, bs, _stream(dev))
+
+
+def write_kv_decode(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor,
+                    v_pool: torch.Tensor, block_tables: torch.Tensor,
+                    context_lens: torch.Tensor) -> None:
+    """Writes row b at position context_lens[b]-1 of sequence b; rows with length 0 are skipped."""
+    dev = _require_gpu(k_new, v_new, k_pool, v_pool, block_tables, context_lens)
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
+    batch = k_new.shape[0]
+    if k_new.shape != v_new.shape or tuple(k_new.shape[1:]) != (hkv, d):
+        raise ValueError("K/V shapes must be [batch, kv_heads, head_dim]")
+    if k_new.stride() != v_new.stride() or k_new.stride(2) != 1 or k_new.stride(1) != d:
+        raise ValueError("new K/V rows must have contiguous heads and equal strides")
+    block_tables = _int32(block_tables, "block_tables")
+    context_lens = _int32(context_lens, "context_lens")
+    if block_tables.ndim != 2 or block_tables.shape[0] != batch or context_lens.shape != (batch,):
+        raise ValueError("block_tables must be [batch, W] and context_lens [batch]")
+    _lib.call("fe_write_kv_decode", k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0),
+              k_pool.data_ptr(), v_pool.data_ptr(), nb, block_tables.data_ptr(),
+              block_tables.shape[1], context_lens.data_ptr(), batch, hkv, d, bs, _stream(dev))
+
+
+def gather_kv(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Tensor,
+              context_lens: torch.Tensor, out_offsets: torch.Tensor,
+              total_tokens: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Materialises every sequence's K/V rows: returns [total_tokens, kv_heads, head_dim] pair."""
+    dev = _require_gpu(k_pool, v_pool, block_tables, context_lens, out_offsets)
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
+    block_tables = _int32(block_tables, "block_tables")
+    context_lens = _int32(context_lens, "context_lens")
+    out_offsets = _int32(out_offsets, "out_offsets")
+    batch = context_lens.shape[0]
+    if block_tables.ndim != 2 or block_tables.shape[0] != batch or out_offsets.shape != (batch + 1,):
+        raise ValueError("block_tables [batch, W], context_lens [batch], out_offsets [batch+1]")
+    k_out = torch.empty((total_tokens, hkv, d), dtype=FP16, device=dev)
+    v_out = torch.empty_like(k_out)
+    _lib.call("fe_gather_kv", k_pool.data_ptr(), v_pool.data_ptr(), nb, block_tables.data_ptr(),
+              block_tables.shape[1], context_lens.data_ptr(), out_offsets.data_ptr(),
+              k_out.data_ptr(), v_out.data_ptr(), batch, total_tokens, hkv, d, bs, _stream(dev))
+    return k_out, v_out
+
+
+# ---------------------------------------------------------------------------------------
+# decode
+# ---------------------------------------------------------------------------------------
+
+_WORKSPACES: dict[tuple, torch.Tensor] = {}
+
+
+def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, target_splits: int = 0) -> int:
+    return int(_lib.load().fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, target_splits))
+
+
+def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A per-device scratch buffer reused by every decode call on that device.
+
+    Calls on one stream are ordered, so sharing is safe there; callers running
+    decode on several streams at once must pass their own workspace.
+    """
+    key = (device.type, device.index)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                 block_tables: torch.Tensor, context_lens: torch.Tensor, *,
+                 scale: float | None = None, k_new: torch.Tensor | None = None,
+                 v_new: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                 workspace: torch.Tensor | None = None, target_splits: int = 0) -> torch.Tensor:
+    """Single-token paged decode attention over one layer's pools.
+
+    q [B, Hq, D] fp16 (rows may be strided, heads contiguous); pools
+    [NB, BS, Hkv, D]; block_tables int32 [B, W]; context_lens int32 [B]
+    (0 = inactive row -> zeros).  With k_new/v_new ([B, Hkv, D]) the new token's
+    K/V are written to the pool at position context_lens-1 in the same launch.
+    """
+    dev = _require_gpu(q, k_pool, v_pool, block_tables, context_lens, k_new, v_new, out)
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
+    if q.ndim != 3 or q.shape[2] != d or q.dtype != FP16:
+        raise ValueError("q must be float16 [batch, num_q_heads, head_dim]")
+    batch, hq, _ = q.shape
+    if q.stride(2) != 1 or q.stride(1) != d:
+        raise ValueError("q heads must be contiguous")
+    if hq % hkv:
+        raise ValueError("Q heads must be a multiple of KV heads")
+    block_tables = _int32(block_tables, "block_tables")
+    context_lens = _int32(context_lens, "context_lens")
+    if block_tables.ndim != 2 or block_tables.shape[0] != batch or context_lens.shape != (batch,):
+        raise ValueError("block_tables must be [batch, W] and context_lens [batch]")
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new must be given together")
+    new_stride = 0
+    if k_new is not None:
+        if k_new.shape != (batch, hkv, d) or v_new.shape != k_new.shape:
+            raise ValueError("k_new/v_new must be [batch, kv_heads, head_dim]")
+        if k_new.dtype != FP16 or v_new.dtype != FP16:
+            raise ValueError("k_new/v_new must be float16")
+        if k_new.stride() != v_new.stride() or k_new.stride(2) != 1 or k_new.stride(1) != d:
+            raise ValueError("k_new/v_new heads must be contiguous with equal strides")
+        new_stride = k_new.stride(0)
+    if out is None:
+        out = torch.empty((batch, hq, d), dtype=FP16, device=dev)
+    elif out.shape != (batch, hq, d) or out.dtype != FP16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float16 [batch, num_q_heads, head_dim]")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    need = decode_workspace_bytes(batch, hq, d, target_splits)
+    if workspace is None:
+        workspace = decode_workspace(dev, need)
+    _lib.call("fe_paged_decode", q.data_ptr(), q.stride(0), out.data_ptr(), _ptr(k_new),
+              _ptr(v_new), new_stride, k_pool.data_ptr(), v_pool.data_ptr(), nb,
+              block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(),
+              workspace.data_ptr(), workspace.numel() * workspace.element_size(), batch, hq, hkv,
+              d, bs, float(scale), int(target_splits), _stream(dev))
+    return out
+
+
+def lse_merge(part_out: torch.Tensor, part_lse: torch.Tensor,
+              with_lse: bool = False) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+    """Merges S split results: part_out fp32 [S, R, D], part_lse fp32 [S, R] (natural log)."""
+    dev = _require_gpu(part_out, part_lse)
+    if part_out.ndim != 3 or part_lse.shape != part_out.shape[:2]:
+        raise ValueError("part_out must be [S, R, D] and part_lse [S, R]")
+    if part_out.dtype != torch.float32 or part_lse.dtype != torch.float32:
+        raise ValueError("partials must be float32")
+    part_out, part_lse = part_out.contiguous(), part_lse.contiguous()
+    s, r, d = part_out.shape
+    out = torch.empty((r, d), dtype=FP16, device=dev)
+    out_lse = torch.empty((r,), dtype=torch.float32, device=dev) if with_lse else None
+    _lib.call("fe_lse_merge", part_out.data_ptr(), part_lse.data_ptr(), s, r, d, out.data_ptr(),
+              _ptr(out_lse), _stream(dev))
+    return (out, out_lse) if with_lse else out
+
+
+# ---------------------------------------------------------------------------------------
+# prefill
+# ---------------------------------------------------------------------------------------
+
+def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                  block_tables: torch.Tensor, q_offsets: torch.Tensor,
+                  context_lens: torch.Tensor, max_q_len: int, *, scale: float | None = None,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """Ragged causal prefill: q [total_q, Hq, D]; sequence s owns rows
+    q_offsets[s]:q_offsets[s+1] at positions context_lens[s]-n_s .. context_lens[s]-1."""
+    dev = _require_gpu(q, k_pool, v_pool, block_tables, q_offsets, context_lens, out)
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
+    if q.ndim != 3 or q.shape[2] != d or q.dtype != FP16 or not q.is_contiguous():
+        raise ValueError("q must be a contiguous float16 [total_q, num_q_heads, head_dim]")
+    total_q, hq, _ = q.shape
+    if hq % hkv:
+        raise ValueError("Q heads must be a multiple of KV heads")
+    block_tables = _int32(block_tables, "block_tables")
+    q_offsets = _int32(q_offsets, "q_offsets")
+    context_lens = _int32(context_lens, "context_lens")
+    num_seqs = context_lens.shape[0]
+    if q_offsets.shape != (num_seqs + 1,) or block_tables.ndim != 2 or block_tables.shape[0] != num_seqs:
+        raise ValueError("q_offsets [S+1], block_tables [S, W], context_lens [S]")
+    if out is None:
+        out = torch.empty_like(q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    _lib.call("fe_prefill_paged", q.data_ptr(), out.data_ptr(), k_pool.data_ptr(),
+              v_pool.data_ptr(), nb, block_tables.data_ptr(), block_tables.shape[1],
+              q_offsets.data_ptr(), context_lens.data_ptr(), num_seqs, total_q, int(max_q_len),
+              hq, hkv, d, bs, float(scale), _stream(dev))
+    return out

@@ -1,0 +1,178 @@
+/*
+ * flexengine_amd.h -- C ABI of the MI355X (gfx950) paged-attention library
+ * (libfe_paged.so).
+ *
+ * This is the drop-in boundary for FlexEngine's paged-attention hot path.
+ * Every entry point takes plain device pointers, element counts and a HIP
+ * stream; no PyTorch type crosses the boundary.  All buffers are owned by the
+ * caller.  Every entry point is asynchronous on `stream`, performs no host
+ * synchronisation and no device allocation, so it may be recorded into a HIP
+ * graph.  Return value: 0 on success, a negative FE_ERR_* code for an argument
+ * the library rejects before launching anything, or a positive hipError_t
+ * returned by the launch.
+ *
+ * Tensor layouts (fp16 = IEEE binary16, row-major, contiguous unless a stride
+ * argument says otherwise):
+ *   KV pool of one layer   k_pool, v_pool : [num_blocks, block_size, kv_heads, head_dim]
+ *       (the layout of PagedKVCache.k[layer] in
+ *        src/flexengine/engine/kv_cache/allocator.py:30-32)
+ *   block tables           int32 [batch, table_stride]; row b lists the
+ *       physical blocks of sequence b in logical order.
+ *   context lengths        int32 [batch]; tokens of sequence b that attention
+ *       covers, INCLUDING the token being decoded.  0 marks an inactive row,
+ *       whose output is exact zeros (paged_attention.py:131,138).
+ *
+ * Supported shapes: head_dim in {64, 128}; num_q_heads a multiple of
+ * kv_heads with a group size of at most 16; block_size a power of two.
+ */
+#ifndef FLEXENGINE_AMD_H
+#define FLEXENGINE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers. */
+typedef struct ihipStream_t* fe_stream_t;
+
+#define FE_OK 0
+#define FE_ERR_INVALID_ARGUMENT (-1)  /* null pointer, bad size, misalignment */
+#define FE_ERR_UNSUPPORTED (-2)       /* head_dim / group size / block size not built */
+#define FE_ERR_WORKSPACE (-3)         /* workspace missing or smaller than required */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int fe_version(void);
+
+/* Human-readable text for any return code of this library. */
+const char* fe_error_string(int code);
+
+/*
+ * KV page write ("reshape and cache"): for every new token t,
+ *   k_pool[slot_block[t], slot_offset[t], h, :] = k_new[t, h, :]   (and v)
+ * Rows whose slot_block is negative are skipped (inactive / padded rows).
+ * Bit-exact byte copy.  k_new/v_new rows are `new_token_stride` elements
+ * apart (>= kv_heads*head_dim), heads within a row are contiguous.
+ * Replaces PagedKVCache._locators + PagedKVCache.write
+ * (src/flexengine/engine/kv_cache/allocator.py:107-127): the caller passes the
+ * (block, offset) pairs that _locators builds on the host.
+ */
+int fe_write_kv(const void* k_new, const void* v_new, int64_t new_token_stride,
+                void* k_pool, void* v_pool, int num_blocks,
+                const int32_t* slot_block, const int32_t* slot_offset,
+                int num_tokens, int kv_heads, int head_dim, int block_size,
+                fe_stream_t stream);
+
+/*
+ * Decode-step KV page write with device-side slot mapping: for each row b
+ * with context_lens[b] = L > 0, writes k_new[b] / v_new[b] ([kv_heads,
+ * head_dim], rows new_batch_stride elements apart) at logical position L-1,
+ * i.e. block block_tables[b, (L-1)/bs], offset (L-1)%bs.  Rows with L == 0 are left untouched.
+ * Replaces the graph-path write in decode_static
+ * (src/flexengine/inference/models/qwen2.py:156-161), with inactive rows
+ * skipped instead of rewritten.
+ */
+int fe_write_kv_decode(const void* k_new, const void* v_new, int64_t new_batch_stride,
+                       void* k_pool, void* v_pool, int num_blocks,
+                       const int32_t* block_tables, int table_stride,
+                       const int32_t* context_lens, int batch,
+                       int kv_heads, int head_dim, int block_size,
+                       fe_stream_t stream);
+
+/*
+ * Block-table gather ("materialize"): for every sequence b and position
+ * t < context_lens[b],
+ *   k_out[out_offsets[b] + t] = k_pool[block_tables[b, t/bs], t%bs]   (and v)
+ * k_out/v_out are [total_tokens, kv_heads, head_dim]; out_offsets has batch+1
+ * entries (exclusive prefix sum of context_lens; out_offsets[batch] =
+ * total_tokens).  Bit-exact byte copy.
+ * Replaces PagedKVCache.materialize (allocator.py:129-134), batched.
+ */
+int fe_gather_kv(const void* k_pool, const void* v_pool, int num_blocks,
+                 const int32_t* block_tables, int table_stride,
+                 const int32_t* context_lens, const int32_t* out_offsets,
+                 void* k_out, void* v_out, int batch, int total_tokens,
+                 int kv_heads, int head_dim, int block_size, fe_stream_t stream);
+
+/*
+ * Bytes of caller-owned workspace that fe_paged_decode needs for a given
+ * batch / head configuration and split target (0 = library default).
+ * The workspace may be reused by consecutive calls on one stream.
+ */
+size_t fe_paged_decode_workspace_size(int batch, int num_q_heads, int head_dim,
+                                      int target_splits);
+
+/*
+ * Fused single-token paged decode attention over one layer:
+ *   out[b, hq, :] = softmax_t(scale * q[b,hq,:] . K[b,t,hq/G,:]) V[b,t,hq/G,:]
+ * for t < context_lens[b], K/V rows fetched through block_tables; G =
+ * num_q_heads / kv_heads.  Rows with context_lens[b] == 0 get exact zeros.
+ * Work is split over the keys ("split-K") into about `target_splits` equal
+ * pieces per KV head (0 = library default); partial results are combined by a
+ * log-sum-exp merge launched on the same stream.
+ * If k_new and v_new are non-null ([batch, kv_heads, head_dim], rows
+ * new_batch_stride elements apart) the kernel
+ * also performs the decode-step page write of fe_write_kv_decode and uses
+ * those rows for position L-1, so one call is "write KV, then attend".
+ * q and out are [batch, num_q_heads, head_dim]; q rows are q_batch_stride
+ * elements apart.
+ * Replaces triton_paged_decode_batch / _paged_decode_batch_kernel
+ * (src/flexengine/inference/kernels/paged_attention.py:99-155) and the batched
+ * backend signature shared with flashinfer_paged_decode_batch
+ * (src/flexengine/inference/attention/flashinfer_backend.py:33-72); the
+ * reference's positions/active_mask pair maps to context_lens =
+ * (positions + 1) * active.
+ */
+int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
+                    const void* k_new, const void* v_new, int64_t new_batch_stride,
+                    void* k_pool, void* v_pool, int num_blocks,
+                    const int32_t* block_tables, int table_stride,
+                    const int32_t* context_lens,
+                    void* workspace, size_t workspace_bytes,
+                    int batch, int num_q_heads, int kv_heads, int head_dim,
+                    int block_size, float scale, int target_splits,
+                    fe_stream_t stream);
+
+/*
+ * Log-sum-exp merge of split attention results:
+ *   LSE[r]   = log(sum_s exp(part_lse[s, r]))
+ *   out[r,:] = sum_s exp(part_lse[s, r] - LSE[r]) * part_out[s, r, :]
+ * part_out fp32 [num_splits, rows, head_dim] (each normalised by its own
+ * softmax denominator), part_lse fp32 [num_splits, rows] (natural log),
+ * out fp16 [rows, head_dim]; out_lse (fp32 [rows], nullable) receives LSE.
+ * A split whose lse is -inf contributes nothing; a row whose every split is
+ * -inf gets zeros.  This is the combine step of split-K decode; the
+ * reference has no split-K, its single-pass online softmax
+ * (src/flexengine/inference/attention/paged.py:50-70) is the quantity the
+ * merge reproduces.
+ */
+int fe_lse_merge(const float* part_out, const float* part_lse, int num_splits,
+                 int rows, int head_dim, void* out, float* out_lse,
+                 fe_stream_t stream);
+
+/*
+ * Ragged chunked-prefill attention over paged KV (causal), fp16 MFMA:
+ * sequence s owns query rows [q_offsets[s], q_offsets[s+1]) of q/out
+ * ([total_q, num_q_heads, head_dim]); its context length is
+ * context_lens[s] (cached tokens + its new tokens, whose K/V must already be
+ * in the pool).  Query row j of sequence s sits at absolute position
+ * context_lens[s] - n_s + j and attends to keys t <= that position.
+ * Replaces the per-request materialized route that the reference takes for
+ * every multi-token chunk (src/flexengine/inference/attention/paged.py:27-40,
+ * called per request from qwen2.py:117-126).
+ */
+int fe_prefill_paged(const void* q, void* out,
+                     const void* k_pool, const void* v_pool, int num_blocks,
+                     const int32_t* block_tables, int table_stride,
+                     const int32_t* q_offsets, const int32_t* context_lens,
+                     int num_seqs, int total_q, int max_q_len,
+                     int num_q_heads, int kv_heads, int head_dim,
+                     int block_size, float scale, fe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLEXENGINE_AMD_H */

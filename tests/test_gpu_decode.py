@@ -1,0 +1,249 @@
+"""GPU: fused paged decode (fe_paged_decode + split-K LSE merge) against the oracle.
+
+Tolerance (hot-path contract): max |err| <= 2e-3 and mean |err| <= 2e-4 of the
+fp16 output against the float64 oracle.  Page writes fused into the decode call
+must be bit-exact.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flexengine_amd import attention, ops, workloads
+from flexengine_amd.kv_cache import CacheLayout, PagedKVCache
+from oracle import paged_ref as R
+from tests.parity import assert_attention_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def run_decode(w: workloads.DecodeWorkload, target_splits: int = 0, fuse: bool = True):
+    d = w.to(DEV)
+    kn = d.k_new if fuse else None
+    vn = d.v_new if fuse else None
+    out = ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens,
+                           k_new=kn, v_new=vn, target_splits=target_splits)
+    torch.cuda.synchronize()
+    return out.cpu(), d
+
+
+def oracle_decode(w: workloads.DecodeWorkload):
+    kp, vp = w.k_pool.numpy().copy(), w.v_pool.numpy().copy()
+    if w.k_new is not None:
+        R.write_kv_decode(kp, vp, w.block_tables.numpy(), w.context_lens.numpy(),
+                          w.k_new.numpy(), w.v_new.numpy(), w.block_size)
+    out = R.decode_reference(w.q.numpy(), kp, vp, w.block_tables.numpy(),
+                             w.context_lens.numpy(), w.block_size)
+    return out, kp, vp
+
+
+# --------------------------------------------------------------------------------------
+# the reference's own GPU test cases, through the per-request interface
+# --------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("length", [1, 17, 129, 513])
+def test_reference_case_noncontiguous_pages(length):
+    """test_triton_paged_attention.py:10-26: CacheLayout(1, 80, 16, 2, 64), 8 q-heads,
+    reversed page table, fp16; here held to the tighter contract tolerance."""
+    g = torch.Generator().manual_seed(7 + length)
+    cache = PagedKVCache(CacheLayout(1, 80, 16, 2, 64), device=DEV)
+    cache.reserve("r", length)
+    cache.tables["r"] = list(reversed(cache.tables["r"]))
+    keys = torch.randn(length, 2, 64, generator=g).half()
+    values = torch.randn(length, 2, 64, generator=g).half()
+    cache.write(0, "r", 0, keys.to(DEV), values.to(DEV))
+    query = torch.randn(1, 8, 64, generator=g).half()
+    position = torch.tensor([length - 1], device=DEV)
+    got = attention.attention_for_request(query.to(DEV), cache, 0, "r", length, position)
+    exp = R.attention_materialized(query.numpy(), keys.numpy(), values.numpy(), [length - 1])
+    assert got.dtype == torch.float16 and got.shape == (1, 8, 64)
+    assert_attention_close(got.cpu().numpy(), exp, what=f"length {length}")
+
+
+def test_reference_case_group_size_seven():
+    """test_flashinfer_attention.py:36-49: Qwen2.5-0.5B heads (14 q / 2 kv / D 64), length 17."""
+    g = torch.Generator().manual_seed(36)
+    length = 17
+    cache = PagedKVCache(CacheLayout(1, 8, 16, 2, 64), device=DEV)
+    cache.reserve("r", length)
+    keys = torch.randn(length, 2, 64, generator=g).half()
+    cache.write(0, "r", 0, keys.to(DEV), keys.to(DEV))
+    query = torch.randn(1, 14, 64, generator=g).half()
+    pos = torch.tensor([length - 1], device=DEV)
+    got = attention.attention_for_request(query.to(DEV), cache, 0, "r", length, pos)
+    exp = R.attention_materialized(query.numpy(), keys.numpy(), keys.numpy(), [length - 1])
+    assert_attention_close(got.cpu().numpy(), exp)
+
+
+# --------------------------------------------------------------------------------------
+# benchmark configurations at full size
+# --------------------------------------------------------------------------------------
+
+def test_c1_full():
+    w = workloads.c1_workload()
+    got, _ = run_decode(w)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what="C1")
+
+
+def test_c2_full_with_fused_page_write():
+    w = workloads.c2_workload()
+    got, d = run_decode(w)
+    exp, kp, vp = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what="C2")
+    # fused page write: pools byte-identical to the oracle's write
+    assert d.k_pool.cpu().numpy().tobytes() == kp.tobytes()
+    assert d.v_pool.cpu().numpy().tobytes() == vp.tobytes()
+
+
+def test_c2_split_count_invariance():
+    """One piece per sequence vs. the finest split give the same result (to tolerance)."""
+    w = workloads.c2_workload()
+    exp, _, _ = oracle_decode(w)
+    outs = []
+    for target in (1, 64, 4096):
+        got, _ = run_decode(w, target_splits=target)
+        assert_attention_close(got.numpy(), exp, what=f"target_splits={target}")
+        outs.append(got.float().numpy())
+    assert np.abs(outs[0] - outs[2]).max() <= 2e-3
+
+
+def test_c3_shared_prefix_split_k():
+    w = workloads.c3_workload(groups=2, per_group=8)
+    got, _ = run_decode(w)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what="C3 (2x8)")
+
+
+# --------------------------------------------------------------------------------------
+# shapes and edge cases
+# --------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("hq,hkv,d", [(12, 2, 128), (14, 2, 64), (16, 1, 128), (8, 8, 64),
+                                      (16, 2, 128), (5, 5, 128), (28, 4, 128)])
+def test_head_configurations(hq, hkv, d):
+    lengths = [1, 2, 15, 16, 17, 63, 64, 65, 200, 1000]
+    w = workloads.make_decode_workload("shape", hq * 31 + d, len(lengths), hq, hkv, d, lengths)
+    got, _ = run_decode(w)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what=f"{hq}/{hkv}/{d}")
+
+
+@pytest.mark.parametrize("bs", [1, 2, 4, 8, 32, 64])
+def test_block_sizes(bs):
+    lengths = [1, 3, 33, 100, 257, 700]
+    w = workloads.make_decode_workload("bs", 500 + bs, len(lengths), 12, 2, 128, lengths,
+                                       block_size=bs, with_new_kv=True)
+    got, d = run_decode(w)
+    exp, kp, vp = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what=f"block_size {bs}")
+    assert d.k_pool.cpu().numpy().tobytes() == kp.tobytes()
+
+
+def test_inactive_rows_give_exact_zeros():
+    lengths = [40, 0, 300, 0, 1]
+    w = workloads.make_decode_workload("inactive", 77, 5, 12, 2, 128, [max(n, 1) for n in lengths])
+    w.context_lens = torch.tensor(lengths, dtype=torch.int32)
+    d = w.to(DEV)
+    out = torch.full_like(d.q, 7.0)
+    ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens, out=out)
+    got = out.cpu()
+    assert torch.count_nonzero(got[1]) == 0 and torch.count_nonzero(got[3]) == 0
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp)
+
+
+def test_batched_backend_signature_positions_and_active_mask():
+    """The reference's batched contract: (q, cache, layer, tables(int64), positions, active)."""
+    g = torch.Generator().manual_seed(99)
+    cache = PagedKVCache(CacheLayout(2, 64, 16, 2, 128), device=DEV)
+    rows = ["a", "b", "c"]
+    lens = [50, 130, 7]
+    for r, n in zip(rows, lens):
+        cache.reserve(r, n)
+        kv = torch.randn(n, 2, 128, generator=g).half().to(DEV)
+        cache.write(1, r, 0, kv, kv * 0.5)
+    tables = cache.block_table(rows).to(torch.long)
+    positions = torch.tensor([n - 1 for n in lens], device=DEV)
+    active = torch.tensor([1.0, 0.0, 1.0], device=DEV)
+    q = torch.randn(3, 12, 128, generator=g).half().to(DEV)
+    got = attention.paged_decode_batch(q, cache, 1, tables, positions, active).cpu().numpy()
+    exp = R.paged_decode_batch(q.cpu().numpy(), cache.k[1].cpu().numpy(), cache.v[1].cpu().numpy(),
+                               tables.cpu().numpy(), positions.cpu().numpy(),
+                               active.cpu().numpy(), 16)
+    assert_attention_close(got, exp)
+    assert (got[1] == 0).all()
+
+
+def test_stale_nan_beyond_context_is_ignored():
+    """Pool slots past the context (same block) hold NaN; outputs must stay finite."""
+    lengths = [5, 21, 40]
+    w = workloads.make_decode_workload("nan", 5, 3, 12, 2, 128, lengths)
+    kp, vp = w.k_pool.clone(), w.v_pool.clone()
+    for b, n in enumerate(lengths):
+        for t in range(n, ((n + 15) // 16) * 16):
+            blk = int(w.block_tables[b, t // 16])
+            kp[blk, t % 16] = float("nan")
+            vp[blk, t % 16] = float("nan")
+    w.k_pool, w.v_pool = kp, vp
+    got, _ = run_decode(w)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp)
+
+
+def test_long_single_sequence_many_splits():
+    w = workloads.make_decode_workload("long", 8, 1, 12, 2, 128, [20000])
+    got, _ = run_decode(w)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what="L=20000")
+
+
+def test_strided_query_rows():
+    """q as a view into a fused QKV projection output (row stride > Hq*D)."""
+    lengths = [33, 90]
+    w = workloads.make_decode_workload("stride", 12, 2, 12, 2, 128, lengths)
+    d = w.to(DEV)
+    big = torch.zeros(2, 16 * 128, dtype=torch.float16, device=DEV)
+    big[:, : 12 * 128] = d.q.reshape(2, -1)
+    qv = big[:, : 12 * 128].view(2, 12, 128)
+    got = ops.paged_decode(qv, d.k_pool, d.v_pool, d.block_tables, d.context_lens).cpu()
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp)
+
+
+def test_out_of_range_table_entries_do_not_fault():
+    """Garbage block ids are clamped into the pool (no fault); valid rows are unaffected."""
+    lengths = [40, 40]
+    w = workloads.make_decode_workload("clamp", 21, 2, 12, 2, 128, lengths)
+    w.block_tables = w.block_tables.clone()
+    w.block_tables[1, :] = 10 ** 6
+    got, _ = run_decode(w)
+    exp, _, _ = oracle_decode(workloads.make_decode_workload("clamp", 21, 2, 12, 2, 128, lengths))
+    assert_attention_close(got[:1].numpy(), exp[:1])
+    assert torch.isfinite(got[1].float()).all()
+
+
+def test_lse_merge_entry_point():
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((6, 128))
+    k = rng.standard_normal((300, 128))
+    v = rng.standard_normal((300, 128))
+    po, pl = R.split_attention(q, k, v, [0, 50, 50, 170, 300])
+    out, lse = ops.lse_merge(torch.tensor(po, dtype=torch.float32, device=DEV),
+                             torch.tensor(pl, dtype=torch.float32, device=DEV), with_lse=True)
+    exp_o, exp_l = R.lse_merge(po, pl)
+    assert_attention_close(out.cpu().numpy(), exp_o)
+    np.testing.assert_allclose(lse.cpu().numpy(), exp_l, atol=1e-4)
+
+
+def test_error_codes_surface_as_exceptions():
+    q = torch.zeros(1, 12, 96, dtype=torch.float16, device=DEV)
+    pool = torch.zeros(4, 16, 2, 96, dtype=torch.float16, device=DEV)
+    t = torch.zeros(1, 1, dtype=torch.int32, device=DEV)
+    c = torch.ones(1, dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match="unsupported"):
+        ops.paged_decode(q, pool, pool, t, c)

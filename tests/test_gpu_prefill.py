@@ -1,0 +1,98 @@
+"""GPU: ragged chunked-prefill attention (fe_prefill_paged) against the oracle."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flexengine_amd import attention, ops, workloads
+from flexengine_amd.kv_cache import CacheLayout, PagedKVCache
+from oracle import paged_ref as R
+from tests.parity import assert_attention_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _case(seed, n_new, cached, hq=12, hkv=2, d=128, bs=16):
+    g = torch.Generator().manual_seed(seed)
+    ctx = [c + n for c, n in zip(cached, n_new)]
+    pages = [math.ceil(x / bs) for x in ctx]
+    nb = sum(pages) + 3
+    k_pool = torch.randn(nb, bs, hkv, d, generator=g).half()
+    v_pool = torch.randn(nb, bs, hkv, d, generator=g).half()
+    perm = torch.randperm(nb, generator=g)
+    width = max(pages)
+    tables = torch.zeros(len(ctx), width, dtype=torch.int32)
+    at = 0
+    for i, p in enumerate(pages):
+        tables[i, :p] = perm[at:at + p]
+        tables[i, p:] = perm[at + p - 1] if p else 0
+        at += p
+    offs = np.concatenate([[0], np.cumsum(n_new)]).astype(np.int32)
+    q = torch.randn(int(offs[-1]), hq, d, generator=g).half()
+    return q, torch.tensor(offs), torch.tensor(ctx, dtype=torch.int32), tables, k_pool, v_pool
+
+
+def _run(q, offs, ctx, tables, kp, vp):
+    n_new = (offs[1:] - offs[:-1]).tolist()
+    out = ops.prefill_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), tables.to(DEV), offs.to(DEV),
+                            ctx.to(DEV), max(n_new) if n_new else 0)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("n_new,cached", [([1], [0]), ([5], [0]), ([16], [0]), ([17], [3]),
+                                          ([64], [0]), ([65], [100]), ([130, 7, 1], [0, 40, 999]),
+                                          ([0, 33], [10, 10])])
+def test_ragged_prefill_small(n_new, cached):
+    q, offs, ctx, tables, kp, vp = _case(sum(n_new) + 7 * len(n_new), n_new, cached)
+    got = _run(q, offs, ctx, tables, kp, vp)
+    exp = R.prefill_reference(q.numpy(), offs.numpy(), ctx.numpy(), kp.numpy(), vp.numpy(),
+                              tables.numpy(), 16)
+    assert_attention_close(got, exp, what=f"n={n_new} c={cached}")
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", [(14, 2, 64, 16), (8, 8, 64, 4), (16, 2, 128, 32)])
+def test_prefill_shapes(hq, hkv, d, bs):
+    q, offs, ctx, tables, kp, vp = _case(hq + d + bs, [70, 3], [25, 200], hq, hkv, d, bs)
+    got = _run(q, offs, ctx, tables, kp, vp)
+    exp = R.prefill_reference(q.numpy(), offs.numpy(), ctx.numpy(), kp.numpy(), vp.numpy(),
+                              tables.numpy(), bs)
+    assert_attention_close(got, exp)
+
+
+def test_c4_prefill_chunks_full():
+    w = workloads.c4_workload()
+    got = _run(w.q, w.q_offsets, w.context_lens, w.block_tables, w.k_pool, w.v_pool)
+    exp = R.prefill_reference(w.q.numpy(), w.q_offsets.numpy(), w.context_lens.numpy(),
+                              w.k_pool.numpy(), w.v_pool.numpy(), w.block_tables.numpy(), 16)
+    assert_attention_close(got, exp, what="C4 prefill")
+
+
+def test_per_request_interface_multi_token_chunk():
+    """attention_for_request with Q > 1 takes the prefill kernel (the reference routes it to
+    the materialized SDPA, test_triton_paged_attention.py:29-41); compare with the oracle."""
+    g = torch.Generator().manual_seed(29)
+    cache = PagedKVCache(CacheLayout(1, 8, 4, 1, 64), device=DEV)
+    cache.reserve("r", 4)
+    keys = torch.randn(4, 1, 64, generator=g).half()
+    cache.write(0, "r", 0, keys.to(DEV), keys.to(DEV))
+    query = torch.randn(4, 2, 64, generator=g).half()
+    positions = torch.arange(4, device=DEV)
+    got = attention.attention_for_request(query.to(DEV), cache, 0, "r", 4, positions)
+    exp = R.attention_materialized(query.numpy(), keys.numpy(), keys.numpy(), np.arange(4))
+    assert_attention_close(got.cpu().numpy(), exp)
+
+
+def test_prefill_then_decode_consistency():
+    """The prefill row at position p equals a decode call with context p + 1."""
+    q, offs, ctx, tables, kp, vp = _case(5, [40], [60])
+    got = _run(q, offs, ctx, tables, kp, vp)
+    j = 23
+    pos = 60 + j
+    dec = ops.paged_decode(q[j:j + 1].to(DEV), kp.to(DEV), vp.to(DEV), tables.to(DEV),
+                           torch.tensor([pos + 1], dtype=torch.int32, device=DEV)).cpu().numpy()
+    assert np.abs(got[j] - dec[0].astype(np.float64)).max() <= 2e-3
