@@ -110,7 +110,8 @@ def main(argv=None) -> int:
     pools = [(d.k_pool, d.v_pool)] + [(d.k_pool.clone(), d.v_pool.clone())
                                       for _ in range(max(1, args.pools) - 1)]
     out = torch.empty_like(d.q)
-    ws = ops.decode_workspace(dev, ops.decode_workspace_bytes(w.batch, 12, 128, args.target_splits))
+    ws = ops.decode_workspace(dev, ops.decode_workspace_bytes(
+        w.batch, 12, 128, w.block_tables.shape[1] * w.block_size, args.target_splits))
     nbytes = w.algorithmic_bytes()
 
     def step(i: int) -> None:

@@ -6,10 +6,13 @@ a kernel is called, the call raises RuntimeError.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libfe_paged.so"
+# FE_PAGED_LIB may point at another build of the same library (e.g. a tuning
+# variant); by default the in-tree build next to this file is used.
+LIB_PATH = Path(os.environ.get("FE_PAGED_LIB", Path(__file__).resolve().parent / "libfe_paged.so"))
 
 FE_OK = 0
 FE_ERR_INVALID_ARGUMENT = -1
@@ -29,7 +32,7 @@ SIGNATURES: dict[str, tuple] = {
     "fe_write_kv": (_i, [_p, _p, _i64, _p, _p, _i, _p, _p, _i, _i, _i, _i, _p]),
     "fe_write_kv_decode": (_i, [_p, _p, _i64, _p, _p, _i, _p, _i, _p, _i, _i, _i, _i, _p]),
     "fe_gather_kv": (_i, [_p, _p, _i, _p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p]),
-    "fe_paged_decode_workspace_size": (_sz, [_i, _i, _i, _i]),
+    "fe_paged_decode_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
     "fe_paged_decode": (_i, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i, _p, _i, _p, _p, _sz,
                              _i, _i, _i, _i, _i, _f, _i, _p]),
     "fe_lse_merge": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),

@@ -82,14 +82,26 @@ __device__ __forceinline__ f16x4 hi4(f16x8 v) { return f16x4{v[4], v[5], v[6], v
 
 __device__ __forceinline__ int clamp_len(int L) { return L > 0 ? L : 0; }
 
-__device__ __forceinline__ int split_chunk_quads(const int32_t* ctx, int B, int target) {
+// Context length as the kernels see it: negative -> 0, and never more than
+// the block table can address (max_len = table width * block size).
+__device__ __forceinline__ int seq_len(const int32_t* ctx, int b, int max_len) {
+  const int L = clamp_len(ctx[b]);
+  return L < max_len ? L : max_len;
+}
+
+__device__ __forceinline__ int split_chunk_quads(const int32_t* ctx, int B, int max_len,
+                                                 int target) {
   const int lane = lane_id();
   int total = 0;
   for (int base = 0; base < B; base += kWave) {
     const int b = base + lane;
-    const int L = b < B ? clamp_len(ctx[b]) : 0;
+    const int L = b < B ? seq_len(ctx, b, max_len) : 0;
     total += wave_sum_i((L + 63) >> 6);
   }
+  // the shuffle reduction leaves the same value in every lane; readfirstlane
+  // tells the compiler it is wave-uniform, so every bound and address derived
+  // from it stays in scalar registers
+  total = __builtin_amdgcn_readfirstlane(total);
   const int chunk = (total + target - 1) / target;
   return chunk > 0 ? chunk : 1;
 }
@@ -103,14 +115,15 @@ struct Piece {
   int tok_end;   // one past the last key position of the piece
 };
 
-// Finds the piece with id `item`; false when item is past the last piece.
-__device__ __forceinline__ bool locate_piece(const int32_t* ctx, int B, int chunk,
-                                             int item, Piece& pc) {
+// Finds the piece with id `item`; false when item is past the last piece, in
+// which case `total` receives the number of pieces.
+__device__ __forceinline__ bool locate_piece(const int32_t* ctx, int B, int max_len, int chunk,
+                                             int item, Piece& pc, int& total) {
   const int lane = lane_id();
   int carry = 0;
   for (int base = 0; base < B; base += kWave) {
     const int b = base + lane;
-    const int L = b < B ? clamp_len(ctx[b]) : 0;
+    const int L = b < B ? seq_len(ctx, b, max_len) : 0;
     const int nq = (L + 63) >> 6;
     const int ns = (nq + chunk - 1) / chunk;
     const int incl = wave_scan_incl_i(ns) + carry;
@@ -129,19 +142,20 @@ __device__ __forceinline__ bool locate_piece(const int32_t* ctx, int B, int chun
     }
     carry = readlane_i(incl, kWave - 1);
   }
+  total = carry;
   return false;
 }
 
 // Number of pieces of sequence b and the id of its first piece.
-__device__ __forceinline__ void seq_pieces(const int32_t* ctx, int B, int chunk, int b,
-                                           int& nsplit, int& first) {
+__device__ __forceinline__ void seq_pieces(const int32_t* ctx, int B, int max_len, int chunk,
+                                           int b, int& nsplit, int& first) {
   const int lane = lane_id();
   int carry = 0;
   nsplit = 0;
   first = 0;
   for (int base = 0; base < B; base += kWave) {
     const int bb = base + lane;
-    const int L = bb < B ? clamp_len(ctx[bb]) : 0;
+    const int L = bb < B ? seq_len(ctx, bb, max_len) : 0;
     const int nq = (L + 63) >> 6;
     const int ns = (nq + chunk - 1) / chunk;
     const int incl = wave_scan_incl_i(ns) + carry;

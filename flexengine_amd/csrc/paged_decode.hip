@@ -1,14 +1,20 @@
 // Fused single-token paged decode attention for gfx950 (MI355X).
 //
 // Work decomposition
-//   grid = (pieces, kv_heads); one 256-thread workgroup (4 waves) per
-//   (piece of a sequence's keys, KV head).  The pieces come from the
+//   grid = (target + 2*batch, kv_heads); one 256-thread workgroup (4 waves)
+//   per (piece of a sequence's keys, KV head).  The pieces come from the
 //   device-side split-K partition in fe_common.h, so every workgroup gets an
-//   equal share of keys whatever the context-length mix.  Within a workgroup
-//   wave w takes the 16-token tiles w, w+4, w+8, ... of the piece (tile engine:
-//   attn_core.h) and the four waves are merged through LDS at the end.  A
-//   sequence cut into several pieces writes fp32 partials plus a base-2
-//   log-sum-exp per query head, and decode_merge_kernel combines them.
+//   equal share of keys whatever the context-length mix.  Wave w takes the
+//   16-token tiles w, w+4, w+8, ... of the piece (tile engines: attn_core.h)
+//   and the four waves are merged through LDS.  Workgroups past the last piece
+//   write the zero rows of inactive sequences.
+//
+// Split-K merge: a sequence cut into several pieces has each piece write its
+// fp32 partial output plus a base-2 log-sum-exp per query head to the
+// workspace; decode_merge_kernel, launched right after on the same stream,
+// combines them.  Merging inside the decode kernel would need device-scope
+// release/acquire fences, which on CDNA3/4 write back and invalidate the whole
+// L2 of the XCD per workgroup -- far more expensive than a second launch.
 //
 // One wave serves all G = Hq/Hkv query heads of its KV head (the 16 MFMA
 // columns), so every K/V byte is read from HBM once per step; the reference's
@@ -25,6 +31,15 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kDefaultTarget = 512;
 constexpr int kMaxGroup = 16;
 
+// Register stages of the K/V prefetch pipeline and the occupancy the register
+// allocation is held to (waves per SIMD); tuned on MI355X for head_dim 128.
+#ifndef FE_DECODE_STAGES
+#define FE_DECODE_STAGES 2
+#endif
+#ifndef FE_DECODE_WAVES_PER_EU
+#define FE_DECODE_WAVES_PER_EU 3
+#endif
+
 struct DecodeArgs {
   const f16* q;
   f16* out;
@@ -34,36 +49,20 @@ struct DecodeArgs {
   f16* v_pool;
   const int32_t* tables;
   const int32_t* ctx;
-  float* ws_o;    // [pieces, Hq, D]
-  float* ws_lse;  // [pieces, Hq]  (base 2)
+  float* ws_o;       // [pieces, Hq, D]
+  float* ws_lse;     // [pieces, Hq]  (base 2)
   int64_t q_stride;
   int64_t new_stride;
   int W, B, Hq, Hkv, G, BS, bs_log2, NB, target;
+  int max_len;       // W * BS: longest context the tables can address
   float scale_log2;  // softmax scale * log2(e)
 };
 
-template <int D>
-__global__ __launch_bounds__(kThreads) void paged_decode_kernel(const DecodeArgs a) {
-  using C = TileCfg<D>;
-  extern __shared__ __align__(16) unsigned char smem[];
-
-  const int chunk = split_chunk_quads(a.ctx, a.B, a.target);
-  Piece pc;
-  if (!locate_piece(a.ctx, a.B, chunk, blockIdx.x, pc)) return;
-
-  const int h = blockIdx.y;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = lane_id();
-  const int g = lane >> 4;
-  const int n = lane & 15;
-  const int G = a.G;
-  const int b = pc.b;
-
-  TileCore<D> core;
-  core.k_pool = a.k_pool;
-  core.v_pool = a.v_pool;
-  core.trow = a.tables + (int64_t)b * a.W;
-  core.rs = (int64_t)a.Hkv * D;
+template <int D, class Core>
+__device__ __forceinline__ void setup_core(Core& core, const DecodeArgs& a, const Piece& pc, int h,
+                                           unsigned char* stage) {
+  core.trow = a.tables + (int64_t)pc.b * a.W;
+  core.rs = a.Hkv * D;
   core.hoff = h * D;
   core.W = a.W;
   core.NB = a.NB;
@@ -73,44 +72,108 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(const DecodeArgs
   core.limit = pc.tok_end;
   core.scale_log2 = a.scale_log2;
   if (a.k_new != nullptr) {
-    core.knew_row = a.k_new + (int64_t)b * a.new_stride + (int64_t)h * D;
-    core.vnew_row = a.v_new + (int64_t)b * a.new_stride + (int64_t)h * D;
+    core.knew_row = a.k_new + (int64_t)pc.b * a.new_stride + (int64_t)h * D;
+    core.vnew_row = a.v_new + (int64_t)pc.b * a.new_stride + (int64_t)h * D;
     core.new_pos = pc.L - 1;
   } else {
     core.knew_row = nullptr;
     core.vnew_row = nullptr;
     core.new_pos = -1;
   }
-  core.stage = smem + w * C::STAGE;
+  core.stage = stage;
+}
 
+template <int D, bool PAGE16>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(FE_DECODE_WAVES_PER_EU, 8)))
+void paged_decode_kernel(const DecodeArgs a) {
+  using C = TileCfg<D>;
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int h = blockIdx.y;
+  const int item = blockIdx.x;
+  const int chunk = split_chunk_quads(a.ctx, a.B, a.max_len, a.target);
+  Piece pc;
+  int total = 0;
+  if (!locate_piece(a.ctx, a.B, a.max_len, chunk, item, pc, total)) {
+    // spare workgroup: zero rows of inactive sequences
+    const int b = item - total;
+    if (b < a.B && seq_len(a.ctx, b, a.max_len) == 0) {
+      for (int e = threadIdx.x; e < a.G * D; e += kThreads)
+        a.out[((int64_t)b * a.Hq + h * a.G) * D + e] = (f16)0.f;
+    }
+    return;
+  }
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = lane_id();
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int G = a.G;
+  const int b = pc.b;
+  const int t_first = pc.tok_begin / kTile + w;
+  const int t_end = (pc.tok_end + kTile - 1) / kTile;
+
+  f16x8 qv[C::NK];
   {
     const int hq = h * G + (n < G ? n : G - 1);
     const f16* qrow = a.q + (int64_t)b * a.q_stride + (int64_t)hq * D;
 #pragma unroll
     for (int s = 0; s < C::NK; ++s) {
       const f16x8 v = ld16(qrow + (4 * s + g) * 8);
-      core.qv[s] = n < G ? v : f16x8{};
+      qv[s] = n < G ? v : f16x8{};
     }
   }
-  core.init_acc();
-  core.run(pc.tok_begin / kTile + w, kWaves, (pc.tok_end + kTile - 1) / kTile);
 
-  // ---- combine the four waves ----
-  const float l_tot = core.l_total();
+  float m_run, l_tot;
+  f32x4 o[C::NX];
+  if constexpr (PAGE16) {
+    Page16Core<D> core;
+    setup_core<D>(core, a, pc, h, smem + w * C::STAGE);
+    core.k_pool = a.k_pool;
+    core.v_pool = a.v_pool;
+    core.k_pool_w = a.k_pool;
+    core.v_pool_w = a.v_pool;
+    core.t_first = t_first;
+    core.step = kWaves;
+#pragma unroll
+    for (int s = 0; s < C::NK; ++s) core.qv[s] = qv[s];
+    core.init_acc();
+    core.template run<FE_DECODE_STAGES>(t_end);
+    m_run = core.m_run;
+    l_tot = core.l_total();
+#pragma unroll
+    for (int x = 0; x < C::NX; ++x) o[x] = core.o[x];
+  } else {
+    TileCore<D> core;
+    setup_core<D>(core, a, pc, h, smem + w * C::STAGE);
+    core.k_pool = a.k_pool;
+    core.v_pool = a.v_pool;
+#pragma unroll
+    for (int s = 0; s < C::NK; ++s) core.qv[s] = qv[s];
+    core.init_acc();
+    core.run(t_first, kWaves, t_end);
+    m_run = core.m_run;
+    l_tot = core.l_total();
+#pragma unroll
+    for (int x = 0; x < C::NX; ++x) o[x] = core.o[x];
+  }
+
+  // ---- combine the four waves through LDS ----
   float* mO = reinterpret_cast<float*>(smem + kWaves * C::STAGE);  // [4][G][D]
   float* mM = mO + kWaves * G * D;                                 // [4][16]
   float* mL = mM + kWaves * kMaxGroup;                             // [4][16]
   if (n < G) {
 #pragma unroll
     for (int x = 0; x < C::NX; ++x)
-      *reinterpret_cast<f32x4*>(mO + (w * G + n) * D + 16 * x + 4 * g) = core.o[x];
+      *reinterpret_cast<f32x4*>(mO + (w * G + n) * D + 16 * x + 4 * g) = o[x];
     if (g == 0) {
-      mM[w * kMaxGroup + n] = core.m_run;
+      mM[w * kMaxGroup + n] = m_run;
       mL[w * kMaxGroup + n] = l_tot;
     }
   }
   __syncthreads();
-  const int item = blockIdx.x;
+  const bool split = pc.nsplit > 1;
   for (int e = threadIdx.x; e < G * D; e += kThreads) {
     const int hh = e / D;
     const int d = e - hh * D;
@@ -127,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(const DecodeArgs
     }
     const float res = num / den;
     const int hq = h * G + hh;
-    if (pc.nsplit == 1) {
+    if (!split) {
       a.out[((int64_t)b * a.Hq + hq) * D + d] = (f16)res;
     } else {
       a.ws_o[((int64_t)item * a.Hq + hq) * D + d] = res;
@@ -136,36 +199,47 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(const DecodeArgs
   }
 }
 
-// Combines the pieces of every split sequence; writes zeros for inactive rows.
+// Combines the pieces of every split sequence: one workgroup of D threads per
+// (sequence, query head), thread d owning output dim d.  The piece loop is
+// unrolled so that the partial loads of several pieces are in flight at once.
 template <int D>
-__global__ __launch_bounds__(kThreads) void decode_merge_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
   const int b = blockIdx.x;
-  const int h = blockIdx.y;
-  const int G = a.G;
-  const int L = clamp_len(a.ctx[b]);
-  if (L == 0) {
-    for (int e = threadIdx.x; e < G * D; e += kThreads)
-      a.out[((int64_t)b * a.Hq + h * G) * D + e] = (f16)0.f;
-    return;
-  }
-  const int chunk = split_chunk_quads(a.ctx, a.B, a.target);
+  const int hq = blockIdx.y;
+  const int d = threadIdx.x;
+  if (seq_len(a.ctx, b, a.max_len) == 0) return;  // inactive: zeros written by the decode kernel
+  const int chunk = split_chunk_quads(a.ctx, a.B, a.max_len, a.target);
   int ns, first;
-  seq_pieces(a.ctx, a.B, chunk, b, ns, first);
-  if (ns <= 1) return;
-  for (int e = threadIdx.x; e < G * D; e += kThreads) {
-    const int hh = e / D;
-    const int d = e - hh * D;
-    const int hq = h * G + hh;
-    float M = kNegInf;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, a.ws_lse[(int64_t)(first + s) * a.Hq + hq]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < ns; ++s) {
-      const float sc = exp2f(a.ws_lse[(int64_t)(first + s) * a.Hq + hq] - M);
-      num += sc * a.ws_o[((int64_t)(first + s) * a.Hq + hq) * D + d];
-      den += sc;
+  seq_pieces(a.ctx, a.B, a.max_len, chunk, b, ns, first);
+  if (ns <= 1) return;  // written directly by the decode kernel
+  const float* lse = a.ws_lse + (int64_t)first * a.Hq + hq;
+  const float* po = a.ws_o + ((int64_t)first * a.Hq + hq) * D + d;
+  const int64_t lse_step = a.Hq;
+  const int64_t o_step = (int64_t)a.Hq * D;
+  float M = kNegInf;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, lse[s * lse_step]);
+  float num = 0.f, den = 0.f;
+  int s = 0;
+  for (; s + 4 <= ns; s += 4) {
+    float l4[4], o4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      l4[u] = lse[(s + u) * lse_step];
+      o4[u] = po[(s + u) * o_step];
     }
-    a.out[((int64_t)b * a.Hq + hq) * D + d] = (f16)(num / den);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float wgt = exp2f(l4[u] - M);
+      num += wgt * o4[u];
+      den += wgt;
+    }
   }
+  for (; s < ns; ++s) {
+    const float wgt = exp2f(lse[s * lse_step] - M);
+    num += wgt * po[s * o_step];
+    den += wgt;
+  }
+  a.out[((int64_t)b * a.Hq + hq) * D + d] = (f16)(num / den);
 }
 
 // General LSE merge of S partial results (natural-log LSE at the boundary).
@@ -201,11 +275,22 @@ inline int log2_exact(int x) {
 }
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// workspace = [partial outputs | partial lse]
 inline size_t ws_o_bytes(int batch, int hq, int d, int target) {
   return align256((size_t)(target + batch) * hq * d * sizeof(float));
 }
 inline size_t ws_lse_bytes(int batch, int hq, int target) {
   return align256((size_t)(target + batch) * hq * sizeof(float));
+}
+
+// Pieces per KV head the kernel aims for.  Raised above the request when the
+// tables allow very long contexts, so that no piece exceeds 64 quads (4096
+// keys, 64 tiles per wave: one block-id fetch per wave).
+inline int effective_target(int batch, int max_context, int target_splits) {
+  const int target = target_splits > 0 ? target_splits : kDefaultTarget;
+  const int64_t max_quads = ((int64_t)max_context + 63) / 64;
+  const int64_t need = ((int64_t)batch * max_quads + 63) / 64;
+  return need > target ? (int)need : target;
 }
 
 template <int D>
@@ -216,21 +301,25 @@ size_t decode_lds_bytes(int G) {
 
 template <int D>
 int launch_decode(const DecodeArgs& a, hipStream_t stream) {
-  const dim3 grid(a.target + a.B, a.Hkv);
-  hipLaunchKernelGGL(paged_decode_kernel<D>, grid, dim3(kThreads), decode_lds_bytes<D>(a.G),
-                     stream, a);
-  int st = FE_LAUNCH_STATUS();
+  const dim3 grid(a.target + 2 * a.B, a.Hkv);
+  const size_t lds = decode_lds_bytes<D>(a.G);
+  if (a.BS % kTile == 0)
+    hipLaunchKernelGGL((paged_decode_kernel<D, true>), grid, dim3(kThreads), lds, stream, a);
+  else
+    hipLaunchKernelGGL((paged_decode_kernel<D, false>), grid, dim3(kThreads), lds, stream, a);
+  const int st = FE_LAUNCH_STATUS();
   if (st != 0) return st;
-  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.B, a.Hkv), dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.B, a.Hq), dim3(D), 0, stream, a);
   return FE_LAUNCH_STATUS();
 }
 
 }  // namespace
 
 extern "C" size_t fe_paged_decode_workspace_size(int batch, int num_q_heads, int head_dim,
-                                                 int target_splits) {
-  if (batch < 0 || num_q_heads <= 0 || head_dim <= 0) return 0;
-  const int target = target_splits > 0 ? target_splits : kDefaultTarget;
+                                                 int max_context, int target_splits) {
+  if (batch < 0 || num_q_heads <= 0 || head_dim <= 0 || max_context < 0 || target_splits < 0)
+    return 0;
+  const int target = effective_target(batch, max_context, target_splits);
   return ws_o_bytes(batch, num_q_heads, head_dim, target) +
          ws_lse_bytes(batch, num_q_heads, target);
 }
@@ -256,12 +345,16 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
   FE_CHECK_ARG((k_new == nullptr) == (v_new == nullptr));
   FE_CHECK_ARG(q_batch_stride % 8 == 0 && q_batch_stride >= (int64_t)num_q_heads * head_dim);
   FE_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(k_pool) && aligned16(v_pool));
+  // lane offsets inside a block are 32-bit
+  FE_CHECK_ARG((int64_t)block_size * kv_heads * head_dim < (int64_t)1 << 30);
   if (k_new) {
     FE_CHECK_ARG(aligned16(k_new) && aligned16(v_new) && new_batch_stride % 8 == 0 &&
                  new_batch_stride >= (int64_t)kv_heads * head_dim);
   }
-  const int target = target_splits > 0 ? target_splits : kDefaultTarget;
-  const size_t need = fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, target);
+  const int max_len = table_stride * block_size;
+  FE_CHECK_ARG((int64_t)table_stride * block_size < ((int64_t)1 << 30));
+  const int target = effective_target(batch, max_len, target_splits);
+  const size_t need = fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, max_len, target);
   if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
     return FE_ERR_WORKSPACE;
 
@@ -274,8 +367,10 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
   a.v_pool = (f16*)v_pool;
   a.tables = block_tables;
   a.ctx = context_lens;
-  a.ws_o = (float*)workspace;
-  a.ws_lse = (float*)((char*)workspace + ws_o_bytes(batch, num_q_heads, head_dim, target));
+  char* ws = (char*)workspace;
+  a.ws_o = (float*)ws;
+  ws += ws_o_bytes(batch, num_q_heads, head_dim, target);
+  a.ws_lse = (float*)ws;
   a.q_stride = q_batch_stride;
   a.new_stride = new_batch_stride;
   a.W = table_stride;
@@ -287,6 +382,7 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
   a.bs_log2 = bs_log2;
   a.NB = num_blocks;
   a.target = target;
+  a.max_len = max_len;
   a.scale_log2 = scale * kLog2e;
   if (head_dim == 64) return launch_decode<64>(a, (hipStream_t)stream);
   return launch_decode<128>(a, (hipStream_t)stream);

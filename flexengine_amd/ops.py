@@ -125,12 +125,15 @@ def gather_kv(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Te
 _WORKSPACES: dict[tuple, torch.Tensor] = {}
 
 
-def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, target_splits: int = 0) -> int:
-    return int(_lib.load().fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, target_splits))
+def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_context: int,
+                           target_splits: int = 0) -> int:
+    """Workspace bytes for fe_paged_decode; max_context = table width * block size."""
+    return int(_lib.load().fe_paged_decode_workspace_size(batch, num_q_heads, head_dim,
+                                                          max_context, target_splits))
 
 
 def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A per-device scratch buffer reused by every decode call on that device.
+    """A per-device workspace reused by every decode call on that device.
 
     Calls on one stream are ordered, so sharing is safe there; callers running
     decode on several streams at once must pass their own workspace.
@@ -185,7 +188,7 @@ def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
         raise ValueError("out must be a contiguous float16 [batch, num_q_heads, head_dim]")
     if scale is None:
         scale = 1.0 / math.sqrt(d)
-    need = decode_workspace_bytes(batch, hq, d, target_splits)
+    need = decode_workspace_bytes(batch, hq, d, block_tables.shape[1] * bs, target_splits)
     if workspace is None:
         workspace = decode_workspace(dev, need)
     _lib.call("fe_paged_decode", q.data_ptr(), q.stride(0), out.data_ptr(), _ptr(k_new),

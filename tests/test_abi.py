@@ -96,12 +96,15 @@ def test_host_side_validation_rejects_before_launch(lib):
 
 
 def test_workspace_size_grows_with_batch_and_target(lib):
-    a = lib.fe_paged_decode_workspace_size(64, 12, 128, 0)
-    b = lib.fe_paged_decode_workspace_size(128, 12, 128, 0)
-    c = lib.fe_paged_decode_workspace_size(64, 12, 128, 2048)
+    a = lib.fe_paged_decode_workspace_size(64, 12, 128, 4096, 0)
+    b = lib.fe_paged_decode_workspace_size(128, 12, 128, 4096, 0)
+    c = lib.fe_paged_decode_workspace_size(64, 12, 128, 4096, 2048)
     assert 0 < a < b and a < c
     assert a % 256 == 0
-    assert lib.fe_paged_decode_workspace_size(-1, 12, 128, 0) == 0
+    assert lib.fe_paged_decode_workspace_size(-1, 12, 128, 4096, 0) == 0
+    # very long tables raise the split target (pieces stay <= 4096 keys)
+    d = lib.fe_paged_decode_workspace_size(64, 12, 128, 1 << 20, 0)
+    assert d > a
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

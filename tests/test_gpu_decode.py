@@ -247,3 +247,38 @@ def test_error_codes_surface_as_exceptions():
     c = torch.ones(1, dtype=torch.int32, device=DEV)
     with pytest.raises(RuntimeError, match="unsupported"):
         ops.paged_decode(q, pool, pool, t, c)
+
+
+@pytest.mark.parametrize("bs", [16, 32])
+def test_fused_write_short_contexts(bs):
+    """The decoded token's row is stored and re-read inside the kernel; at L=1 the output
+    must equal v_new exactly for every query head of the group."""
+    lengths = [1, 2, 15, 16, 17, 63, 64, 65, 130]
+    w = workloads.make_decode_workload("fused", 40 + bs, len(lengths), 12, 2, 128, lengths,
+                                       block_size=bs, with_new_kv=True)
+    got, d = run_decode(w)
+    exp, kp, vp = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what="fused short")
+    v_new = w.v_new.numpy()
+    for h in range(12):
+        assert (got[0, h].numpy() == v_new[0, h // 6]).all()
+    assert d.k_pool.cpu().numpy().tobytes() == kp.tobytes()
+    assert d.v_pool.cpu().numpy().tobytes() == vp.tobytes()
+
+
+def test_workspace_reuse_across_shapes():
+    """One workspace serves calls of different shapes and split counts in a row."""
+    big = workloads.c2_workload(batch=32)
+    small = workloads.make_decode_workload("small", 3, 3, 12, 2, 128, [700, 5, 2000])
+    exp_big, _, _ = oracle_decode(big)
+    exp_small, _, _ = oracle_decode(small)
+    ws = torch.full((ops.decode_workspace_bytes(32, 12, 128, 4096, 2048),), 0x7F,
+                    dtype=torch.uint8, device=DEV)  # garbage contents
+    db, dsm = big.to(DEV), small.to(DEV)
+    for target in (2048, 7, 512, 64):
+        ob = ops.paged_decode(db.q, db.k_pool, db.v_pool, db.block_tables, db.context_lens,
+                              k_new=db.k_new, v_new=db.v_new, workspace=ws, target_splits=target)
+        osm = ops.paged_decode(dsm.q, dsm.k_pool, dsm.v_pool, dsm.block_tables, dsm.context_lens,
+                               workspace=ws, target_splits=target)
+        assert_attention_close(ob.cpu().numpy(), exp_big, what=f"big t={target}")
+        assert_attention_close(osm.cpu().numpy(), exp_small, what=f"small t={target}")
