@@ -50,7 +50,23 @@ def parse_args(argv=None):
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                   help="only run a device-to-device copy of MB MiB --steps times (calibrates the "
+                        "rocprofv3 FETCH_SIZE / WRITE_SIZE counters against a known byte count)")
     return p.parse_args(argv)
+
+
+def calibrate_copy(mb: int, steps: int) -> int:
+    import torch
+
+    src = torch.ones(mb << 20, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read_per_launch": src.numel(),
+                      "bytes_written_per_launch": dst.numel(), "launches": steps}), flush=True)
+    return 0
 
 
 def cpu_baseline(w, budget_s: float) -> dict:
@@ -103,6 +119,8 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy, args.steps)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     w = workloads.c2_workload()
@@ -209,7 +227,8 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "fe_paged_decode (paged_decode_kernel<128> + decode_merge_kernel<128>)",
+            "kernel": "paged_decode_kernel<128, true> (fe_paged_decode: page write + split-K "
+                      "attention + in-kernel LSE merge, one launch)",
             "us_per_launch": round(per_launch_ms * 1e3, 3),
         },
         "cpu_baseline": cpu,

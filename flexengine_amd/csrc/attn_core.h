@@ -349,9 +349,9 @@ struct Page16Core {
     for (int j = 0; j < C::NK; ++j)
       if (j * C::RPI + vrow == r)
         *reinterpret_cast<f16x8*>(vb + v_off0() + v_soff(j)) = ld16(vnew_row + (lane % C::CPR) * 8);
-    // the stores complete before any tile load is issued (and the compiler may
-    // not move the buffer loads above them)
-    __threadfence_block();
+    // The same lanes load these addresses later: a wave's memory operations to
+    // one address are performed in order, so only the compiler needs holding
+    // back (it may not move the buffer loads above these stores).
     compiler_fence();
   }
 

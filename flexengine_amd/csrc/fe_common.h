@@ -89,20 +89,38 @@ __device__ __forceinline__ int seq_len(const int32_t* ctx, int b, int max_len) {
   return L < max_len ? L : max_len;
 }
 
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const int o = __shfl_xor(v, m, kWave);
+    v = v > o ? v : o;
+  }
+  return v;
+}
+
+// Chunk size in quads.  Besides ~target pieces in total, no sequence may be
+// cut into more than kMaxPieces pieces (the merge holds their weights in LDS).
+constexpr int kMaxPieces = 64;
+
 __device__ __forceinline__ int split_chunk_quads(const int32_t* ctx, int B, int max_len,
                                                  int target) {
   const int lane = lane_id();
-  int total = 0;
+  int total = 0, longest = 0;
   for (int base = 0; base < B; base += kWave) {
     const int b = base + lane;
-    const int L = b < B ? seq_len(ctx, b, max_len) : 0;
-    total += wave_sum_i((L + 63) >> 6);
+    const int nq = b < B ? (seq_len(ctx, b, max_len) + 63) >> 6 : 0;
+    total += wave_sum_i(nq);
+    const int m = wave_max_i(nq);
+    longest = longest > m ? longest : m;
   }
-  // the shuffle reduction leaves the same value in every lane; readfirstlane
-  // tells the compiler it is wave-uniform, so every bound and address derived
-  // from it stays in scalar registers
+  // the shuffle reductions leave the same value in every lane; readfirstlane
+  // tells the compiler they are wave-uniform, so every bound and address
+  // derived from them stays in scalar registers
   total = __builtin_amdgcn_readfirstlane(total);
-  const int chunk = (total + target - 1) / target;
+  longest = __builtin_amdgcn_readfirstlane(longest);
+  int chunk = (total + target - 1) / target;
+  const int floor_chunk = (longest + kMaxPieces - 1) / kMaxPieces;
+  chunk = chunk > floor_chunk ? chunk : floor_chunk;
   return chunk > 0 ? chunk : 1;
 }
 

@@ -9,12 +9,20 @@
 //   and the four waves are merged through LDS.  Workgroups past the last piece
 //   write the zero rows of inactive sequences.
 //
-// Split-K merge: a sequence cut into several pieces has each piece write its
-// fp32 partial output plus a base-2 log-sum-exp per query head to the
-// workspace; decode_merge_kernel, launched right after on the same stream,
-// combines them.  Merging inside the decode kernel would need device-scope
-// release/acquire fences, which on CDNA3/4 write back and invalidate the whole
-// L2 of the XCD per workgroup -- far more expensive than a second launch.
+// Split-K merge, in the same launch: a sequence cut into several pieces has
+// each piece write its fp32 partial output plus a base-2 log-sum-exp per query
+// head to the workspace, then draw a ticket from a per-(sequence, KV head)
+// counter; the workgroup drawing the last ticket merges all pieces and resets
+// the counter, so the workspace is ready for the next call without a memset.
+// Cross-workgroup visibility uses device-coherent accesses only: partials are
+// written and read with agent-scope atomic stores/loads (which bypass the
+// per-XCD L2), and the writer waits for its stores to complete before taking
+// its ticket.  The agent-scope fences of the language memory model would
+// instead write back and invalidate the whole L2 of the XCD per workgroup.
+//
+// The grid is flattened as x = piece * kv_heads + kv_head, so the kv_heads
+// workgroups of one piece are dispatched together: they read interleaved
+// halves of the same 512-byte pool rows.
 //
 // One wave serves all G = Hq/Hkv query heads of its KV head (the 16 MFMA
 // columns), so every K/V byte is read from HBM once per step; the reference's
@@ -28,7 +36,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kDefaultTarget = 512;
+// Default split target: about 512 working workgroups in total (two per CU of
+// MI355X's 256), i.e. 512 / kv_heads pieces per KV head; measured best at C2.
+constexpr int kDefaultWorkgroups = 512;
 constexpr int kMaxGroup = 16;
 
 // Register stages of the K/V prefetch pipeline and the occupancy the register
@@ -51,12 +61,94 @@ struct DecodeArgs {
   const int32_t* ctx;
   float* ws_o;       // [pieces, Hq, D]
   float* ws_lse;     // [pieces, Hq]  (base 2)
+  int* tickets;      // [B, Hkv], zero between calls
   int64_t q_stride;
   int64_t new_stride;
   int W, B, Hq, Hkv, G, BS, bs_log2, NB, target;
   int max_len;       // W * BS: longest context the tables can address
   float scale_log2;  // softmax scale * log2(e)
 };
+
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until every memory operation this wave issued has completed.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Combines the ns pieces (ids first .. first+ns-1) of sequence b, KV head h:
+// per query head, out = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
+// Each thread owns up to kMergePer output elements; the partial outputs of up
+// to kMergeBatch pieces are requested together with the LSEs, so the common
+// case (ns <= kMergeBatch) costs a single round trip to memory.
+constexpr int kMergeBatch = 16;
+constexpr int kMergePer = 3;  // ceil(G*D / 256) for G*D <= 768 (G 6, D 128)
+
+template <int D>
+__device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, int first, int ns,
+                                             unsigned char* smem) {
+  const int G = a.G;
+  const int GD = G * D;
+  float* wts = reinterpret_cast<float*>(smem);  // [ns][G] LSEs -> weights, then [G] 1/den
+  float* inv = wts + ns * G;
+  const int64_t step = (int64_t)a.Hq * D;
+  const float* base = a.ws_o + ((int64_t)first * a.Hq + h * G) * D;
+  __syncthreads();  // LDS reuse: the wave merge above is done with it
+  for (int e0 = 0; e0 < GD; e0 += kThreads * kMergePer) {
+    float acc[kMergePer];
+#pragma unroll
+    for (int r = 0; r < kMergePer; ++r) acc[r] = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += kMergeBatch) {
+      // requests: this batch's partial outputs, and (first batch) every LSE
+      float v[kMergePer][kMergeBatch];
+#pragma unroll
+      for (int r = 0; r < kMergePer; ++r) {
+        const int e = e0 + r * kThreads + (int)threadIdx.x;
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+          v[r][u] = (e < GD && s0 + u < ns) ? load_coherent(base + (s0 + u) * step + e) : 0.f;
+      }
+      if (s0 == 0) {
+        for (int i = threadIdx.x; i < ns * G; i += kThreads) {
+          const int s = i / G, hh = i - s * G;
+          wts[i] = load_coherent(a.ws_lse + (int64_t)(first + s) * a.Hq + h * G + hh);
+        }
+        __syncthreads();
+        if (threadIdx.x < G) {
+          const int hh = threadIdx.x;
+          float M = kNegInf;
+          for (int s = 0; s < ns; ++s) M = fmaxf(M, wts[s * G + hh]);
+          float den = 0.f;
+          for (int s = 0; s < ns; ++s) {
+            const float wv = exp2f(wts[s * G + hh] - M);
+            wts[s * G + hh] = wv;
+            den += wv;
+          }
+          inv[hh] = 1.f / den;
+        }
+        __syncthreads();
+      }
+#pragma unroll
+      for (int r = 0; r < kMergePer; ++r) {
+        const int e = e0 + r * kThreads + (int)threadIdx.x;
+        const int hh = (e < GD ? e : 0) / D;
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+          if (s0 + u < ns) acc[r] += wts[(s0 + u) * G + hh] * v[r][u];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kMergePer; ++r) {
+      const int e = e0 + r * kThreads + (int)threadIdx.x;
+      if (e < GD) {
+        const int hh = e / D;
+        a.out[((int64_t)b * a.Hq + h * G) * D + e] = (f16)(acc[r] * inv[hh]);
+      }
+    }
+  }
+}
 
 template <int D, class Core>
 __device__ __forceinline__ void setup_core(Core& core, const DecodeArgs& a, const Piece& pc, int h,
@@ -90,8 +182,8 @@ void paged_decode_kernel(const DecodeArgs a) {
   using C = TileCfg<D>;
   extern __shared__ __align__(16) unsigned char smem[];
 
-  const int h = blockIdx.y;
-  const int item = blockIdx.x;
+  const int h = blockIdx.x % a.Hkv;
+  const int item = blockIdx.x / a.Hkv;
   const int chunk = split_chunk_quads(a.ctx, a.B, a.max_len, a.target);
   Piece pc;
   int total = 0;
@@ -163,6 +255,7 @@ void paged_decode_kernel(const DecodeArgs a) {
   float* mO = reinterpret_cast<float*>(smem + kWaves * C::STAGE);  // [4][G][D]
   float* mM = mO + kWaves * G * D;                                 // [4][16]
   float* mL = mM + kWaves * kMaxGroup;                             // [4][16]
+  int* flag = reinterpret_cast<int*>(mL + kWaves * kMaxGroup);
   if (n < G) {
 #pragma unroll
     for (int x = 0; x < C::NX; ++x)
@@ -193,53 +286,23 @@ void paged_decode_kernel(const DecodeArgs a) {
     if (!split) {
       a.out[((int64_t)b * a.Hq + hq) * D + d] = (f16)res;
     } else {
-      a.ws_o[((int64_t)item * a.Hq + hq) * D + d] = res;
-      if (d == 0) a.ws_lse[(int64_t)item * a.Hq + hq] = M + log2f(den);
+      store_coherent(a.ws_o + ((int64_t)item * a.Hq + hq) * D + d, res);
+      if (d == 0) store_coherent(a.ws_lse + (int64_t)item * a.Hq + hq, M + log2f(den));
     }
   }
-}
+  if (!split) return;
 
-// Combines the pieces of every split sequence: one workgroup of D threads per
-// (sequence, query head), thread d owning output dim d.  The piece loop is
-// unrolled so that the partial loads of several pieces are in flight at once.
-template <int D>
-__global__ __launch_bounds__(D) void decode_merge_kernel(const DecodeArgs a) {
-  const int b = blockIdx.x;
-  const int hq = blockIdx.y;
-  const int d = threadIdx.x;
-  if (seq_len(a.ctx, b, a.max_len) == 0) return;  // inactive: zeros written by the decode kernel
-  const int chunk = split_chunk_quads(a.ctx, a.B, a.max_len, a.target);
-  int ns, first;
-  seq_pieces(a.ctx, a.B, a.max_len, chunk, b, ns, first);
-  if (ns <= 1) return;  // written directly by the decode kernel
-  const float* lse = a.ws_lse + (int64_t)first * a.Hq + hq;
-  const float* po = a.ws_o + ((int64_t)first * a.Hq + hq) * D + d;
-  const int64_t lse_step = a.Hq;
-  const int64_t o_step = (int64_t)a.Hq * D;
-  float M = kNegInf;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, lse[s * lse_step]);
-  float num = 0.f, den = 0.f;
-  int s = 0;
-  for (; s + 4 <= ns; s += 4) {
-    float l4[4], o4[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      l4[u] = lse[(s + u) * lse_step];
-      o4[u] = po[(s + u) * o_step];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float wgt = exp2f(l4[u] - M);
-      num += wgt * o4[u];
-      den += wgt;
-    }
-  }
-  for (; s < ns; ++s) {
-    const float wgt = exp2f(lse[s * lse_step] - M);
-    num += wgt * po[s * o_step];
-    den += wgt;
-  }
-  a.out[((int64_t)b * a.Hq + hq) * D + d] = (f16)(num / den);
+  // ---- split-K: the last piece of (b, h) to finish merges all pieces ----
+  wait_stores();  // this thread's partials are complete at the device-coherent level
+  __syncthreads();
+  int* ticket = a.tickets + b * a.Hkv + h;
+  if (threadIdx.x == 0)
+    *flag = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            pc.nsplit - 1;
+  __syncthreads();
+  if (!*flag) return;
+  if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  merge_pieces<D>(a, b, h, item - pc.split, pc.nsplit, smem);
 }
 
 // General LSE merge of S partial results (natural-log LSE at the boundary).
@@ -275,7 +338,11 @@ inline int log2_exact(int x) {
 }
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// workspace = [partial outputs | partial lse]
+// workspace = [tickets (fixed region) | partial outputs | partial lse].  The
+// ticket region sits at offset 0 with a fixed size, so calls of any shape
+// share it and find it zero.
+constexpr int kMaxTickets = 65536;
+constexpr size_t kTicketBytes = kMaxTickets * sizeof(int);
 inline size_t ws_o_bytes(int batch, int hq, int d, int target) {
   return align256((size_t)(target + batch) * hq * d * sizeof(float));
 }
@@ -286,8 +353,9 @@ inline size_t ws_lse_bytes(int batch, int hq, int target) {
 // Pieces per KV head the kernel aims for.  Raised above the request when the
 // tables allow very long contexts, so that no piece exceeds 64 quads (4096
 // keys, 64 tiles per wave: one block-id fetch per wave).
-inline int effective_target(int batch, int max_context, int target_splits) {
-  const int target = target_splits > 0 ? target_splits : kDefaultTarget;
+inline int effective_target(int batch, int kv_heads, int max_context, int target_splits) {
+  const int target =
+      target_splits > 0 ? target_splits : (kDefaultWorkgroups + kv_heads - 1) / kv_heads;
   const int64_t max_quads = ((int64_t)max_context + 63) / 64;
   const int64_t need = ((int64_t)batch * max_quads + 63) / 64;
   return need > target ? (int)need : target;
@@ -295,21 +363,21 @@ inline int effective_target(int batch, int max_context, int target_splits) {
 
 template <int D>
 size_t decode_lds_bytes(int G) {
-  return (size_t)kWaves * TileCfg<D>::STAGE + (size_t)kWaves * G * D * sizeof(float) +
-         2 * kWaves * kMaxGroup * sizeof(float);
+  const size_t waves = (size_t)kWaves * TileCfg<D>::STAGE + (size_t)kWaves * G * D * sizeof(float) +
+                       2 * kWaves * kMaxGroup * sizeof(float) + 16;
+  // merge_pieces: kMaxPieces x G weights + G inverses
+  const size_t merge = (size_t)(kMaxPieces + 1) * G * sizeof(float);
+  return waves > merge ? waves : merge;
 }
 
 template <int D>
 int launch_decode(const DecodeArgs& a, hipStream_t stream) {
-  const dim3 grid(a.target + 2 * a.B, a.Hkv);
+  const dim3 grid((a.target + 2 * a.B) * a.Hkv);
   const size_t lds = decode_lds_bytes<D>(a.G);
   if (a.BS % kTile == 0)
     hipLaunchKernelGGL((paged_decode_kernel<D, true>), grid, dim3(kThreads), lds, stream, a);
   else
     hipLaunchKernelGGL((paged_decode_kernel<D, false>), grid, dim3(kThreads), lds, stream, a);
-  const int st = FE_LAUNCH_STATUS();
-  if (st != 0) return st;
-  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.B, a.Hq), dim3(D), 0, stream, a);
   return FE_LAUNCH_STATUS();
 }
 
@@ -319,8 +387,9 @@ extern "C" size_t fe_paged_decode_workspace_size(int batch, int num_q_heads, int
                                                  int max_context, int target_splits) {
   if (batch < 0 || num_q_heads <= 0 || head_dim <= 0 || max_context < 0 || target_splits < 0)
     return 0;
-  const int target = effective_target(batch, max_context, target_splits);
-  return ws_o_bytes(batch, num_q_heads, head_dim, target) +
+  // sized for the largest default (kv_heads = 1): valid for every kv_heads
+  const int target = effective_target(batch, 1, max_context, target_splits);
+  return kTicketBytes + ws_o_bytes(batch, num_q_heads, head_dim, target) +
          ws_lse_bytes(batch, num_q_heads, target);
 }
 
@@ -338,6 +407,7 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
   FE_CHECK_ARG(num_q_heads % kv_heads == 0);
   const int G = num_q_heads / kv_heads;
   if (G > kMaxGroup) return FE_ERR_UNSUPPORTED;
+  if ((int64_t)batch * kv_heads > kMaxTickets) return FE_ERR_UNSUPPORTED;
   const int bs_log2 = log2_exact(block_size);
   if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
   if (batch == 0) return FE_OK;
@@ -351,9 +421,11 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
     FE_CHECK_ARG(aligned16(k_new) && aligned16(v_new) && new_batch_stride % 8 == 0 &&
                  new_batch_stride >= (int64_t)kv_heads * head_dim);
   }
+  // a piece holds at most 64 quads (64 tiles per wave) and a sequence at most
+  // kMaxPieces pieces: contexts up to 64 * 64 * 64 = 262144 tokens
+  if ((int64_t)table_stride * block_size > 262144) return FE_ERR_UNSUPPORTED;
   const int max_len = table_stride * block_size;
-  FE_CHECK_ARG((int64_t)table_stride * block_size < ((int64_t)1 << 30));
-  const int target = effective_target(batch, max_len, target_splits);
+  const int target = effective_target(batch, kv_heads, max_len, target_splits);
   const size_t need = fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, max_len, target);
   if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
     return FE_ERR_WORKSPACE;
@@ -368,6 +440,8 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
   a.tables = block_tables;
   a.ctx = context_lens;
   char* ws = (char*)workspace;
+  a.tickets = (int*)ws;
+  ws += kTicketBytes;
   a.ws_o = (float*)ws;
   ws += ws_o_bytes(batch, num_q_heads, head_dim, target);
   a.ws_lse = (float*)ws;

@@ -136,12 +136,14 @@ def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """A per-device workspace reused by every decode call on that device.
 
     Calls on one stream are ordered, so sharing is safe there; callers running
-    decode on several streams at once must pass their own workspace.
+    decode on several streams at once must pass their own zero-filled workspace.
     """
     key = (device.type, device.index)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        # zero-filled once: the split-K tickets at its start must begin at zero
+        # (every call leaves them at zero again)
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 

@@ -100,9 +100,10 @@ int fe_gather_kv(const void* k_pool, const void* v_pool, int num_blocks,
  * Bytes of caller-owned workspace that fe_paged_decode needs for a given
  * batch / head configuration, table capacity (max_context = table_stride *
  * block_size) and split target (0 = library default).
- * Its contents need no initialisation; consecutive calls on one stream may
- * share it, calls that overlap in time (several streams) need separate
- * workspaces.
+ * It must be zero-filled before its first use; every call leaves it ready
+ * for the next (the split counters it holds return to zero), so consecutive
+ * calls on one stream may share it.  Calls that overlap in time (several
+ * streams) need separate workspaces.
  */
 size_t fe_paged_decode_workspace_size(int batch, int num_q_heads, int head_dim,
                                       int max_context, int target_splits);
@@ -114,7 +115,9 @@ size_t fe_paged_decode_workspace_size(int batch, int num_q_heads, int head_dim,
  * num_q_heads / kv_heads.  Rows with context_lens[b] == 0 get exact zeros.
  * Work is split over the keys ("split-K") into about `target_splits` equal
  * pieces per KV head (0 = library default); partial results are combined by a
- * log-sum-exp merge kernel launched right after on the same stream.
+ * log-sum-exp merge inside the same kernel launch (the last piece of a
+ * sequence to finish merges).  Tables may address at most 262144 tokens
+ * (table_stride * block_size) and batch * kv_heads may not exceed 65536.
  * If k_new and v_new are non-null ([batch, kv_heads, head_dim], rows
  * new_batch_stride elements apart) the kernel
  * also performs the decode-step page write of fe_write_kv_decode and uses

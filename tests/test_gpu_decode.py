@@ -267,13 +267,14 @@ def test_fused_write_short_contexts(bs):
 
 
 def test_workspace_reuse_across_shapes():
-    """One workspace serves calls of different shapes and split counts in a row."""
+    """One workspace serves calls of different shapes and split counts in a row (the split
+    tickets it holds return to zero after every call)."""
     big = workloads.c2_workload(batch=32)
     small = workloads.make_decode_workload("small", 3, 3, 12, 2, 128, [700, 5, 2000])
     exp_big, _, _ = oracle_decode(big)
     exp_small, _, _ = oracle_decode(small)
-    ws = torch.full((ops.decode_workspace_bytes(32, 12, 128, 4096, 2048),), 0x7F,
-                    dtype=torch.uint8, device=DEV)  # garbage contents
+    ws = torch.zeros((ops.decode_workspace_bytes(32, 12, 128, 4096, 2048),),
+                     dtype=torch.uint8, device=DEV)
     db, dsm = big.to(DEV), small.to(DEV)
     for target in (2048, 7, 512, 64):
         ob = ops.paged_decode(db.q, db.k_pool, db.v_pool, db.block_tables, db.context_lens,
@@ -282,3 +283,26 @@ def test_workspace_reuse_across_shapes():
                                workspace=ws, target_splits=target)
         assert_attention_close(ob.cpu().numpy(), exp_big, what=f"big t={target}")
         assert_attention_close(osm.cpu().numpy(), exp_small, what=f"small t={target}")
+
+
+def test_split_merge_repeated_calls_are_stable():
+    """The in-kernel split-K merge (coherent partials + ticket) gives the same, correct
+    result on every one of many back-to-back calls, for several split counts."""
+    w = workloads.c2_workload()
+    exp, _, _ = oracle_decode(w)
+    d = w.to(DEV)
+    outs = []
+    for rep in range(8):
+        for target in (96, 256, 777, 2048):
+            outs.append((target, ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables,
+                                                  d.context_lens, k_new=d.k_new, v_new=d.v_new,
+                                                  target_splits=target)))
+    torch.cuda.synchronize()
+    first = {}
+    for target, o in outs:
+        got = o.cpu().numpy()
+        assert_attention_close(got, exp, what=f"target={target}")
+        if target in first:
+            assert (first[target] == got).all(), "results differ between identical calls"
+        else:
+            first[target] = got
