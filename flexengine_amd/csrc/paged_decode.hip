@@ -69,6 +69,9 @@ struct DecodeArgs {
   float scale_log2;  // softmax scale * log2(e)
 };
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kSc1 = 16;  // buffer-instruction cache policy: sc1 (device-coherent)
+
 __device__ __forceinline__ void store_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -80,72 +83,68 @@ __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)
 
 // Combines the ns pieces (ids first .. first+ns-1) of sequence b, KV head h:
 // per query head, out = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
-// Each thread owns up to kMergePer output elements; the partial outputs of up
-// to kMergeBatch pieces are requested together with the LSEs, so the common
-// case (ns <= kMergeBatch) costs a single round trip to memory.
+// Each thread owns up to kMergePer output elements and computes their weights
+// itself from the LSEs it loads alongside the partial outputs; pieces are taken
+// kMergeBatch at a time with an online max, so the common case (ns <=
+// kMergeBatch) is one round trip to memory and no barrier.
 constexpr int kMergeBatch = 16;
-constexpr int kMergePer = 3;  // ceil(G*D / 256) for G*D <= 768 (G 6, D 128)
+constexpr int kMergePer = 3;
 
 template <int D>
-__device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, int first, int ns,
-                                             unsigned char* smem) {
+__device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, int first,
+                                             int ns) {
   const int G = a.G;
   const int GD = G * D;
-  float* wts = reinterpret_cast<float*>(smem);  // [ns][G] LSEs -> weights, then [G] 1/den
-  float* inv = wts + ns * G;
-  const int64_t step = (int64_t)a.Hq * D;
-  const float* base = a.ws_o + ((int64_t)first * a.Hq + h * G) * D;
-  __syncthreads();  // LDS reuse: the wave merge above is done with it
+  const float* lse_base = a.ws_lse + (int64_t)first * a.Hq + h * G;
+  const float* o_base = a.ws_o + ((int64_t)first * a.Hq + h * G) * D;
+  const int64_t o_step = (int64_t)a.Hq * D;
   for (int e0 = 0; e0 < GD; e0 += kThreads * kMergePer) {
-    float acc[kMergePer];
+    float M[kMergePer], num[kMergePer], den[kMergePer];
 #pragma unroll
-    for (int r = 0; r < kMergePer; ++r) acc[r] = 0.f;
+    for (int r = 0; r < kMergePer; ++r) {
+      M[r] = kNegInf;
+      num[r] = 0.f;
+      den[r] = 0.f;
+    }
     for (int s0 = 0; s0 < ns; s0 += kMergeBatch) {
-      // requests: this batch's partial outputs, and (first batch) every LSE
-      float v[kMergePer][kMergeBatch];
+      float lv[kMergePer][kMergeBatch], ov[kMergePer][kMergeBatch];
 #pragma unroll
       for (int r = 0; r < kMergePer; ++r) {
-        const int e = e0 + r * kThreads + (int)threadIdx.x;
+        int e = e0 + r * kThreads + (int)threadIdx.x;
+        e = e < GD ? e : GD - 1;
+        const int hh = e / D;
 #pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u)
-          v[r][u] = (e < GD && s0 + u < ns) ? load_coherent(base + (s0 + u) * step + e) : 0.f;
-      }
-      if (s0 == 0) {
-        for (int i = threadIdx.x; i < ns * G; i += kThreads) {
-          const int s = i / G, hh = i - s * G;
-          wts[i] = load_coherent(a.ws_lse + (int64_t)(first + s) * a.Hq + h * G + hh);
+        for (int u = 0; u < kMergeBatch; ++u) {
+          const int sidx = s0 + u < ns ? s0 + u : ns - 1;  // clamped: always a written slot
+          lv[r][u] = load_coherent(lse_base + (int64_t)sidx * a.Hq + hh);
+          ov[r][u] = load_coherent(o_base + sidx * o_step + e);
         }
-        __syncthreads();
-        if (threadIdx.x < G) {
-          const int hh = threadIdx.x;
-          float M = kNegInf;
-          for (int s = 0; s < ns; ++s) M = fmaxf(M, wts[s * G + hh]);
-          float den = 0.f;
-          for (int s = 0; s < ns; ++s) {
-            const float wv = exp2f(wts[s * G + hh] - M);
-            wts[s * G + hh] = wv;
-            den += wv;
-          }
-          inv[hh] = 1.f / den;
-        }
-        __syncthreads();
       }
 #pragma unroll
       for (int r = 0; r < kMergePer; ++r) {
-        const int e = e0 + r * kThreads + (int)threadIdx.x;
-        const int hh = (e < GD ? e : 0) / D;
+        float bm = kNegInf;
 #pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u)
-          if (s0 + u < ns) acc[r] += wts[(s0 + u) * G + hh] * v[r][u];
+        for (int u = 0; u < kMergeBatch; ++u) {
+          if (s0 + u >= ns) lv[r][u] = kNegInf;
+          bm = fmaxf(bm, lv[r][u]);
+        }
+        const float newM = fmaxf(M[r], bm);
+        const float alpha = M[r] == kNegInf ? 0.f : exp2f(M[r] - newM);
+        num[r] *= alpha;
+        den[r] *= alpha;
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+          const float wv = lv[r][u] == kNegInf ? 0.f : exp2f(lv[r][u] - newM);
+          num[r] += wv * ov[r][u];
+          den[r] += wv;
+        }
+        M[r] = newM;
       }
     }
 #pragma unroll
     for (int r = 0; r < kMergePer; ++r) {
       const int e = e0 + r * kThreads + (int)threadIdx.x;
-      if (e < GD) {
-        const int hh = e / D;
-        a.out[((int64_t)b * a.Hq + h * G) * D + e] = (f16)(acc[r] * inv[hh]);
-      }
+      if (e < GD) a.out[((int64_t)b * a.Hq + h * G) * D + e] = (f16)(num[r] / den[r]);
     }
   }
 }
@@ -177,7 +176,7 @@ __device__ __forceinline__ void setup_core(Core& core, const DecodeArgs& a, cons
 
 template <int D, bool PAGE16>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(FE_DECODE_WAVES_PER_EU, 8)))
+__attribute__((amdgpu_waves_per_eu(PAGE16 ? FE_DECODE_WAVES_PER_EU : 2, 8)))
 void paged_decode_kernel(const DecodeArgs a) {
   using C = TileCfg<D>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -251,58 +250,75 @@ void paged_decode_kernel(const DecodeArgs a) {
     for (int x = 0; x < C::NX; ++x) o[x] = core.o[x];
   }
 
-  // ---- combine the four waves through LDS ----
-  float* mO = reinterpret_cast<float*>(smem + kWaves * C::STAGE);  // [4][G][D]
-  float* mM = mO + kWaves * G * D;                                 // [4][16]
-  float* mL = mM + kWaves * kMaxGroup;                             // [4][16]
-  int* flag = reinterpret_cast<int*>(mL + kWaves * kMaxGroup);
-  if (n < G) {
+  // ---- combine the four waves: waves 1..3 park their state in LDS (lane-major,
+  // conflict-free), wave 0 combines in its own register layout: lane (g, n)
+  // holds O[head n][16x + 4g + i], so the per-head scale factors are per lane.
+  f32x4* park = reinterpret_cast<f32x4*>(smem + kWaves * C::STAGE);  // [3][NX][64]
+  float* park_m = reinterpret_cast<float*>(park + (kWaves - 1) * C::NX * kWave);
+  float* park_l = park_m + (kWaves - 1) * kWave;
+  int* flag = reinterpret_cast<int*>(park_l + (kWaves - 1) * kWave);
+  if (w > 0) {
 #pragma unroll
-    for (int x = 0; x < C::NX; ++x)
-      *reinterpret_cast<f32x4*>(mO + (w * G + n) * D + 16 * x + 4 * g) = o[x];
-    if (g == 0) {
-      mM[w * kMaxGroup + n] = m_run;
-      mL[w * kMaxGroup + n] = l_tot;
-    }
+    for (int x = 0; x < C::NX; ++x) park[((w - 1) * C::NX + x) * kWave + lane] = o[x];
+    park_m[(w - 1) * kWave + lane] = m_run;
+    park_l[(w - 1) * kWave + lane] = l_tot;
   }
   __syncthreads();
   const bool split = pc.nsplit > 1;
-  for (int e = threadIdx.x; e < G * D; e += kThreads) {
-    const int hh = e / D;
-    const int d = e - hh * D;
-    float M = kNegInf;
+  if (w == 0) {
+    float M = m_run;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, mM[ww * kMaxGroup + hh]);
-    float num = 0.f, den = 0.f;
+    for (int v = 0; v < kWaves - 1; ++v) M = fmaxf(M, park_m[v * kWave + lane]);
+    const float sc0 = m_run == kNegInf ? 0.f : exp2f(m_run - M);
+    float den = sc0 * l_tot;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) {
-      const float mw = mM[ww * kMaxGroup + hh];
-      const float sc = mw == kNegInf ? 0.f : exp2f(mw - M);
-      num += sc * mO[(ww * G + hh) * D + d];
-      den += sc * mL[ww * kMaxGroup + hh];
+    for (int x = 0; x < C::NX; ++x) o[x] *= sc0;
+#pragma unroll
+    for (int v = 0; v < kWaves - 1; ++v) {
+      const float mv = park_m[v * kWave + lane];
+      const float sc = mv == kNegInf ? 0.f : exp2f(mv - M);
+      den += sc * park_l[v * kWave + lane];
+#pragma unroll
+      for (int x = 0; x < C::NX; ++x) o[x] += sc * park[(v * C::NX + x) * kWave + lane];
     }
-    const float res = num / den;
-    const int hq = h * G + hh;
-    if (!split) {
-      a.out[((int64_t)b * a.Hq + hq) * D + d] = (f16)res;
-    } else {
-      store_coherent(a.ws_o + ((int64_t)item * a.Hq + hq) * D + d, res);
-      if (d == 0) store_coherent(a.ws_lse + (int64_t)item * a.Hq + hq, M + log2f(den));
+    const float inv = 1.f / den;
+    if (n < G) {
+      const int hq = h * G + n;
+      if (!split) {
+        f16* orow = a.out + ((int64_t)b * a.Hq + hq) * D + 4 * g;
+#pragma unroll
+        for (int x = 0; x < C::NX; ++x)
+          *reinterpret_cast<f16x4*>(orow + 16 * x) =
+              f16x4{(f16)(o[x][0] * inv), (f16)(o[x][1] * inv), (f16)(o[x][2] * inv),
+                    (f16)(o[x][3] * inv)};
+      } else {
+        // device-coherent (sc1) 16-byte stores of this piece's partial output
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            a.ws_o + ((int64_t)item * a.Hq + h * G) * D, 0, G * D * (int)sizeof(float),
+            0x00020000);
+        const uint32_t off = (uint32_t)((n * D + 4 * g) * sizeof(float));
+#pragma unroll
+        for (int x = 0; x < C::NX; ++x)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[x] * inv), r,
+                                                 off + 16 * x * sizeof(float), 0, kSc1);
+        if (g == 0) store_coherent(a.ws_lse + (int64_t)item * a.Hq + hq, M + log2f(den));
+      }
     }
   }
   if (!split) return;
 
   // ---- split-K: the last piece of (b, h) to finish merges all pieces ----
-  wait_stores();  // this thread's partials are complete at the device-coherent level
-  __syncthreads();
-  int* ticket = a.tickets + b * a.Hkv + h;
-  if (threadIdx.x == 0)
-    *flag = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            pc.nsplit - 1;
+  if (w == 0) {
+    wait_stores();  // this piece's partials are complete at the device-coherent level
+    if (lane == 0)
+      *flag = __hip_atomic_fetch_add(a.tickets + b * a.Hkv + h, 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == pc.nsplit - 1;
+  }
   __syncthreads();
   if (!*flag) return;
-  if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  merge_pieces<D>(a, b, h, item - pc.split, pc.nsplit, smem);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.tickets + b * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  merge_pieces<D>(a, b, h, item - pc.split, pc.nsplit);
 }
 
 // General LSE merge of S partial results (natural-log LSE at the boundary).
@@ -362,12 +378,10 @@ inline int effective_target(int batch, int kv_heads, int max_context, int target
 }
 
 template <int D>
-size_t decode_lds_bytes(int G) {
-  const size_t waves = (size_t)kWaves * TileCfg<D>::STAGE + (size_t)kWaves * G * D * sizeof(float) +
-                       2 * kWaves * kMaxGroup * sizeof(float) + 16;
-  // merge_pieces: kMaxPieces x G weights + G inverses
-  const size_t merge = (size_t)(kMaxPieces + 1) * G * sizeof(float);
-  return waves > merge ? waves : merge;
+size_t decode_lds_bytes(int /*G*/) {
+  // V staging of the four waves, then the parked state of waves 1..3 and a flag
+  return (size_t)kWaves * TileCfg<D>::STAGE +
+         (size_t)(kWaves - 1) * (TileCfg<D>::NX * kWave * 16 + 2 * kWave * sizeof(float)) + 16;
 }
 
 template <int D>
