@@ -227,7 +227,7 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "paged_decode_kernel<128, true> (fe_paged_decode: page write + split-K "
+            "kernel": "piece_decode_kernel<128, true> (fe_paged_decode: page write + split-K "
                       "attention + in-kernel LSE merge, one launch)",
             "us_per_launch": round(per_launch_ms * 1e3, 3),
         },

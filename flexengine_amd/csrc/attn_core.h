@@ -32,11 +32,12 @@ struct TileCfg {
   static constexpr int NX = D / 16;       // PV output tiles of 16 dims
   static constexpr int CPR = D / 8;       // 16-byte chunks per K/V row
   static constexpr int RPI = kWave / CPR; // V rows covered by one load instruction
-  // LDS pitch of a staged V row: D halves + 8 bytes = D/2 + 2 dwords, which is
-  // 2 mod 32 for D = 64 and 128.  Row r then starts at bank 2r mod 32, so the
-  // four rows 4g+i (g = 0..3) that one column read touches start at banks
-  // 8g + 2i and their 8-dword spans are disjoint: no bank conflicts.
-  static constexpr int ROWB = D * 2 + 8;
+  // LDS pitch of a staged V row: D halves + 32 bytes = D/2 + 8 dwords, which is
+  // 8 mod 32 for D = 64 and 128.  The transposing read of a 16-dim slice (see
+  // softmax_pv_tile) has each 16-lane group fetch 8 bytes from 4 rows x 4
+  // consecutive 8-byte columns; rows 8 dwords apart put those 16 fetches on
+  // distinct bank pairs.
+  static constexpr int ROWB = D * 2 + 32;
   static constexpr int STAGE = kTile * ROWB;
 };
 
@@ -46,9 +47,24 @@ __device__ __forceinline__ int clamp_block(int blk, int nb) {
 
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
+// Running-max slack of the online softmax, in base-2 units: the max a tile's
+// scores are exponentiated against is only raised when some column's tile max
+// exceeds it by more than this, so most tiles skip the rescale of o and l, and
+// every probability stays <= 2^kRescaleSlack (exact in fp16 for the PV MFMA).
+constexpr float kRescaleSlack = 8.f;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
 // Shared softmax + PV step of one 16-key tile (scores already in sacc).
 // Lane (g,n): sacc[i] = raw score of key t0 + 4g + i for column n; keys at or
 // past `limit` are masked.  V rows of the tile are in `stage` (row pitch ROWB).
+//
+// The PV product O^T[16 dims x 16 cols] += V^T . P^T takes its A operand
+// (lane (g,n): V[key 4g+i][dim 16x+n], i = 0..3) from one transposing LDS read
+// per 16-dim slice: ds_read_b64_tr_b16 returns to lane l of a 16-lane group
+// the halves M[4j + l/4][l%4] (j = 0..3), M[r] being the 8 bytes addressed by
+// lane r of the group; lane (g, r) therefore addresses
+// V[key 4g + r/4][dims 16x + 4(r%4) .. +3].
 template <int D>
 __device__ __forceinline__ void softmax_pv_tile(f32x4 sacc, int t0, int limit, float scale_log2,
                                                 const unsigned char* stage, float& m_run,
@@ -66,23 +82,26 @@ __device__ __forceinline__ void softmax_pv_tile(f32x4 sacc, int t0, int limit, f
   float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
   mx = fmaxf(mx, shfl_xor_f(mx, 16));
   mx = fmaxf(mx, shfl_xor_f(mx, 32));
-  const float m_new = fmaxf(m_run, mx);
-  const float m_use = m_new == kNegInf ? 0.f : m_new;
-  const float alpha = exp2f(m_run - m_use);
+  if (__ballot(mx > m_run + kRescaleSlack)) {  // wave-uniform
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = m_new == kNegInf ? 1.f : exp2f(m_run - m_new);
+    l_run *= alpha;
+#pragma unroll
+    for (int x = 0; x < C::NX; ++x) o[x] *= alpha;
+    m_run = m_new;
+  }
+  const float m_use = m_run == kNegInf ? 0.f : m_run;
   float p[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = exp2f(sv[i] - m_use);
-  l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-  m_run = m_new;
+  l_run += (p[0] + p[1]) + (p[2] + p[3]);
   const f16x4 pb = {(f16)p[0], (f16)p[1], (f16)p[2], (f16)p[3]};
+  const unsigned char* vb = stage + (4 * g + (n >> 2)) * C::ROWB + (n & 3) * 8;
 #pragma unroll
   for (int x = 0; x < C::NX; ++x) {
-    o[x] *= alpha;
-    f16x4 va;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      va[i] = *reinterpret_cast<const f16*>(stage + (4 * g + i) * C::ROWB + (16 * x + n) * 2);
-    o[x] = mfma16(va, pb, o[x]);
+    const s16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(vb + 32 * x));
+    o[x] = mfma16(__builtin_bit_cast(f16x4, raw), pb, o[x]);
   }
 }
 
@@ -182,9 +201,7 @@ struct TileCore {
       for (int j = 0; j < C::NK; ++j) {
         const int r = j * C::RPI + lane / C::CPR;
         unsigned char* dst = stage + r * C::ROWB + cv * 16;
-        const uint4 bits = *reinterpret_cast<const uint4*>(&vv[j]);
-        *reinterpret_cast<uint2*>(dst) = uint2{bits.x, bits.y};
-        *reinterpret_cast<uint2*>(dst + 8) = uint2{bits.z, bits.w};
+        *reinterpret_cast<f16x8*>(dst) = vv[j];  // ROWB is a multiple of 16
       }
     }
     compiler_fence();
@@ -216,38 +233,34 @@ struct TileCore {
 };
 
 // Fast path for block sizes that are multiples of 16: the 16 keys of a tile
-// share one physical block, so the block id and the row base are wave-uniform
-// (scalar registers) and each lane only carries a 32-bit offset.  The block
-// ids of all of a wave's tiles are fetched with one vector load before the
-// first tile, so no table access sits between two tiles' K/V loads.
+// share one physical block, so a tile is fully described by wave-uniform
+// values -- the pool row of its first key and its key count.  The wave's tiles
+// form a list held one per lane (lane k: tile k, k < 64), filled from the block
+// tables before the first load, so no table access sits between two tiles'
+// K/V loads.  Consecutive tiles may belong to different sequences: the caller
+// sees every tile end and flushes / resets the accumulators at a sequence
+// boundary (see run()).
 template <int D>
-struct Page16Core {
+struct TileListCore {
   using C = TileCfg<D>;
 
   const f16* k_pool;
   const f16* v_pool;
   f16* k_pool_w;          // writable aliases for the fused page write
   f16* v_pool_w;
-  const int32_t* trow;
   int rs;                 // elements per pool row (kv_heads * D)
   int hoff;               // kv_head * D
-  int W, NB, BS, bs_log2;
-  int tok_end;
-  int limit;
   float scale_log2;
-  const f16* knew_row;
-  const f16* vnew_row;
-  int new_pos;
-  unsigned char* stage;
+  unsigned char* stage;   // per-wave LDS tile, C::STAGE bytes
 
   f16x8 qv[C::NK];
   float m_run;
   float l_run;
   f32x4 o[C::NX];
 
-  int t_first;            // first tile of this wave
-  int step;               // tile stride (waves per workgroup)
-  int blk_vec;            // lane k: physical block of tile t_first + k*step (k < 64)
+  int ntiles;             // tiles in the list (<= 64)
+  int row_vec;            // lane k < ntiles: pool row (block * BS + offset) of tile k's first key
+  int rows_vec;           // lane k < ntiles: keys in tile k (1..16)
 
   __device__ __forceinline__ void init_acc() {
     m_run = kNegInf;
@@ -256,32 +269,20 @@ struct Page16Core {
     for (int x = 0; x < C::NX; ++x) o[x] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Lane k (< ntiles <= 64) fetches the physical block of tile k; other lanes 0.
-  __device__ __forceinline__ void fetch_blocks(int ntiles) {
-    const int k = lane_id();
-    int blk = 0;
-    if (k < ntiles) {
-      int page = ((t_first + k * step) * kTile) >> bs_log2;
-      page = page < W ? page : W - 1;
-      blk = clamp_block(trow[page], NB);
-    }
-    blk_vec = blk;
-  }
-
-  // Row base (element offset of row 0 of the tile, kv head included), uniform.
+  // Element offset of row 0 of tile k (kv head included); wave-uniform.
   __device__ __forceinline__ int64_t tile_base(int k) const {
-    const int t0 = (t_first + k * step) * kTile;
-    const int blk = __builtin_amdgcn_readlane(blk_vec, k & (kWave - 1));
-    return ((int64_t)blk * BS + (t0 & (BS - 1))) * rs + hoff;
+    return (int64_t)__builtin_amdgcn_readlane(row_vec, k & (kWave - 1)) * rs + hoff;
   }
-
-  __device__ __forceinline__ int tile_t0(int k) const { return (t_first + k * step) * kTile; }
+  // Keys of tile k; 0 past the end of the list.
+  __device__ __forceinline__ int tile_rows(int k) const {
+    const int r = __builtin_amdgcn_readlane(rows_vec, k & (kWave - 1));
+    return k < ntiles ? r : 0;
+  }
 
   // Tile loads are raw buffer loads: a scalar descriptor per tile (base = row
-  // 0 of the tile for this KV head, extent = rows still inside the piece) and
-  // a loop-invariant 32-bit byte offset per lane.  Rows past the piece fall
-  // outside the descriptor's range and read as zeros, so stale pool contents
-  // beyond the context never reach the accumulators.
+  // 0 of the tile for this KV head, extent = the tile's keys) and a
+  // loop-invariant 32-bit byte offset per lane.  Rows past the extent read as
+  // zeros, so stale pool contents beyond a context never reach the accumulators.
   __device__ __forceinline__ uint32_t k_off0() const {
     const int lane = lane_id();
     return (uint32_t)(((lane & 15) * rs + (lane >> 4) * 8) * 2);
@@ -311,11 +312,11 @@ struct Page16Core {
     return __builtin_amdgcn_make_buffer_rsrc(p, 0, nrec, 0x00020000);
   }
 
-  // Issues the K/V loads of tile k; nothing here waits for data.
+  // Issues the K/V loads of tile k; nothing here waits for data.  Past the end
+  // of the list the descriptors have zero extent and touch no memory.
   __device__ __forceinline__ void load_tile(int k, f16x8 (&kk)[C::NK], f16x8 (&vv)[C::NK]) const {
     const int64_t base = tile_base(k);
-    const int rem = tok_end - tile_t0(k);
-    const int rows = rem < 0 ? 0 : (rem < kTile ? rem : kTile);
+    const int rows = tile_rows(k);
     const __amdgpu_buffer_rsrc_t kr = tile_rsrc(k_pool, base, rows);
     const __amdgpu_buffer_rsrc_t vr = tile_rsrc(v_pool, base, rows);
     const uint32_t ko = k_off0();
@@ -326,16 +327,15 @@ struct Page16Core {
     for (int j = 0; j < C::NK; ++j) vv[j] = buf_ld16(vr, vo, v_soff(j));
   }
 
-  // Fused page write of the decoded token (position new_pos, inside this
-  // wave's tile k): each lane that will load a 16-byte chunk of that row first
-  // stores the new chunk to the same address, so its later load (same thread,
-  // same address, program order) returns the new bytes.  Issued right after the
-  // block-id fetch, whose latency the k_new / v_new loads overlap.
-  __device__ __forceinline__ void write_new_row(int k) const {
+  // Fused page write of a decoded token (row r of tile k): each lane that will
+  // load a 16-byte chunk of that row first stores the new chunk to the same
+  // address, so its later load (same thread, same address, program order)
+  // returns the new bytes.
+  __device__ __forceinline__ void write_new_row(int k, int r, const f16* knew_row,
+                                                const f16* vnew_row) const {
     const int lane = lane_id();
     const int g = lane >> 4;
     const int n = lane & 15;
-    const int r = new_pos - tile_t0(k);
     const int64_t base = tile_base(k);
     char* kb = reinterpret_cast<char*>(k_pool_w + base);
     char* vb = reinterpret_cast<char*>(v_pool_w + base);
@@ -358,7 +358,6 @@ struct Page16Core {
   __device__ __forceinline__ void compute_tile(int k, const f16x8 (&kk)[C::NK],
                                                f16x8 (&vv)[C::NK]) {
     const int lane = lane_id();
-    const int t0 = tile_t0(k);
     const int vrow = lane / C::CPR;
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -373,42 +372,44 @@ struct Page16Core {
       for (int j = 0; j < C::NK; ++j) {
         const int r = j * C::RPI + vrow;
         unsigned char* dst = stage + r * C::ROWB + cv * 16;
-        const uint4 bits = *reinterpret_cast<const uint4*>(&vv[j]);
-        *reinterpret_cast<uint2*>(dst) = uint2{bits.x, bits.y};
-        *reinterpret_cast<uint2*>(dst + 8) = uint2{bits.z, bits.w};
+        *reinterpret_cast<f16x8*>(dst) = vv[j];  // ROWB is a multiple of 16
       }
     }
     compiler_fence();
-    softmax_pv_tile<D>(sacc, t0, limit, scale_log2, stage, m_run, l_run, o);
+    softmax_pv_tile<D>(sacc, 0, tile_rows(k), scale_log2, stage, m_run, l_run, o);
     compiler_fence();
   }
 
-  // All tiles t_first + k*step < t_end (at most 64 per wave: the host bounds
-  // the piece size).  NSTAGE register stages: while tile k is computed, the
+  // Walks the list with NSTAGE register stages: while tile k is computed, the
   // loads of tiles k+1 .. k+NSTAGE-1 are in flight.  Loads are issued
-  // unconditionally (tiles past the end have a zero-extent descriptor and touch
-  // no memory), so the loop has no join points and every wait is exact.
+  // unconditionally (zero-extent past the end), so the loop has no join points
+  // and every wait is exact.  After each tile, tile_end(k) runs; it returns
+  // false to stop (it must at k == ntiles - 1).  The prologue loads of the
+  // first NSTAGE-1 tiles are issued by prologue() so the caller can place
+  // other work between them and the loop.
   template <int NSTAGE>
-  __device__ __forceinline__ void run(int t_end) {
-    static_assert(NSTAGE >= 2, "need at least two register stages");
-    const int ntiles = t_first < t_end ? (t_end - t_first + step - 1) / step : 0;
-    if (ntiles == 0) return;
-    fetch_blocks(ntiles);
-    if (new_pos >= 0) {
-      // tile index (within this wave) holding the decoded token, if any
-      const int tn = new_pos / kTile - t_first;
-      if (tn >= 0 && tn % step == 0 && tn / step < ntiles) write_new_row(tn / step);
-    }
-    f16x8 kbuf[NSTAGE][C::NK], vbuf[NSTAGE][C::NK];
+  struct Buffers {
+    f16x8 k[NSTAGE][C::NK];
+    f16x8 v[NSTAGE][C::NK];
+  };
+
+  template <int NSTAGE>
+  __device__ __forceinline__ void prologue(Buffers<NSTAGE>& buf) const {
 #pragma unroll
-    for (int u = 0; u < NSTAGE - 1; ++u) load_tile(u, kbuf[u], vbuf[u]);
+    for (int u = 0; u < NSTAGE - 1; ++u) load_tile(u, buf.k[u], buf.v[u]);
+  }
+
+  template <int NSTAGE, class TileEnd>
+  __device__ __forceinline__ void run(Buffers<NSTAGE>& buf, TileEnd& tile_end) {
+    static_assert(NSTAGE >= 2, "need at least two register stages");
     int k = 0;
     while (true) {
 #pragma unroll
       for (int u = 0; u < NSTAGE; ++u) {
-        load_tile(k + NSTAGE - 1, kbuf[(u + NSTAGE - 1) % NSTAGE], vbuf[(u + NSTAGE - 1) % NSTAGE]);
-        compute_tile(k, kbuf[u], vbuf[u]);
-        if (++k >= ntiles) return;
+        load_tile(k + NSTAGE - 1, buf.k[(u + NSTAGE - 1) % NSTAGE], buf.v[(u + NSTAGE - 1) % NSTAGE]);
+        compute_tile(k, buf.k[u], buf.v[u]);
+        if (!tile_end(*this, k)) return;
+        ++k;
       }
     }
   }
