@@ -1,0 +1,205 @@
+"""A Qwen2 decoder that runs its attention on the HIP paged-attention kernels.
+
+The caller side of the hot path: the two forwards of FlexEngine's
+Qwen2Adapter (src/flexengine/inference/models/qwen2.py) with the same
+semantics, on this package's kernels and random-initialised weights (there is
+no network for checkpoints).
+
+* forward(chunks, cache) -- the ragged mixed batch of qwen2.py:79-136: every
+  chunk (request_id, input_ids, start) is a run of tokens at absolute
+  positions start..start+n-1; per layer the new K/V rows are written to the
+  paged pool *before* attention, and attention is causal per request.  All
+  chunks' K/V go through one fe_write_kv launch and all chunks' attention
+  through one fe_prefill_paged launch (the reference loops over requests).
+  Returns the last-token logits of each chunk.
+* decode_static(input_ids, positions, block_tables, active_mask, cache) -- the
+  graph-compatible one-token step of qwen2.py:138-186 over fixed padded batch
+  tensors; per layer the page write of the new token and the attention run in
+  one fe_paged_decode launch.  Inactive rows leave the pool untouched and give
+  zero logits.
+
+RoPE follows qwen2.py:15-17,46,73-77: inv_freq = theta^(-2i/D), the half-split
+rotate_half, cos/sin cast to the activation dtype.  RMSNorm computes in fp32
+and casts back before the weight, like transformers' Qwen2RMSNorm.  The
+projections and the MLP are plain library GEMMs (hipBLASLt via torch).
+Default configuration: Qwen2.5-1.5B (28 layers, hidden 1536, 12/2 heads,
+head_dim 128, intermediate 8960, vocab 151936, tied embeddings, q/k/v bias,
+RMS eps 1e-6, theta 1e6).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from flexengine_amd import attention, ops
+
+
+@dataclass
+class Qwen2Config:
+    vocab_size: int = 151936
+    hidden_size: int = 1536
+    intermediate_size: int = 8960
+    num_hidden_layers: int = 28
+    num_attention_heads: int = 12
+    num_key_value_heads: int = 2
+    head_dim: int = 128
+    rope_theta: float = 1000000.0
+    rms_norm_eps: float = 1e-6
+    tie_word_embeddings: bool = True
+
+    @property
+    def parameters(self) -> int:
+        h, i, d = self.hidden_size, self.intermediate_size, self.head_dim
+        qkv = h * (self.num_attention_heads + 2 * self.num_key_value_heads) * d
+        qkv += (self.num_attention_heads + 2 * self.num_key_value_heads) * d
+        per_layer = qkv + self.num_attention_heads * d * h + 3 * h * i + 2 * h
+        head = 0 if self.tie_word_embeddings else self.vocab_size * h
+        return self.vocab_size * h + self.num_hidden_layers * per_layer + h + head
+
+
+@dataclass
+class Chunk:
+    """A run of new tokens of one request (engine/scheduler/policies.py:15-18)."""
+    request_id: str
+    input_ids: list[int]
+    start: int
+
+
+class _Layer:
+    def __init__(self, cfg: Qwen2Config, dev, dtype, gen, std):
+        h, i, d = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+        nqkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * d
+
+        def randn(*shape):
+            return (torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dtype)
+
+        self.input_norm = torch.ones(h, device=dev, dtype=dtype)
+        self.post_norm = torch.ones(h, device=dev, dtype=dtype)
+        # q, k and v projections stacked into one GEMM: rows [q | k | v]
+        self.w_qkv = randn(nqkv, h)
+        self.b_qkv = randn(nqkv)
+        self.w_o = randn(h, cfg.num_attention_heads * d)
+        # gate and up stacked into one GEMM: rows [gate | up]
+        self.w_gate_up = randn(2 * i, h)
+        self.w_down = randn(h, i)
+
+
+class Qwen2Model:
+    def __init__(self, cfg: Qwen2Config | None = None, device: str | torch.device = "cuda:0",
+                 dtype=torch.float16, seed: int = 5, std: float = 0.02):
+        self.cfg = cfg = cfg or Qwen2Config()
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError("Qwen2Model runs its attention on the HIP kernels: ROCm GPU only")
+        if cfg.num_attention_heads % cfg.num_key_value_heads:
+            raise ValueError("Invalid GQA head ratio")
+        self.dtype = dtype
+        self.nq, self.nkv, self.dim = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        self.layers = cfg.num_hidden_layers
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(seed)
+        self.embed = (torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen, device=self.device,
+                                  dtype=torch.float32) * std).to(dtype)
+        self.layer_weights = [_Layer(cfg, self.device, dtype, gen, std) for _ in range(self.layers)]
+        self.final_norm = torch.ones(cfg.hidden_size, device=self.device, dtype=dtype)
+        self.lm_head = self.embed if cfg.tie_word_embeddings else (
+            torch.randn((cfg.vocab_size, cfg.hidden_size), generator=gen, device=self.device,
+                        dtype=torch.float32) * std).to(dtype)
+        self.inv_freq = 1.0 / cfg.rope_theta ** (
+            torch.arange(0, self.dim, 2, device=self.device, dtype=torch.float32) / self.dim)
+        self.scale = 1.0 / math.sqrt(self.dim)
+
+    # ---- building blocks ----------------------------------------------------------
+
+    def _norm(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        f = x.float()
+        f = f * torch.rsqrt(f.square().mean(-1, keepdim=True) + self.cfg.rms_norm_eps)
+        return weight * f.to(x.dtype)
+
+    def _rope(self, q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor):
+        """qwen2.py:73-77: x*cos + rotate_half(x)*sin, cos/sin in the activation dtype."""
+        freqs = positions.float().unsqueeze(1) * self.inv_freq.unsqueeze(0)
+        emb = torch.cat([freqs, freqs], dim=-1)
+        cos, sin = emb.cos().to(q.dtype).unsqueeze(1), emb.sin().to(q.dtype).unsqueeze(1)
+        half = self.dim // 2
+
+        def rotate_half(x):
+            return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+        return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+    def _qkv(self, x: torch.Tensor, lw: _Layer, positions: torch.Tensor):
+        n = x.shape[0]
+        h = self._norm(x, lw.input_norm)
+        qkv = F.linear(h, lw.w_qkv, lw.b_qkv)
+        q = qkv[:, :self.nq * self.dim].view(n, self.nq, self.dim)
+        k = qkv[:, self.nq * self.dim:(self.nq + self.nkv) * self.dim].view(n, self.nkv, self.dim)
+        v = qkv[:, (self.nq + self.nkv) * self.dim:].view(n, self.nkv, self.dim)
+        q, k = self._rope(q, k, positions)
+        return q, k, v.contiguous()
+
+    def _mlp_residual(self, x: torch.Tensor, attn: torch.Tensor, lw: _Layer) -> torch.Tensor:
+        x = x + F.linear(attn.reshape(x.shape[0], self.nq * self.dim), lw.w_o)
+        gate_up = F.linear(self._norm(x, lw.post_norm), lw.w_gate_up)
+        inter = self.cfg.intermediate_size
+        return x + F.linear(F.silu(gate_up[:, :inter]) * gate_up[:, inter:], lw.w_down)
+
+    # ---- the two forwards ---------------------------------------------------------
+
+    @torch.inference_mode()
+    def forward(self, chunks: list[Chunk], cache) -> list[torch.Tensor]:
+        """Ragged mixed batch (qwen2.py:79-136); returns the last-token logits per chunk."""
+        lengths = [len(c.input_ids) for c in chunks]
+        if not chunks or any(n < 1 for n in lengths):
+            raise ValueError("empty forward chunks")
+        dev = self.device
+        ids = torch.tensor([t for c in chunks for t in c.input_ids], dtype=torch.long).to(dev)
+        pos_list = [p for c in chunks for p in range(c.start, c.start + len(c.input_ids))]
+        positions = torch.tensor(pos_list, dtype=torch.long).to(dev)
+        # slot map of every new token, built once for all layers (allocator.py:107-114)
+        blocks, offsets = [], []
+        for c in chunks:
+            b, o = cache._locators(c.request_id, c.start, len(c.input_ids))
+            if any(cache.refs[blk] > 1 for blk in set(b)):
+                raise RuntimeError("cannot write a shared immutable KV block")
+            blocks += b
+            offsets += o
+        slots = torch.tensor([blocks, offsets], dtype=torch.int32).to(dev)
+        width = max(len(cache.tables[c.request_id]) for c in chunks)
+        tables = cache.block_table([c.request_id for c in chunks], width)
+        q_offsets = torch.tensor([0] + [sum(lengths[:j + 1]) for j in range(len(lengths))],
+                                 dtype=torch.int32).to(dev)
+        ctx = torch.tensor([c.start + n for c, n in zip(chunks, lengths)], dtype=torch.int32).to(dev)
+        max_q = max(lengths)
+        x = self.embed.index_select(0, ids)
+        for layer, lw in enumerate(self.layer_weights):
+            q, k, v = self._qkv(x, lw, positions)
+            ops.write_kv(k, v, cache.k[layer], cache.v[layer], slots[0], slots[1])
+            attn = ops.prefill_paged(q.contiguous(), cache.k[layer], cache.v[layer], tables,
+                                     q_offsets, ctx, max_q, scale=self.scale)
+            x = self._mlp_residual(x, attn, lw)
+        ends = torch.tensor([sum(lengths[:j + 1]) - 1 for j in range(len(lengths))],
+                            dtype=torch.long).to(dev)
+        logits = F.linear(self._norm(x.index_select(0, ends), self.final_norm), self.lm_head)
+        return [logits[j] for j in range(len(lengths))]
+
+    @torch.inference_mode()
+    def decode_static(self, input_ids: torch.Tensor, positions: torch.Tensor,
+                      block_tables: torch.Tensor, active_mask: torch.Tensor, cache) -> torch.Tensor:
+        """Graph-compatible one-token decode over fixed padded batch tensors
+        (qwen2.py:138-186): logits [B, vocab], zero for inactive rows."""
+        batch = input_ids.shape[0]
+        if input_ids.ndim != 1 or positions.shape != (batch,) or active_mask.reshape(-1).shape != (batch,):
+            raise ValueError("invalid static decode inputs")
+        active = active_mask.reshape(-1)
+        x = self.embed.index_select(0, input_ids)
+        for layer, lw in enumerate(self.layer_weights):
+            q, k, v = self._qkv(x, lw, positions)
+            attn = attention.paged_decode_batch(q, cache, layer, block_tables, positions, active,
+                                                k_new=k.contiguous(), v_new=v)
+            x = self._mlp_residual(x, attn, lw)
+        logits = F.linear(self._norm(x, self.final_norm), self.lm_head)
+        return logits * active.to(logits.dtype)[:, None]

@@ -158,3 +158,36 @@ def test_c3_prefix_sharing_structure():
     t = w.block_tables
     assert torch.equal(t[0, :128], t[3, :128]) and not torch.equal(t[0, :128], t[4, :128])
     assert w.unique_tokens < int(w.context_lens.sum())
+
+
+def test_qwen25_15b_parameter_count():
+    from flexengine_amd.model import Qwen2Config
+    # 1.5437 B parameters with tied embeddings (public model card)
+    assert abs(Qwen2Config().parameters - 1.5437e9) / 1.5437e9 < 0.005
+
+
+def test_model_requires_gpu():
+    from flexengine_amd.model import Qwen2Config, Qwen2Model
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        Qwen2Model(Qwen2Config(num_hidden_layers=1, vocab_size=16), device="cpu")
+
+
+def test_graph_inputs_pad_rows_with_scratch_blocks():
+    """runtime.py:201-213: padded rows point at scratch blocks; active rows carry
+    token, position and table."""
+    from flexengine_amd.decode_step import SCRATCH_ID, GraphDecodeStep
+    from flexengine_amd.model import Chunk
+    cache = PagedKVCache(CacheLayout(1, 40, 4, 2, 8), device="cpu")
+    cache.reserve("a", 6)
+    step = GraphDecodeStep(model=None, cache=cache, max_model_len=16)
+    assert len(cache.tables[SCRATCH_ID]) == 8 * 4 // 4
+    inp = step.graph_inputs([Chunk("a", [42], 5)], 4)
+    assert inp["input_ids"].tolist() == [42, 0, 0, 0]
+    assert inp["positions"].tolist() == [5, 0, 0, 0]
+    table = cache.tables["a"]
+    assert inp["block_tables"][0, :2].tolist() == table
+    assert inp["block_tables"][0, 2:].tolist() == [step.scratch_blocks[0]] * 2
+    for row in range(1, 4):
+        assert inp["block_tables"][row].tolist() == [step.scratch_blocks[row]] * 4
+    with pytest.raises(ValueError):
+        step.graph_inputs([Chunk("a", [1], 0)] * 5, 4)
