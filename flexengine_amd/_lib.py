@@ -1,4 +1,5 @@
-"""ctypes binding of libfe_paged.so, the C ABI declared in include/flexengine_amd.h.
+"""ctypes binding of libfe_paged.so, the C ABI declared in include/flexengine_amd.h and
+include/flexengine_amd_model.h.
 
 There is no fallback: if the library is missing, or no ROCm GPU is present when
 a kernel is called, the call raises RuntimeError.
@@ -38,6 +39,12 @@ SIGNATURES: dict[str, tuple] = {
     "fe_lse_merge": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),
     "fe_prefill_paged": (_i, [_p, _p, _p, _p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _i,
                               _f, _p]),
+    # include/flexengine_amd_model.h
+    "fe_rmsnorm": (_i, [_p, _i, _p, _p, _p, _p, _i, _i, _f, _p]),
+    "fe_rope_qkv": (_i, [_p, _i64, _i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "fe_silu_mul": (_i, [_p, _i64, _i, _p, _i, _i, _p]),
+    "fe_gemm_skinny_splits": (_i, [_i, _i]),
+    "fe_gemm_skinny": (_i, [_p, _i, _i, _p, _i, _p, _i, _p]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -4,7 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "flexengine_amd.h"
+#include "flexengine_amd_model.h"
 
 namespace fe {
 

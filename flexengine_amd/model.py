@@ -20,8 +20,10 @@ no network for checkpoints).
 
 RoPE follows qwen2.py:15-17,46,73-77: inv_freq = theta^(-2i/D), the half-split
 rotate_half, cos/sin cast to the activation dtype.  RMSNorm computes in fp32
-and casts back before the weight, like transformers' Qwen2RMSNorm.  The
-projections and the MLP are plain library GEMMs (hipBLASLt via torch).
+and casts back before the weight, like transformers' Qwen2RMSNorm.  Both, the
+residual adds and the SiLU product run as fused HIP kernels
+(include/flexengine_amd_model.h); the projections run on the skinny HIP GEMM
+for decode-sized batches and on the library GEMM (hipBLASLt via torch) above.
 Default configuration: Qwen2.5-1.5B (28 layers, hidden 1536, 12/2 heads,
 head_dim 128, intermediate 8960, vocab 151936, tied embeddings, q/k/v bias,
 RMS eps 1e-6, theta 1e6).
@@ -32,7 +34,6 @@ import math
 from dataclasses import dataclass
 
 import torch
-import torch.nn.functional as F
 
 from flexengine_amd import attention, ops
 
@@ -113,39 +114,35 @@ class Qwen2Model:
         self.scale = 1.0 / math.sqrt(self.dim)
 
     # ---- building blocks ----------------------------------------------------------
+    # Per layer: fused add + RMSNorm, the q/k/v GEMM, RoPE + split, attention, the o
+    # GEMM, add + RMSNorm, the gate/up GEMM, SiLU product, the down GEMM.  GEMMs of
+    # up to ops.SKINNY_MAX_ROWS rows run on the skinny HIP GEMM, whose fp32 partials
+    # the next kernel sums; larger ones on the library GEMM.
 
-    def _norm(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-        f = x.float()
-        f = f * torch.rsqrt(f.square().mean(-1, keepdim=True) + self.cfg.rms_norm_eps)
-        return weight * f.to(x.dtype)
+    def _qkv(self, h: torch.Tensor, lw: _Layer, positions: torch.Tensor):
+        qkv = ops.linear(h, lw.w_qkv, lw.b_qkv)
+        return ops.rope_qkv(qkv, positions, self.inv_freq, self.nq, self.nkv, self.dim,
+                            bias=lw.b_qkv)
 
-    def _rope(self, q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor):
-        """qwen2.py:73-77: x*cos + rotate_half(x)*sin, cos/sin in the activation dtype."""
-        freqs = positions.float().unsqueeze(1) * self.inv_freq.unsqueeze(0)
-        emb = torch.cat([freqs, freqs], dim=-1)
-        cos, sin = emb.cos().to(q.dtype).unsqueeze(1), emb.sin().to(q.dtype).unsqueeze(1)
-        half = self.dim // 2
+    def _after_attention(self, x: torch.Tensor, attn: torch.Tensor, lw: _Layer,
+                         next_norm: torch.Tensor) -> torch.Tensor:
+        """Residual stream update of one layer after its attention; x is updated in
+        place and the normalised input of the next layer (or of the LM head) returned."""
+        o = ops.linear(attn.reshape(x.shape[0], self.nq * self.dim), lw.w_o)
+        h2, _ = ops.rmsnorm(o, lw.post_norm, self.cfg.rms_norm_eps, residual=x)
+        act = ops.silu_mul(ops.linear(h2, lw.w_gate_up))
+        h, _ = ops.rmsnorm(ops.linear(act, lw.w_down), next_norm, self.cfg.rms_norm_eps, residual=x)
+        return h
 
-        def rotate_half(x):
-            return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+    def _next_norm(self, layer: int) -> torch.Tensor:
+        return (self.layer_weights[layer + 1].input_norm if layer + 1 < self.layers
+                else self.final_norm)
 
-        return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
-
-    def _qkv(self, x: torch.Tensor, lw: _Layer, positions: torch.Tensor):
-        n = x.shape[0]
-        h = self._norm(x, lw.input_norm)
-        qkv = F.linear(h, lw.w_qkv, lw.b_qkv)
-        q = qkv[:, :self.nq * self.dim].view(n, self.nq, self.dim)
-        k = qkv[:, self.nq * self.dim:(self.nq + self.nkv) * self.dim].view(n, self.nkv, self.dim)
-        v = qkv[:, (self.nq + self.nkv) * self.dim:].view(n, self.nkv, self.dim)
-        q, k = self._rope(q, k, positions)
-        return q, k, v.contiguous()
-
-    def _mlp_residual(self, x: torch.Tensor, attn: torch.Tensor, lw: _Layer) -> torch.Tensor:
-        x = x + F.linear(attn.reshape(x.shape[0], self.nq * self.dim), lw.w_o)
-        gate_up = F.linear(self._norm(x, lw.post_norm), lw.w_gate_up)
-        inter = self.cfg.intermediate_size
-        return x + F.linear(F.silu(gate_up[:, :inter]) * gate_up[:, inter:], lw.w_down)
+    def _logits(self, h: torch.Tensor) -> torch.Tensor:
+        out = ops.linear(h, self.lm_head)
+        if out.dtype == torch.float32:  # skinny-GEMM partials
+            out = (out.sum(0) if out.shape[0] > 1 else out[0]).to(self.dtype)
+        return out
 
     # ---- the two forwards ---------------------------------------------------------
 
@@ -175,15 +172,16 @@ class Qwen2Model:
         ctx = torch.tensor([c.start + n for c, n in zip(chunks, lengths)], dtype=torch.int32).to(dev)
         max_q = max(lengths)
         x = self.embed.index_select(0, ids)
+        h, _ = ops.rmsnorm(x, self.layer_weights[0].input_norm, self.cfg.rms_norm_eps)
         for layer, lw in enumerate(self.layer_weights):
-            q, k, v = self._qkv(x, lw, positions)
+            q, k, v = self._qkv(h, lw, positions)
             ops.write_kv(k, v, cache.k[layer], cache.v[layer], slots[0], slots[1])
-            attn = ops.prefill_paged(q.contiguous(), cache.k[layer], cache.v[layer], tables,
-                                     q_offsets, ctx, max_q, scale=self.scale)
-            x = self._mlp_residual(x, attn, lw)
+            attn = ops.prefill_paged(q, cache.k[layer], cache.v[layer], tables, q_offsets, ctx,
+                                     max_q, scale=self.scale)
+            h = self._after_attention(x, attn, lw, self._next_norm(layer))
         ends = torch.tensor([sum(lengths[:j + 1]) - 1 for j in range(len(lengths))],
                             dtype=torch.long).to(dev)
-        logits = F.linear(self._norm(x.index_select(0, ends), self.final_norm), self.lm_head)
+        logits = self._logits(h.index_select(0, ends))
         return [logits[j] for j in range(len(lengths))]
 
     @torch.inference_mode()
@@ -195,11 +193,16 @@ class Qwen2Model:
         if input_ids.ndim != 1 or positions.shape != (batch,) or active_mask.reshape(-1).shape != (batch,):
             raise ValueError("invalid static decode inputs")
         active = active_mask.reshape(-1)
+        # the batched backend contract's conversions, once per step for all layers
+        # (paged_attention.py:115,131,138): length = position + 1, 0 for inactive rows
+        ctx = attention.context_lens_from_positions(positions, active)
+        tables = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
         x = self.embed.index_select(0, input_ids)
+        h, _ = ops.rmsnorm(x, self.layer_weights[0].input_norm, self.cfg.rms_norm_eps)
         for layer, lw in enumerate(self.layer_weights):
-            q, k, v = self._qkv(x, lw, positions)
-            attn = attention.paged_decode_batch(q, cache, layer, block_tables, positions, active,
-                                                k_new=k.contiguous(), v_new=v)
-            x = self._mlp_residual(x, attn, lw)
-        logits = F.linear(self._norm(x, self.final_norm), self.lm_head)
+            q, k, v = self._qkv(h, lw, positions)
+            attn = ops.paged_decode(q, cache.k[layer], cache.v[layer], tables, ctx, scale=self.scale,
+                                    k_new=k, v_new=v)
+            h = self._after_attention(x, attn, lw, self._next_norm(layer))
+        logits = self._logits(h)
         return logits * active.to(logits.dtype)[:, None]

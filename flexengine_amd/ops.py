@@ -250,3 +250,92 @@ def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
               q_offsets.data_ptr(), context_lens.data_ptr(), num_seqs, total_q, int(max_q_len),
               hq, hkv, d, bs, float(scale), _stream(dev))
     return out
+
+
+# ---------------------------------------------------------------------------------------
+# decoder-layer kernels (include/flexengine_amd_model.h)
+# ---------------------------------------------------------------------------------------
+
+SKINNY_MAX_ROWS = 32
+
+
+def _source(t: torch.Tensor) -> tuple[int, int, int, int, int]:
+    """(ptr, row stride, splits, rows, cols) of a sourced input: fp16 rows [rows, cols]
+    (unit column stride) or fp32 skinny-GEMM partials [splits, rows, cols]."""
+    if t.dtype == torch.float32:
+        if t.ndim != 3 or not t.is_contiguous():
+            raise ValueError("partials must be contiguous float32 [splits, rows, cols]")
+        s, rows, cols = t.shape
+        return t.data_ptr(), cols, s, rows, cols
+    if t.dtype != FP16 or t.ndim != 2 or t.stride(1) != 1:
+        raise ValueError("input must be float16 [rows, cols] with unit column stride")
+    return t.data_ptr(), t.stride(0), 0, t.shape[0], t.shape[1]
+
+
+def gemm_skinny(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """fp32 partial products [splits, M, N] of x [M, K] @ weight[N, K]^T (M <= 32);
+    consumers (rmsnorm, rope_qkv, silu_mul) sum the splits."""
+    dev = _require_gpu(x, weight)
+    if x.ndim != 2 or weight.ndim != 2 or x.shape[1] != weight.shape[1]:
+        raise ValueError("x [M, K] and weight [N, K] required")
+    if x.dtype != FP16 or weight.dtype != FP16 or not x.is_contiguous() or not weight.is_contiguous():
+        raise ValueError("x and weight must be contiguous float16")
+    m, k = x.shape
+    n = weight.shape[0]
+    splits = int(_lib.load().fe_gemm_skinny_splits(n, k))
+    part = torch.empty((splits, m, n), dtype=torch.float32, device=dev)
+    _lib.call("fe_gemm_skinny", x.data_ptr(), m, k, weight.data_ptr(), n, part.data_ptr(), splits,
+              _stream(dev))
+    return part
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """x @ weight^T (+ bias): the skinny HIP GEMM's fp32 partials (bias left to the
+    consumer) for at most SKINNY_MAX_ROWS rows, the library GEMM in fp16 otherwise."""
+    if x.shape[0] <= SKINNY_MAX_ROWS and x.shape[1] % 32 == 0:
+        return gemm_skinny(x.contiguous(), weight)
+    return torch.nn.functional.linear(x, weight, bias)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            residual: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """(weight * norm(x + residual), x + residual); with residual=None the second
+    value is None.  x is fp16 [rows, hidden] or skinny partials; the residual is
+    updated in place."""
+    ptr, _, splits, rows, hidden = _source(x)
+    dev = _require_gpu(x, weight, residual)
+    out = torch.empty((rows, hidden), dtype=FP16, device=dev)
+    if residual is not None and (residual.shape != (rows, hidden) or not residual.is_contiguous()):
+        raise ValueError("residual must be a contiguous [rows, hidden] tensor")
+    _lib.call("fe_rmsnorm", ptr, splits, _ptr(residual), _ptr(residual), weight.data_ptr(),
+              out.data_ptr(), rows, hidden, float(eps), _stream(dev))
+    return out, residual
+
+
+def rope_qkv(qkv: torch.Tensor, positions: torch.Tensor, inv_freq: torch.Tensor, num_q_heads: int,
+             kv_heads: int, head_dim: int, bias: torch.Tensor | None = None):
+    """Splits a fused [q | k | v] projection into q [rows, Hq, D], k, v [rows, Hkv, D]
+    with RoPE applied to q and k (positions int64 [rows])."""
+    ptr, stride, splits, rows, cols = _source(qkv)
+    if cols != (num_q_heads + 2 * kv_heads) * head_dim:
+        raise ValueError("qkv width does not match the head configuration")
+    dev = _require_gpu(qkv, positions, inv_freq, bias)
+    if positions.dtype != torch.int64 or positions.shape != (rows,):
+        raise ValueError("positions must be int64 [rows]")
+    q = torch.empty((rows, num_q_heads, head_dim), dtype=FP16, device=dev)
+    k = torch.empty((rows, kv_heads, head_dim), dtype=FP16, device=dev)
+    v = torch.empty_like(k)
+    _lib.call("fe_rope_qkv", ptr, stride, splits, _ptr(bias) if splits else None,
+              positions.data_ptr(), inv_freq.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+              rows, num_q_heads, kv_heads, head_dim, _stream(dev))
+    return q, k, v
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up over a fused [gate | up] input -> [rows, I]."""
+    ptr, stride, splits, rows, cols = _source(gate_up)
+    dev = _require_gpu(gate_up)
+    inter = cols // 2
+    out = torch.empty((rows, inter), dtype=FP16, device=dev)
+    _lib.call("fe_silu_mul", ptr, stride, splits, out.data_ptr(), rows, inter, _stream(dev))
+    return out

@@ -1,0 +1,88 @@
+/*
+ * flexengine_amd_model.h -- C ABI of the decoder-layer kernels around the
+ * paged attention (same library, libfe_paged.so; same conventions as
+ * flexengine_amd.h: device pointers, caller-owned buffers, asynchronous on
+ * `stream`, no host synchronisation, no allocation, graph-capturable; returns
+ * 0, a negative FE_ERR_* code, or a positive hipError_t).
+ *
+ * These are the caller side of the hot path: the per-layer work of
+ * FlexEngine's Qwen2Adapter decode step (src/flexengine/inference/models/
+ * qwen2.py:139-186) other than the attention, fused so that a graph-replayed
+ * step issues about nine launches per layer.
+ *
+ * "Sourced" inputs: an argument pair (ptr, splits) names a matrix
+ * [rows][cols] that is either fp16 rows (splits == 0; a row stride argument,
+ * where present, gives the element distance between rows) or the fp32
+ * partial products written by fe_gemm_skinny (splits > 0:
+ * [splits][rows][cols] floats, summed by the consumer and rounded to fp16).
+ */
+#ifndef FLEXENGINE_AMD_MODEL_H
+#define FLEXENGINE_AMD_MODEL_H
+
+#include "flexengine_amd.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Fused residual add + RMSNorm over rows of `hidden` (<= 8192) elements:
+ *   r = fp16(x + residual)            (residual may be NULL: r = fp16(x))
+ *   residual_out = r                  (may be NULL)
+ *   out = fp16(weight * fp16(r * rsqrt(mean(r^2) + eps)))
+ * x is sourced (x_splits).  Replaces the residual adds and the RMSNorm calls of
+ * qwen2.py:97,129-130,150,183-185 (HF Qwen2RMSNorm; the reference's optional
+ * Triton RMSNorm is src/flexengine/inference/kernels/rmsnorm.py:9-35).
+ */
+int fe_rmsnorm(const void* x, int x_splits, const void* residual, void* residual_out,
+               const void* weight, void* out, int rows, int hidden, float eps,
+               fe_stream_t stream);
+
+/*
+ * RoPE on a fused projection row [q: Hq*D | k: Hkv*D | v: Hkv*D] (sourced:
+ * qkv, qkv_splits; `bias` [(Hq+2Hkv)*D] fp16 is added to summed partials, may
+ * be NULL), writing q_out [rows, Hq, D], k_out and v_out [rows, Hkv, D]:
+ *   angle = float(positions[row]) * inv_freq[i]            (fp32)
+ *   c, s  = fp16(cos(angle)), fp16(sin(angle))
+ *   out[i] = x[i]*c - x[i+D/2]*s,  out[i+D/2] = x[i+D/2]*c + x[i]*s
+ * with each product and sum rounded to fp16 as PyTorch's fp16 ops do.
+ * positions are int64 (the engine's position tensor).  Replaces
+ * Qwen2Adapter._rope and rotate_half (qwen2.py:15-17,73-77) and the q/k/v
+ * views of qwen2.py:152-155.
+ */
+int fe_rope_qkv(const void* qkv, int64_t row_stride, int qkv_splits, const void* bias,
+                const int64_t* positions, const float* inv_freq, void* q_out, void* k_out,
+                void* v_out, int rows, int num_q_heads, int kv_heads, int head_dim,
+                fe_stream_t stream);
+
+/*
+ * SiLU-gated product of a fused [gate: I | up: I] row (sourced):
+ *   out[row][e] = fp16(fp16(silu(gate[e])) * up[e])        out: [rows, I]
+ * Replaces act_fn(gate_proj(x)) * up_proj(x) of the HF Qwen2MLP called at
+ * qwen2.py:130,184.
+ */
+int fe_silu_mul(const void* gate_up, int64_t row_stride, int splits, void* out, int rows,
+                int inter, fe_stream_t stream);
+
+/*
+ * Number of K slices fe_gemm_skinny uses for a weight of N rows and K columns.
+ */
+int fe_gemm_skinny_splits(int N, int K);
+
+/*
+ * Skinny GEMM for decode-sized batches (M <= 32, K a multiple of 32):
+ *   partials[s][m][o] = sum over k in slice s of x[m][k] * W[o][k]
+ * x: fp16 [M, K]; W: fp16 [N, K] (PyTorch Linear weight layout); partials:
+ * fp32 [splits][M][N] with splits = fe_gemm_skinny_splits(N, K).  Consumers
+ * take (partials, splits) as a sourced input.  Replaces the q/k/v, o, gate/up
+ * and down projections and the LM head of the decode step (qwen2.py:152-154,
+ * 183-186) for small batches.
+ */
+int fe_gemm_skinny(const void* x, int M, int K, const void* W, int N, float* partials,
+                   int splits, fe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLEXENGINE_AMD_MODEL_H */
