@@ -46,41 +46,60 @@ struct Src {
 // One workgroup per row.  r = x (+ residual), rounded to fp16 (the residual
 // stream's dtype); residual_out = r; out = weight * fp16(r * rsqrt(mean(r^2) + eps))
 // (transformers' Qwen2RMSNorm: the normalised value is cast to fp16 before
-// the weight multiply).
+// the weight multiply).  A decode step runs this on a handful of rows, so it
+// is pure latency: every global load of a thread (its x partials, residual and
+// weight elements) is issued before the first one is waited for.
+constexpr int kNormMaxSplits = 8;
+
+template <int PER>  // elements per thread: hidden <= PER * kNormThreads
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
     Src x, const f16* __restrict__ residual, f16* __restrict__ residual_out,
     const f16* __restrict__ weight, f16* __restrict__ out, int rows, int hidden, float eps) {
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t base = (int64_t)row * hidden;
-  float v[kNormMaxPerThread];
+  float v[PER], wv[PER];
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kNormMaxPerThread; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int e = tid + j * kNormThreads;
-    v[j] = 0.f;
-    if (e < hidden) {
-      float a = x.at(row, rows, e, hidden);
-      if (residual) a += (float)residual[base + e];
-      const f16 r = (f16)a;
-      if (residual_out) residual_out[base + e] = r;
-      v[j] = (float)r;
-      ss += v[j] * v[j];
+    const bool ok = e < hidden;
+    const int ec = ok ? e : hidden - 1;
+    float a;
+    if (x.splits == 0) {
+      a = (float)static_cast<const f16*>(x.p)[(int64_t)row * x.stride + ec];
+    } else {
+      const float* f = static_cast<const float*>(x.p);
+      float part[kNormMaxSplits];
+#pragma unroll
+      for (int k = 0; k < kNormMaxSplits; ++k)
+        part[k] = k < x.splits ? f[((int64_t)k * rows + row) * hidden + ec] : 0.f;
+      a = 0.f;
+#pragma unroll
+      for (int k = 0; k < kNormMaxSplits; ++k) a += part[k];
+      for (int k = kNormMaxSplits; k < x.splits; ++k) a += f[((int64_t)k * rows + row) * hidden + ec];
+      a = round16(a);
     }
+    const float rsd = residual ? (float)residual[base + ec] : 0.f;
+    wv[j] = (float)weight[ec];
+    const f16 r = (f16)(a + rsd);
+    if (ok && residual_out) residual_out[base + e] = r;
+    v[j] = ok ? (float)r : 0.f;
+    ss += v[j] * v[j];
   }
-  __shared__ float part[kNormThreads / kWave];
+  __shared__ float part_ss[kNormThreads / kWave];
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, kWave);
-  if (lane_id() == 0) part[tid / kWave] = ss;
+  if (lane_id() == 0) part_ss[tid / kWave] = ss;
   __syncthreads();
   float tot = 0.f;
 #pragma unroll
-  for (int w = 0; w < kNormThreads / kWave; ++w) tot += part[w];
+  for (int w = 0; w < kNormThreads / kWave; ++w) tot += part_ss[w];
   const float inv = rsqrtf(tot / (float)hidden + eps);
 #pragma unroll
-  for (int j = 0; j < kNormMaxPerThread; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int e = tid + j * kNormThreads;
-    if (e < hidden) out[base + e] = (f16)((float)weight[e] * round16(v[j] * inv));
+    if (e < hidden) out[base + e] = (f16)(wv[j] * round16(v[j] * inv));
   }
 }
 
@@ -149,9 +168,18 @@ extern "C" int fe_rmsnorm(const void* x, int x_splits, const void* residual, voi
   if (hidden > kNormThreads * kNormMaxPerThread) return FE_ERR_UNSUPPORTED;
   if (rows == 0) return FE_OK;
   FE_CHECK_ARG(x && weight && out);
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
-                     Src{x, hidden, x_splits, nullptr}, (const f16*)residual, (f16*)residual_out,
-                     (const f16*)weight, (f16*)out, rows, hidden, eps);
+  const Src src{x, hidden, x_splits, nullptr};
+  const int per = (hidden + kNormThreads - 1) / kNormThreads;
+#define FE_NORM_LAUNCH(P)                                                                        \
+  hipLaunchKernelGGL(rmsnorm_kernel<P>, dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream, \
+                     src, (const f16*)residual, (f16*)residual_out, (const f16*)weight,         \
+                     (f16*)out, rows, hidden, eps)
+  if (per <= 2) FE_NORM_LAUNCH(2);
+  else if (per <= 4) FE_NORM_LAUNCH(4);
+  else if (per <= 8) FE_NORM_LAUNCH(8);
+  else if (per <= 16) FE_NORM_LAUNCH(16);
+  else FE_NORM_LAUNCH(32);
+#undef FE_NORM_LAUNCH
   return FE_LAUNCH_STATUS();
 }
 
