@@ -1,0 +1,131 @@
+"""Per-configuration timings of the attention kernels (configs C1, C3, C4).
+
+    python -m flexengine_amd.bench_attention [--iters 50] [--configs c1,c3,c4]
+
+bench.py measures the headline config (C2); this script times the others the
+same way -- inputs resident in HBM, several rotating copies of the KV pool so
+the 256 MB Infinity Cache cannot serve repeats, HIP events on the launch
+stream -- and prints one JSON line per config:
+
+* C1 (B=8, 14/2 heads, D 64, L ~ U{16..512}): decode latency and GB/s.
+* C3 (B=256 in 8 groups sharing a 2048-token prefix): decode time, GB/s over
+  the compulsory unique bytes, and the "effective" GB/s over the logical bytes.
+* C4 (mixed step): the ragged prefill launch in TFLOP/s over the valid
+  query-key pairs against the 2.5 PFLOP/s fp16 MFMA peak, the 48 decode rows
+  in GB/s, and the whole step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+import torch
+
+from flexengine_amd import ops, workloads
+
+HBM_PEAK = 8.0e12
+MFMA_FP16_PEAK = 2.5e15
+
+
+def _timed(fn, iters: int) -> float:
+    """Mean seconds per call of fn(i) over `iters` calls, HIP events on the current stream."""
+    for i in range(3):
+        fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(iters):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / iters
+
+
+def _pools(w, copies: int):
+    return [(w.k_pool, w.v_pool)] + [(w.k_pool.clone(), w.v_pool.clone()) for _ in range(copies - 1)]
+
+
+def bench_decode(name: str, w, iters: int, copies: int, unique_bytes: int | None = None) -> dict:
+    d = w.to("cuda:0")
+    pools = _pools(d, copies)
+    out = torch.empty_like(d.q)
+
+    def step(i):
+        kp, vp = pools[i % len(pools)]
+        ops.paged_decode(d.q, kp, vp, d.block_tables, d.context_lens, out=out)
+
+    sec = _timed(step, iters)
+    logical = w.algorithmic_bytes(logical=True)
+    res = {"config": name, "kernel": "fe_paged_decode", "us_per_call": round(sec * 1e6, 2),
+           "batch": w.batch, "context_tokens": int(w.context_lens.sum()),
+           "bytes": logical, "GB_s": round(logical / sec / 1e9, 1),
+           "pct_hbm_peak": round(100 * logical / sec / HBM_PEAK, 1)}
+    if unique_bytes is not None:
+        res.update({"unique_bytes": unique_bytes, "GB_s": round(unique_bytes / sec / 1e9, 1),
+                    "pct_hbm_peak": round(100 * unique_bytes / sec / HBM_PEAK, 1),
+                    "effective_GB_s": round(logical / sec / 1e9, 1)})
+    return res
+
+
+def bench_c4(iters: int, copies: int) -> dict:
+    w = workloads.c4_workload()
+    d = w.to("cuda:0")
+    pools = _pools(d, copies)
+    out = torch.empty_like(d.q)
+    max_q = int((w.q_offsets[1:] - w.q_offsets[:-1]).max())
+
+    def prefill(i):
+        kp, vp = pools[i % len(pools)]
+        ops.prefill_paged(d.q, kp, vp, d.block_tables, d.q_offsets, d.context_lens, max_q, out=out)
+
+    dec = d.decode
+    dout = torch.empty_like(dec.q)
+
+    def decode(i):
+        kp, vp = pools[i % len(pools)]
+        ops.paged_decode(dec.q, kp, vp, dec.block_tables, dec.context_lens, out=dout)
+
+    def both(i):
+        prefill(i)
+        decode(i)
+
+    t_pre = _timed(prefill, iters)
+    t_dec = _timed(decode, iters)
+    t_all = _timed(both, iters)
+    flops = w.flops()
+    dbytes = w.decode.algorithmic_bytes()
+    return {"config": "C4", "prefill_us": round(t_pre * 1e6, 2), "prefill_flops": flops,
+            "prefill_TFLOP_s": round(flops / t_pre / 1e12, 1),
+            "pct_mfma_fp16_peak": round(100 * flops / t_pre / MFMA_FP16_PEAK, 2),
+            "decode_us": round(t_dec * 1e6, 2), "decode_bytes": dbytes,
+            "decode_GB_s": round(dbytes / t_dec / 1e9, 1), "step_us": round(t_all * 1e6, 2),
+            "prefill_tokens": int(w.q.shape[0]), "chunks": w.meta["n_new"], "cached": w.meta["cached"]}
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--iters", type=int, default=50)
+    p.add_argument("--copies", type=int, default=4, help="rotating KV pool copies")
+    p.add_argument("--configs", default="c1,c3,c4")
+    args = p.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("bench_attention needs a ROCm GPU", file=sys.stderr)
+        return 2
+    cfgs = args.configs.split(",")
+    if "c1" in cfgs:
+        print(json.dumps(bench_decode("C1", workloads.c1_workload(), args.iters, args.copies * 8)),
+              flush=True)
+    if "c3" in cfgs:
+        w = workloads.c3_workload()
+        hkv, d = w.k_pool.shape[2], w.k_pool.shape[3]
+        # compulsory bytes: every distinct K/V row once, plus q and out
+        unique = w.unique_tokens * 2 * hkv * d * 2 + 2 * w.q.numel() * 2
+        print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique)), flush=True)
+    if "c4" in cfgs:
+        print(json.dumps(bench_c4(args.iters, args.copies)), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
