@@ -5,11 +5,28 @@
 // attend causally to keys t <= position over the paged K/V of the sequence
 // (the new rows' own K/V are already in the pool).
 //
-// grid = (64-row query blocks of all sequences, num_q_heads); 256 threads.
-// Wave w of a workgroup owns 16 query rows of one query head: they are the 16
-// MFMA columns of the tile engine in attn_core.h, each column with its own
-// causal limit (position + 1).  The QK^T and PV contractions run on
-// v_mfma_f32_16x16x16_f16 with fp32 accumulation.
+// Work decomposition.  For one KV head h, the query rows of a sequence are the
+// pairs (position, query head of the group) flattened position-major: row
+// r -> position r / G, query head h*G + r % G.  A workgroup (4 waves) owns
+// 64*RT consecutive rows of one sequence and KV head, so all G query heads of
+// the group share every K/V block it loads.  K/V are walked in blocks of 64
+// keys: the workgroup stages a block in LDS (double-buffered; the next block's
+// global loads are in flight while the current one is computed, one barrier
+// per block), and every wave computes its RT tiles of 16 rows against it:
+//
+//   S^T[16 keys x 16 rows] = K . Q^T    v_mfma_f32_16x16x32_f16, k = 32 dims
+//     A = K: lane (g,n) reads key n, dims 32c + 8g .. +7 (16 bytes, LDS)
+//     B = Q: lane (g,n) holds row n's query, same dims (registers)
+//   base-2 online softmax with lazy rescale (attn_core.h), causal mask only on
+//   the blocks that cross the workgroup's first position
+//   O^T[16 dims x 16 rows] += V^T . P^T  v_mfma_f32_16x16x32_f16, k = 32 keys
+//     B = P^T: lane (g,n) holds keys 4g..4g+3 of two 16-key tiles (the score
+//       layout itself), A = V^T: two transposing LDS reads (ds_read_b64_tr_b16)
+//       give lane (g,n) the same keys for dim n.
+//
+// The reference runs a materialized gather + SDPA per request for every
+// multi-token chunk (src/flexengine/inference/attention/paged.py:27-40,
+// called per request from qwen2.py:117-126).
 #include "attn_core.h"
 
 using namespace fe;
@@ -17,14 +34,28 @@ using namespace fe;
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerWave = 16;
-constexpr int kRowsPerBlock = 64;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kBlockKeys = 64;
+
+template <int D, int RT>
+struct PCfg {
+  static constexpr int NC = D / 32;                 // 32-dim k-chunks of QK^T
+  static constexpr int NX = D / 16;                 // 16-dim output tiles
+  static constexpr int KP = D * 2 + 16;             // K row pitch in LDS (bytes)
+  static constexpr int VP = D * 2 + 32;             // V row pitch (transposing reads)
+  static constexpr int KBYTES = kBlockKeys * KP;
+  static constexpr int STAGE = KBYTES + kBlockKeys * VP;
+  static constexpr int ROWS = kWaves * 16 * RT;     // rows per workgroup
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per K/V row
+  static constexpr int KPL = kThreads / CPR;        // key rows covered by one load round
+  static constexpr int LOADS = kBlockKeys / KPL;    // load rounds per matrix per block
+};
 
 struct PrefillArgs {
   const f16* q;
   f16* out;
-  f16* k_pool;
-  f16* v_pool;
+  const f16* k_pool;
+  const f16* v_pool;
   const int32_t* tables;
   const int32_t* q_off;
   const int32_t* ctx;
@@ -32,39 +63,38 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-struct QBlock {
-  int s;     // sequence
-  int qb;    // 64-row block index within the sequence
-  int n;     // query rows of the sequence
-  int q0;    // first query row of the sequence in q/out
-  int ctx;   // context length of the sequence
+struct RowBlock {
+  int s;      // sequence
+  int rb;     // row block of the sequence
+  int n;      // new rows (positions) of the sequence
+  int q0;     // first query row of the sequence in q/out
+  int ctx;    // context length (cached + new)
 };
 
-__device__ __forceinline__ int seq_rows(const PrefillArgs& a, int s, int& q0) {
-  q0 = a.q_off[s];
-  const int n = a.q_off[s + 1] - q0;
-  return n > 0 ? n : 0;
-}
-
-// Maps a workgroup id onto (sequence, query block); false past the last block.
-__device__ __forceinline__ bool locate_qblock(const PrefillArgs& a, int item, QBlock& qb) {
+// Maps a workgroup id onto (sequence, row block); false past the last block.
+template <int ROWS>
+__device__ __forceinline__ bool locate_rows(const PrefillArgs& a, int item, RowBlock& rb) {
   const int lane = lane_id();
   int carry = 0;
   for (int base = 0; base < a.S; base += kWave) {
     const int s = base + lane;
     int q0 = 0, n = 0;
-    if (s < a.S) n = seq_rows(a, s, q0);
-    const int nb = (n + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (s < a.S) {
+      q0 = a.q_off[s];
+      n = a.q_off[s + 1] - q0;
+      n = n > 0 ? n : 0;
+    }
+    const int nb = (n * a.G + ROWS - 1) / ROWS;
     const int incl = wave_scan_incl_i(nb) + carry;
     const int excl = incl - nb;
     const unsigned long long hit = __ballot(s < a.S && item >= excl && item < incl);
     if (hit) {
       const int src = __builtin_ctzll(hit);
-      qb.s = base + src;
-      qb.qb = item - readlane_i(excl, src);
-      qb.n = readlane_i(n, src);
-      qb.q0 = readlane_i(q0, src);
-      qb.ctx = clamp_len(a.ctx[qb.s]);
+      rb.s = base + src;
+      rb.rb = item - readlane_i(excl, src);
+      rb.n = readlane_i(n, src);
+      rb.q0 = readlane_i(q0, src);
+      rb.ctx = __builtin_amdgcn_readfirstlane(clamp_len(a.ctx[rb.s]));
       return true;
     }
     carry = readlane_i(incl, kWave - 1);
@@ -72,67 +102,203 @@ __device__ __forceinline__ bool locate_qblock(const PrefillArgs& a, int item, QB
   return false;
 }
 
-template <int D>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) {
-  using C = TileCfg<D>;
-  __shared__ __align__(16) unsigned char smem[4 * C::STAGE];
+__device__ __forceinline__ f32x4 mfma32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
 
-  QBlock qb;
-  if (!locate_qblock(a, blockIdx.x, qb)) return;
-  const int hq = blockIdx.y;
-  const int h = hq / a.G;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+template <int D, int RT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
+void prefill_kernel(const PrefillArgs a) {
+  using P = PCfg<D, RT>;
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  RowBlock rb;
+  if (!locate_rows<P::ROWS>(a, blockIdx.x, rb)) return;
+  const int h = blockIdx.y;
+  const int G = a.G;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = lane_id();
   const int g = lane >> 4;
   const int n = lane & 15;
 
-  const int row0 = qb.qb * kRowsPerBlock + w * kRowsPerWave;  // first row of this wave
-  if (row0 >= qb.n) return;                                   // wave without rows
-  const int cached = qb.ctx >= qb.n ? qb.ctx - qb.n : 0;
-  const int row = row0 + n;
-  const bool valid = row < qb.n;
-  const int last_row = (row0 + kRowsPerWave - 1 < qb.n ? row0 + kRowsPerWave : qb.n) - 1;
+  const int total_rows = rb.n * G;
+  const int cached = rb.ctx >= rb.n ? rb.ctx - rb.n : 0;
+  const int r0 = rb.rb * P::ROWS;
+  const int r_last = min(r0 + P::ROWS, total_rows) - 1;
+  const int key_end = cached + r_last / G + 1;                   // keys this workgroup reads
+  const int nblocks = (key_end + kBlockKeys - 1) / kBlockKeys;
+  const int wr0 = r0 + w * 16 * RT;                               // first row of this wave
+  const int wave_pos_lo = cached + min(wr0, r_last) / G;          // its smallest position
+  // blocks whose last key is <= every row's position need no causal mask
+  const int unmasked_blocks = (wave_pos_lo + 1) / kBlockKeys;
 
-  TileCore<D> core;
-  core.k_pool = a.k_pool;
-  core.v_pool = a.v_pool;
-  core.trow = a.tables + (int64_t)qb.s * a.W;
-  core.rs = (int64_t)a.Hkv * D;
-  core.hoff = h * D;
-  core.W = a.W;
-  core.NB = a.NB;
-  core.BS = a.BS;
-  core.bs_log2 = a.bs_log2;
-  core.tok_end = cached + last_row + 1;
-  core.limit = valid ? cached + row + 1 : 0;
-  core.scale_log2 = a.scale_log2;
-  core.knew_row = nullptr;
-  core.vnew_row = nullptr;
-  core.new_pos = -1;
-  core.stage = smem + w * C::STAGE;
-
-  int qrow_idx = qb.q0 + (valid ? row : last_row);
-  qrow_idx = qrow_idx < a.total_q ? qrow_idx : a.total_q - 1;
-  {
-    const f16* qrow = a.q + ((int64_t)qrow_idx * a.Hq + hq) * D;
+  // ---- this lane's rows: query vectors (B operand), positions ----
+  f16x8 qv[RT][P::NC];
+  int pos[RT];
+  bool valid[RT];
 #pragma unroll
-    for (int s = 0; s < C::NK; ++s) {
-      const f16x8 v = ld16(qrow + (4 * s + g) * 8);
-      core.qv[s] = valid ? v : f16x8{};
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = wr0 + 16 * rt + n;
+    valid[rt] = row < total_rows;
+    const int rc = valid[rt] ? row : r_last;
+    pos[rt] = valid[rt] ? cached + rc / G : -1;
+    const f16* qrow = a.q + ((int64_t)(rb.q0 + rc / G) * a.Hq + h * G + rc % G) * D + 8 * g;
+#pragma unroll
+    for (int c = 0; c < P::NC; ++c) {
+      const f16x8 v = ld16(qrow + 32 * c);
+      qv[rt][c] = valid[rt] ? v : f16x8{};
     }
   }
-  core.init_acc();
-  core.run(0, 1, (core.tok_end + kTile - 1) / kTile);
 
-  const float l = core.l_total();
-  if (valid) {
-    const float inv = 1.f / l;
-    f16* orow = a.out + ((int64_t)qrow_idx * a.Hq + hq) * D;
+  float m_run[RT], l_run[RT];
+  f32x4 o[RT][P::NX];
 #pragma unroll
-    for (int x = 0; x < C::NX; ++x) {
-      const f16x4 v = {(f16)(core.o[x][0] * inv), (f16)(core.o[x][1] * inv),
-                       (f16)(core.o[x][2] * inv), (f16)(core.o[x][3] * inv)};
-      *reinterpret_cast<f16x4*>(orow + 16 * x + 4 * g) = v;
+  for (int rt = 0; rt < RT; ++rt) {
+    m_run[rt] = kNegInf;
+    l_run[rt] = 0.f;
+#pragma unroll
+    for (int x = 0; x < P::NX; ++x) o[rt][x] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // ---- K/V block staging: thread t loads 16-byte chunk t % CPR of key rows
+  //      t / CPR + KPL * i; keys at or past key_end are zero-filled ----
+  const int32_t* trow = a.tables + (int64_t)rb.s * a.W;
+  const int chunk = tid % P::CPR;
+  const int krow = tid / P::CPR;
+  f16x8 ks[P::LOADS], vs[P::LOADS];
+  auto load_block = [&](int kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < P::LOADS; ++i) {
+      const int key = kb * kBlockKeys + krow + P::KPL * i;
+      const bool ok = key < key_end;
+      const int kc = ok ? key : key_end - 1;
+      int page = kc >> a.bs_log2;
+      page = page < a.W ? page : a.W - 1;
+      const int blk = clamp_block(trow[page], a.NB);
+      const int64_t off = (((int64_t)blk * a.BS + (kc & (a.BS - 1))) * a.Hkv + h) * D + chunk * 8;
+      const f16x8 kv = ld16(a.k_pool + off);
+      const f16x8 vv = ld16(a.v_pool + off);
+      ks[i] = ok ? kv : f16x8{};
+      vs[i] = ok ? vv : f16x8{};
+    }
+  };
+  auto store_block = [&](int stage) __attribute__((always_inline)) {
+    unsigned char* kbase = smem + stage * P::STAGE;
+    unsigned char* vbase = kbase + P::KBYTES;
+#pragma unroll
+    for (int i = 0; i < P::LOADS; ++i) {
+      const int r = krow + P::KPL * i;
+      *reinterpret_cast<f16x8*>(kbase + r * P::KP + chunk * 16) = ks[i];
+      *reinterpret_cast<f16x8*>(vbase + r * P::VP + chunk * 16) = vs[i];
+    }
+  };
+
+  load_block(0);
+  store_block(0);
+  __syncthreads();
+
+  for (int kb = 0; kb < nblocks; ++kb) {
+    const bool more = kb + 1 < nblocks;
+    if (more) load_block(kb + 1);
+    const unsigned char* kbase = smem + (kb & 1) * P::STAGE;
+    const unsigned char* vbase = kbase + P::KBYTES;
+
+    // S^T tiles: 4 key tiles x RT row tiles
+    f32x4 st[RT][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) st[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < P::NC; ++c) {
+        const f16x8 kv =
+            *reinterpret_cast<const f16x8*>(kbase + (16 * kt + n) * P::KP + (32 * c + 8 * g) * 2);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) st[rt][kt] = mfma32(kv, qv[rt][c], st[rt][kt]);
+      }
+    }
+
+    // online softmax per row tile; P^T as two f16x8 B operands (keys 0-31, 32-63)
+    f16x8 pb[RT][2];
+    const bool need_mask = kb >= unmasked_blocks;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      float sv[4][4];
+      float mx = kNegInf;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb * kBlockKeys + 16 * kt + 4 * g + i;
+          float v = st[rt][kt][i] * a.scale_log2;
+          if (need_mask && key > pos[rt]) v = kNegInf;
+          sv[kt][i] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, shfl_xor_f(mx, 16));
+      mx = fmaxf(mx, shfl_xor_f(mx, 32));
+      if (__ballot(mx > m_run[rt] + kRescaleSlack)) {  // wave-uniform
+        const float m_new = fmaxf(m_run[rt], mx);
+        const float alpha = m_new == kNegInf ? 1.f : exp2f(m_run[rt] - m_new);
+        l_run[rt] *= alpha;
+#pragma unroll
+        for (int x = 0; x < P::NX; ++x) o[rt][x] *= alpha;
+        m_run[rt] = m_new;
+      }
+      const float m_use = m_run[rt] == kNegInf ? 0.f : m_run[rt];
+      float lsum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        f16x8 p;
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float e = exp2f(sv[2 * j + half][i] - m_use);
+            lsum += e;
+            p[4 * half + i] = (f16)e;
+          }
+        pb[rt][j] = p;
+      }
+      l_run[rt] += lsum;
+    }
+
+    // O^T += V^T . P^T: two 32-key steps per 16-dim tile
+    const unsigned char* vb = vbase + (4 * g + (n >> 2)) * P::VP + (n & 3) * 8;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int x = 0; x < P::NX; ++x) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(vb + (32 * j) * P::VP + 32 * x));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(vb + (32 * j + 16) * P::VP + 32 * x));
+        const f16x4 l4 = __builtin_bit_cast(f16x4, lo), h4 = __builtin_bit_cast(f16x4, hi);
+        const f16x8 va = {l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) o[rt][x] = mfma32(va, pb[rt][j], o[rt][x]);
+      }
+    }
+
+    if (more) store_block((kb + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- normalise and store: lane (g,n) holds O[row n][dims 16x + 4g + i] ----
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    float l = l_run[rt] + shfl_xor_f(l_run[rt], 16);
+    l += shfl_xor_f(l, 32);
+    if (valid[rt]) {
+      const int row = wr0 + 16 * rt + n;
+      const float inv = 1.f / l;
+      f16* orow = a.out + ((int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G) * D + 4 * g;
+#pragma unroll
+      for (int x = 0; x < P::NX; ++x)
+        *reinterpret_cast<f16x4*>(orow + 16 * x) =
+            f16x4{(f16)(o[rt][x][0] * inv), (f16)(o[rt][x][1] * inv), (f16)(o[rt][x][2] * inv),
+                  (f16)(o[rt][x][3] * inv)};
     }
   }
 }
@@ -143,6 +309,15 @@ inline int log2_exact(int x) {
   int l = 0;
   while ((1 << l) < x) ++l;
   return l;
+}
+
+template <int D, int RT>
+void launch_prefill(const PrefillArgs& a, hipStream_t stream) {
+  using P = PCfg<D, RT>;
+  // upper bound on the row blocks: sum_s ceil(n_s G / ROWS) <= total_q G / ROWS + S
+  const int blocks = (int)(((int64_t)a.total_q * a.G + P::ROWS - 1) / P::ROWS) + a.S;
+  hipLaunchKernelGGL((prefill_kernel<D, RT>), dim3(blocks, a.Hkv), dim3(kThreads),
+                     2 * P::STAGE, stream, a);
 }
 
 }  // namespace
@@ -166,8 +341,8 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   PrefillArgs a;
   a.q = (const f16*)q;
   a.out = (f16*)out;
-  a.k_pool = (f16*)k_pool;
-  a.v_pool = (f16*)v_pool;
+  a.k_pool = (const f16*)k_pool;
+  a.v_pool = (const f16*)v_pool;
   a.tables = block_tables;
   a.q_off = q_offsets;
   a.ctx = context_lens;
@@ -181,12 +356,14 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   a.bs_log2 = bs_log2;
   a.NB = num_blocks;
   a.scale_log2 = scale * kLog2e;
-  // upper bound on the number of 64-row blocks: sum_s ceil(n_s/64) <= total_q/64 + num_seqs
-  const int blocks = (total_q + kRowsPerBlock - 1) / kRowsPerBlock + num_seqs;
-  const dim3 grid(blocks, num_q_heads);
-  if (head_dim == 64)
-    hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
-  else
-    hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+  // two row tiles per wave when that still gives about two workgroups per CU
+  const int64_t rows = (int64_t)total_q * a.G * kv_heads;
+  const bool wide = rows >= (int64_t)512 * PCfg<128, 2>::ROWS;
+  hipStream_t s = (hipStream_t)stream;
+  if (head_dim == 64) {
+    if (wide) launch_prefill<64, 2>(a, s); else launch_prefill<64, 1>(a, s);
+  } else {
+    if (wide) launch_prefill<128, 2>(a, s); else launch_prefill<128, 1>(a, s);
+  }
   return FE_LAUNCH_STATUS();
 }
