@@ -38,7 +38,8 @@ SIGNATURES: dict[str, tuple] = {
                              _i, _i, _i, _i, _i, _f, _i, _p]),
     "fe_lse_merge": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),
     "fe_prefill_paged": (_i, [_p, _p, _p, _p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _i,
-                              _f, _p]),
+                              _f, _p, _sz, _p]),
+    "fe_prefill_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
     # include/flexengine_amd_model.h
     "fe_rmsnorm": (_i, [_p, _i, _p, _p, _p, _p, _i, _i, _f, _p]),
     "fe_rope_qkv": (_i, [_p, _i64, _i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),

@@ -35,7 +35,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kBlockKeys = 64;
+constexpr int kBlockKeys = 32;  // one 16x16x32 PV step per block
 
 template <int D, int RT>
 struct PCfg {
@@ -59,9 +59,15 @@ struct PrefillArgs {
   const int32_t* tables;
   const int32_t* q_off;
   const int32_t* ctx;
-  int W, S, total_q, Hq, Hkv, G, BS, bs_log2, NB;
+  float* part_o;     // [KS][total_q * Hq][D] normalised partial outputs (KS > 1)
+  float* part_lse;   // [KS][total_q * Hq] base-2 LSE of each partial
+  int* tickets;      // [row blocks * Hkv], zero between calls
+  int W, S, total_q, Hq, Hkv, G, BS, bs_log2, NB, KS;
   float scale_log2;
 };
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kSc1 = 16;  // buffer-instruction cache policy: sc1 (device-coherent)
 
 struct RowBlock {
   int s;      // sequence
@@ -126,8 +132,13 @@ void prefill_kernel(const PrefillArgs a) {
   const int cached = rb.ctx >= rb.n ? rb.ctx - rb.n : 0;
   const int r0 = rb.rb * P::ROWS;
   const int r_last = min(r0 + P::ROWS, total_rows) - 1;
-  const int key_end = cached + r_last / G + 1;                   // keys this workgroup reads
-  const int nblocks = (key_end + kBlockKeys - 1) / kBlockKeys;
+  const int key_end = cached + r_last / G + 1;                   // keys the row block reads
+  // split ks of KS takes an equal share of the row block's key blocks
+  const int ks = blockIdx.z;
+  const int nblocks_all = (key_end + kBlockKeys - 1) / kBlockKeys;
+  const int per_split = (nblocks_all + a.KS - 1) / a.KS;
+  const int kb_lo = min(ks * per_split, nblocks_all);
+  const int kb_hi = min(kb_lo + per_split, nblocks_all);
   const int wr0 = r0 + w * 16 * RT;                               // first row of this wave
   const int wave_pos_lo = cached + min(wr0, r_last) / G;          // its smallest position
   // blocks whose last key is <= every row's position need no causal mask
@@ -162,25 +173,35 @@ void prefill_kernel(const PrefillArgs a) {
   }
 
   // ---- K/V block staging: thread t loads 16-byte chunk t % CPR of key rows
-  //      t / CPR + KPL * i; keys at or past key_end are zero-filled ----
+  //      t / CPR + KPL * i; keys at or past key_end are zero-filled.  The
+  //      block ids a block needs are fetched one iteration before its K/V
+  //      loads, so no table access sits in front of a K/V load. ----
   const int32_t* trow = a.tables + (int64_t)rb.s * a.W;
   const int chunk = tid % P::CPR;
   const int krow = tid / P::CPR;
-  f16x8 ks[P::LOADS], vs[P::LOADS];
+  f16x8 kst[P::LOADS], vst[P::LOADS];
+  int ids[P::LOADS];
+  auto fetch_ids = [&](int kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < P::LOADS; ++i) {
+      const int key = min(kb * kBlockKeys + krow + P::KPL * i, key_end - 1);
+      int page = key >> a.bs_log2;
+      page = page < a.W ? page : a.W - 1;
+      ids[i] = trow[page];
+    }
+  };
   auto load_block = [&](int kb) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < P::LOADS; ++i) {
       const int key = kb * kBlockKeys + krow + P::KPL * i;
       const bool ok = key < key_end;
       const int kc = ok ? key : key_end - 1;
-      int page = kc >> a.bs_log2;
-      page = page < a.W ? page : a.W - 1;
-      const int blk = clamp_block(trow[page], a.NB);
+      const int blk = clamp_block(ids[i], a.NB);
       const int64_t off = (((int64_t)blk * a.BS + (kc & (a.BS - 1))) * a.Hkv + h) * D + chunk * 8;
       const f16x8 kv = ld16(a.k_pool + off);
       const f16x8 vv = ld16(a.v_pool + off);
-      ks[i] = ok ? kv : f16x8{};
-      vs[i] = ok ? vv : f16x8{};
+      kst[i] = ok ? kv : f16x8{};
+      vst[i] = ok ? vv : f16x8{};
     }
   };
   auto store_block = [&](int stage) __attribute__((always_inline)) {
@@ -189,25 +210,32 @@ void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < P::LOADS; ++i) {
       const int r = krow + P::KPL * i;
-      *reinterpret_cast<f16x8*>(kbase + r * P::KP + chunk * 16) = ks[i];
-      *reinterpret_cast<f16x8*>(vbase + r * P::VP + chunk * 16) = vs[i];
+      *reinterpret_cast<f16x8*>(kbase + r * P::KP + chunk * 16) = kst[i];
+      *reinterpret_cast<f16x8*>(vbase + r * P::VP + chunk * 16) = vst[i];
     }
   };
 
-  load_block(0);
-  store_block(0);
+  if (kb_lo < kb_hi) {
+    fetch_ids(kb_lo);
+    load_block(kb_lo);
+    fetch_ids(kb_lo + 1);
+    store_block(0);
+  }
   __syncthreads();
 
-  for (int kb = 0; kb < nblocks; ++kb) {
-    const bool more = kb + 1 < nblocks;
-    if (more) load_block(kb + 1);
-    const unsigned char* kbase = smem + (kb & 1) * P::STAGE;
+  for (int kb = kb_lo; kb < kb_hi; ++kb) {
+    const bool more = kb + 1 < kb_hi;
+    if (more) {
+      load_block(kb + 1);
+      fetch_ids(kb + 2);
+    }
+    const unsigned char* kbase = smem + ((kb - kb_lo) & 1) * P::STAGE;
     const unsigned char* vbase = kbase + P::KBYTES;
 
-    // S^T tiles: 4 key tiles x RT row tiles
-    f32x4 st[RT][4];
+    // S^T tiles: 2 key tiles x RT row tiles
+    f32x4 st[RT][2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) st[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -219,15 +247,15 @@ void prefill_kernel(const PrefillArgs a) {
       }
     }
 
-    // online softmax per row tile; P^T as two f16x8 B operands (keys 0-31, 32-63)
-    f16x8 pb[RT][2];
+    // online softmax per row tile; P^T of the 32 keys as one f16x8 B operand
+    f16x8 pb[RT];
     const bool need_mask = kb >= unmasked_blocks;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      float sv[4][4];
+      float sv[2][4];
       float mx = kNegInf;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = kb * kBlockKeys + 16 * kt + 4 * g + i;
@@ -248,58 +276,109 @@ void prefill_kernel(const PrefillArgs a) {
       }
       const float m_use = m_run[rt] == kNegInf ? 0.f : m_run[rt];
       float lsum = 0.f;
+      f16x8 p;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        f16x8 p;
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int half = 0; half < 2; ++half)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float e = exp2f(sv[2 * j + half][i] - m_use);
-            lsum += e;
-            p[4 * half + i] = (f16)e;
-          }
-        pb[rt][j] = p;
-      }
+        for (int i = 0; i < 4; ++i) {
+          const float e = exp2f(sv[kt][i] - m_use);
+          lsum += e;
+          p[4 * kt + i] = (f16)e;
+        }
+      pb[rt] = p;
       l_run[rt] += lsum;
     }
 
-    // O^T += V^T . P^T: two 32-key steps per 16-dim tile
+    // O^T += V^T . P^T: one 32-key step per 16-dim tile
     const unsigned char* vb = vbase + (4 * g + (n >> 2)) * P::VP + (n & 3) * 8;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int x = 0; x < P::NX; ++x) {
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(vb + 32 * x));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(vb + 16 * P::VP + 32 * x));
+      const f16x4 l4 = __builtin_bit_cast(f16x4, lo), h4 = __builtin_bit_cast(f16x4, hi);
+      const f16x8 va = {l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
 #pragma unroll
-      for (int x = 0; x < P::NX; ++x) {
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(vb + (32 * j) * P::VP + 32 * x));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(vb + (32 * j + 16) * P::VP + 32 * x));
-        const f16x4 l4 = __builtin_bit_cast(f16x4, lo), h4 = __builtin_bit_cast(f16x4, hi);
-        const f16x8 va = {l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) o[rt][x] = mfma32(va, pb[rt][j], o[rt][x]);
-      }
+      for (int rt = 0; rt < RT; ++rt) o[rt][x] = mfma32(va, pb[rt], o[rt][x]);
     }
 
-    if (more) store_block((kb + 1) & 1);
+    if (more) store_block((kb + 1 - kb_lo) & 1);
     __syncthreads();
   }
 
-  // ---- normalise and store: lane (g,n) holds O[row n][dims 16x + 4g + i] ----
+  // ---- normalise; one split: store.  Several: write this split's partial
+  //      (device-coherent stores), draw a ticket; the last split of the row
+  //      block merges all of them.  Lane (g,n) holds O[row n][dims 16x+4g+i]. ----
+  const bool split = a.KS > 1;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     float l = l_run[rt] + shfl_xor_f(l_run[rt], 16);
     l += shfl_xor_f(l, 32);
-    if (valid[rt]) {
-      const int row = wr0 + 16 * rt + n;
-      const float inv = 1.f / l;
-      f16* orow = a.out + ((int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G) * D + 4 * g;
+    if (!valid[rt]) continue;
+    const int row = wr0 + 16 * rt + n;
+    const int64_t orow_idx = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    if (!split) {
+      f16* orow = a.out + orow_idx * D + 4 * g;
 #pragma unroll
       for (int x = 0; x < P::NX; ++x)
         *reinterpret_cast<f16x4*>(orow + 16 * x) =
-            f16x4{(f16)(o[rt][x][0] * inv), (f16)(o[rt][x][1] * inv), (f16)(o[rt][x][2] * inv),
-                  (f16)(o[rt][x][3] * inv)};
+            f16x4{(f16)(o[rt][x][0] * inv), (f16)(o[rt][x][1] * inv),
+                  (f16)(o[rt][x][2] * inv), (f16)(o[rt][x][3] * inv)};
+    } else {
+      const int64_t prow = (int64_t)ks * a.total_q * a.Hq + orow_idx;
+      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+          a.part_o + prow * D, 0, D * (int)sizeof(float), 0x00020000);
+#pragma unroll
+      for (int x = 0; x < P::NX; ++x)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[rt][x] * inv), r,
+                                               (uint32_t)((16 * x + 4 * g) * sizeof(float)), 0, kSc1);
+      if (g == 0)
+        __hip_atomic_store(a.part_lse + prow, l > 0.f ? m_run[rt] + log2f(l) : kNegInf,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+  if (!split) return;
+  __shared__ int last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials are complete
+  __syncthreads();
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(a.tickets + blockIdx.x * a.Hkv + h, 1, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) == a.KS - 1;
+  __syncthreads();
+  if (!last) return;
+  if (tid == 0)
+    __hip_atomic_store(a.tickets + blockIdx.x * a.Hkv + h, 0, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  // merge: thread -> (row of the block, 4 consecutive dims)
+  const int64_t split_stride = (int64_t)a.total_q * a.Hq;
+  for (int u = tid; u < P::ROWS * (D / 4); u += kThreads) {
+    const int row = r0 + u / (D / 4);
+    if (row > r_last) break;
+    const int d4 = (u % (D / 4)) * 4;
+    const int64_t orow_idx = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
+    float M = kNegInf;
+    for (int k = 0; k < a.KS; ++k)
+      M = fmaxf(M, __hip_atomic_load(a.part_lse + k * split_stride + orow_idx, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT));
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+    for (int k = 0; k < a.KS; ++k) {
+      const int64_t prow = k * split_stride + orow_idx;
+      const float lse = __hip_atomic_load(a.part_lse + prow, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+      if (lse == kNegInf) continue;
+      const float wgt = exp2f(lse - M);
+      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+          a.part_o + prow * D, 0, D * (int)sizeof(float), 0x00020000);
+      num += wgt * __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 r, (uint32_t)(d4 * sizeof(float)), 0, kSc1));
+      den += wgt;
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    *reinterpret_cast<f16x4*>(a.out + orow_idx * D + d4) =
+        f16x4{(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv), (f16)(num[3] * inv)};
   }
 }
 
@@ -312,22 +391,54 @@ inline int log2_exact(int x) {
 }
 
 template <int D, int RT>
-void launch_prefill(const PrefillArgs& a, hipStream_t stream) {
+void launch_prefill(const PrefillArgs& a, int blocks, hipStream_t stream) {
   using P = PCfg<D, RT>;
-  // upper bound on the row blocks: sum_s ceil(n_s G / ROWS) <= total_q G / ROWS + S
-  const int blocks = (int)(((int64_t)a.total_q * a.G + P::ROWS - 1) / P::ROWS) + a.S;
-  hipLaunchKernelGGL((prefill_kernel<D, RT>), dim3(blocks, a.Hkv), dim3(kThreads),
+  hipLaunchKernelGGL((prefill_kernel<D, RT>), dim3(blocks, a.Hkv, a.KS), dim3(kThreads),
                      2 * P::STAGE, stream, a);
 }
 
+constexpr int kMaxTickets = 65536;
+constexpr size_t kTicketBytes = kMaxTickets * sizeof(int);
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Launch shape from host-side sizes only (context lengths live on the device):
+// rows per workgroup (RT), an upper bound on the row blocks, and the key
+// splits KS, aiming at about 1024 workgroups (four per CU).
+struct Plan {
+  int rt, blocks, ks;
+};
+inline Plan plan(int num_seqs, int total_q, int num_q_heads, int kv_heads) {
+  const int64_t rows = (int64_t)total_q * num_q_heads;  // (token, query head) rows
+  Plan p;
+  p.rt = rows >= (int64_t)512 * PCfg<128, 2>::ROWS ? 2 : 1;
+  const int per = kWaves * 16 * p.rt;
+  const int G = num_q_heads / kv_heads;
+  p.blocks = (int)(((int64_t)total_q * G + per - 1) / per) + num_seqs;
+  const int64_t wgs = (int64_t)((rows + per - 1) / per) * 1;
+  int ks = (int)((1024 + wgs - 1) / (wgs > 0 ? wgs : 1));
+  p.ks = ks < 1 ? 1 : (ks > 8 ? 8 : ks);
+  return p;
+}
+
 }  // namespace
+
+extern "C" size_t fe_prefill_workspace_size(int num_seqs, int total_q, int num_q_heads,
+                                            int kv_heads, int head_dim) {
+  if (num_seqs < 0 || total_q < 0 || num_q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
+      num_q_heads % kv_heads)
+    return 0;
+  const Plan p = plan(num_seqs, total_q, num_q_heads, kv_heads);
+  if (p.ks == 1) return kTicketBytes;
+  const size_t rows = (size_t)p.ks * total_q * num_q_heads;
+  return kTicketBytes + align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
+}
 
 extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, const void* v_pool,
                                 int num_blocks, const int32_t* block_tables, int table_stride,
                                 const int32_t* q_offsets, const int32_t* context_lens,
                                 int num_seqs, int total_q, int max_q_len, int num_q_heads,
                                 int kv_heads, int head_dim, int block_size, float scale,
-                                fe_stream_t stream) {
+                                void* workspace, size_t workspace_bytes, fe_stream_t stream) {
   FE_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 &&
                kv_heads > 0 && num_blocks > 0 && table_stride > 0);
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
@@ -337,6 +448,11 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   if (num_seqs == 0 || total_q == 0) return FE_OK;
   FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && q_offsets && context_lens);
   FE_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(k_pool) && aligned16(v_pool));
+  const Plan p = plan(num_seqs, total_q, num_q_heads, kv_heads);
+  if ((int64_t)p.blocks * kv_heads > kMaxTickets) return FE_ERR_UNSUPPORTED;
+  const size_t need = fe_prefill_workspace_size(num_seqs, total_q, num_q_heads, kv_heads, head_dim);
+  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+    return FE_ERR_WORKSPACE;
 
   PrefillArgs a;
   a.q = (const f16*)q;
@@ -346,6 +462,13 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   a.tables = block_tables;
   a.q_off = q_offsets;
   a.ctx = context_lens;
+  char* ws = (char*)workspace;
+  a.tickets = (int*)ws;
+  ws += kTicketBytes;
+  const size_t rows = (size_t)p.ks * total_q * num_q_heads;
+  a.part_o = (float*)ws;
+  ws += align256(rows * head_dim * sizeof(float));
+  a.part_lse = (float*)ws;
   a.W = table_stride;
   a.S = num_seqs;
   a.total_q = total_q;
@@ -355,15 +478,13 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   a.BS = block_size;
   a.bs_log2 = bs_log2;
   a.NB = num_blocks;
+  a.KS = p.ks;
   a.scale_log2 = scale * kLog2e;
-  // two row tiles per wave when that still gives about two workgroups per CU
-  const int64_t rows = (int64_t)total_q * a.G * kv_heads;
-  const bool wide = rows >= (int64_t)512 * PCfg<128, 2>::ROWS;
   hipStream_t s = (hipStream_t)stream;
   if (head_dim == 64) {
-    if (wide) launch_prefill<64, 2>(a, s); else launch_prefill<64, 1>(a, s);
+    if (p.rt == 2) launch_prefill<64, 2>(a, p.blocks, s); else launch_prefill<64, 1>(a, p.blocks, s);
   } else {
-    if (wide) launch_prefill<128, 2>(a, s); else launch_prefill<128, 1>(a, s);
+    if (p.rt == 2) launch_prefill<128, 2>(a, p.blocks, s); else launch_prefill<128, 1>(a, p.blocks, s);
   }
   return FE_LAUNCH_STATUS();
 }

@@ -132,13 +132,15 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_cont
                                                           max_context, target_splits))
 
 
-def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A per-device workspace reused by every decode call on that device.
+def decode_workspace(device: torch.device, nbytes: int, kind: str = "decode") -> torch.Tensor:
+    """A per-device workspace reused by every decode (or, kind="prefill", prefill)
+    call on that device.
 
     Calls on one stream are ordered, so sharing is safe there; callers running
-    decode on several streams at once must pass their own zero-filled workspace.
+    these kernels on several streams at once must pass their own zero-filled
+    workspace.
     """
-    key = (device.type, device.index)
+    key = (device.type, device.index, kind)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         # zero-filled once: the split-K tickets at its start must begin at zero
@@ -245,10 +247,12 @@ def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
         out = torch.empty_like(q)
     if scale is None:
         scale = 1.0 / math.sqrt(d)
+    need = int(_lib.load().fe_prefill_workspace_size(num_seqs, total_q, hq, hkv, d))
+    ws = decode_workspace(dev, need, kind="prefill")
     _lib.call("fe_prefill_paged", q.data_ptr(), out.data_ptr(), k_pool.data_ptr(),
               v_pool.data_ptr(), nb, block_tables.data_ptr(), block_tables.shape[1],
               q_offsets.data_ptr(), context_lens.data_ptr(), num_seqs, total_q, int(max_q_len),
-              hq, hkv, d, bs, float(scale), _stream(dev))
+              hq, hkv, d, bs, float(scale), ws.data_ptr(), ws.numel(), _stream(dev))
     return out
 
 

@@ -175,7 +175,17 @@ int fe_prefill_paged(const void* q, void* out,
                      const int32_t* q_offsets, const int32_t* context_lens,
                      int num_seqs, int total_q, int max_q_len,
                      int num_q_heads, int kv_heads, int head_dim,
-                     int block_size, float scale, fe_stream_t stream);
+                     int block_size, float scale,
+                     void* workspace, size_t workspace_bytes, fe_stream_t stream);
+
+/*
+ * Bytes of device workspace fe_prefill_paged needs for these sizes (its key
+ * splits keep fp32 partial outputs there).  Like the decode workspace it must
+ * be zero-filled before its first use; every call leaves its ticket region
+ * zero again, so one allocation serves every later call on the stream.
+ */
+size_t fe_prefill_workspace_size(int num_seqs, int total_q, int num_q_heads, int kv_heads,
+                                 int head_dim);
 
 #ifdef __cplusplus
 }

@@ -86,7 +86,7 @@ def test_host_side_validation_rejects_before_launch(lib):
     assert rc == _lib.FE_ERR_INVALID_ARGUMENT
     # Hq not a multiple of Hkv
     rc = lib.fe_prefill_paged(null, null, null, null, 1, null, 1, null, null, 1, 1, 1, 12, 5, 128, 16,
-                              0.1, null)
+                              0.1, null, 0, null)
     assert rc == _lib.FE_ERR_INVALID_ARGUMENT
     rc = lib.fe_write_kv(null, null, 256, null, null, 4, null, null, 3, 2, 128, 16, null)
     assert rc == _lib.FE_ERR_INVALID_ARGUMENT
@@ -102,6 +102,11 @@ def test_workspace_size_grows_with_batch_and_target(lib):
     assert 0 < a < b and a < c
     assert a % 256 == 0
     assert lib.fe_paged_decode_workspace_size(-1, 12, 128, 4096, 0) == 0
+    # prefill workspace: tickets only for big prefills, tickets + partials for small ones
+    big = lib.fe_prefill_workspace_size(8, 8192, 12, 2, 128)
+    small = lib.fe_prefill_workspace_size(4, 1377, 12, 2, 128)
+    assert big >= 65536 * 4 and small > 65536 * 4
+    assert lib.fe_prefill_workspace_size(1, 10, 12, 5, 128) == 0
     # very long tables raise the split target (pieces stay <= 4096 keys)
     d = lib.fe_paged_decode_workspace_size(64, 12, 128, 1 << 20, 0)
     assert d > a

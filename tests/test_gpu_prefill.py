@@ -96,3 +96,14 @@ def test_prefill_then_decode_consistency():
     dec = ops.paged_decode(q[j:j + 1].to(DEV), kp.to(DEV), vp.to(DEV), tables.to(DEV),
                            torch.tensor([pos + 1], dtype=torch.int32, device=DEV)).cpu().numpy()
     assert np.abs(got[j] - dec[0].astype(np.float64)).max() <= 2e-3
+
+
+def test_split_prefill_repeated_calls_and_shapes_share_the_workspace():
+    """The key-split merge leaves its tickets at zero: repeated calls of different
+    shapes on the shared workspace give the same results each time."""
+    a = _case(3, [130, 7, 1], [0, 40, 999])
+    b = _case(4, [65], [100])
+    first_a, first_b = _run(*a), _run(*b)
+    for _ in range(3):
+        np.testing.assert_array_equal(_run(*a), first_a)
+        np.testing.assert_array_equal(_run(*b), first_b)
