@@ -9,9 +9,10 @@
 // pairs (position, query head of the group) flattened position-major: row
 // r -> position r / G, query head h*G + r % G.  A workgroup (4 waves) owns
 // 64*RT consecutive rows of one sequence and KV head, so all G query heads of
-// the group share every K/V block it loads.  K/V are walked in blocks of 64
+// the group share every K/V block it loads.  K/V are walked in blocks of 32
 // keys: the workgroup stages a block in LDS (double-buffered; the next block's
-// global loads are in flight while the current one is computed, one barrier
+// global loads, and the block ids of the one after, are in flight while the
+// current one is computed, one barrier
 // per block), and every wave computes its RT tiles of 16 rows against it:
 //
 //   S^T[16 keys x 16 rows] = K . Q^T    v_mfma_f32_16x16x32_f16, k = 32 dims
@@ -23,6 +24,14 @@
 //     B = P^T: lane (g,n) holds keys 4g..4g+3 of two 16-key tiles (the score
 //       layout itself), A = V^T: two transposing LDS reads (ds_read_b64_tr_b16)
 //       give lane (g,n) the same keys for dim n.
+//
+// Key splits: when the row blocks alone give too few workgroups to fill the
+// chip, grid.z = KS workgroups share a row block, each taking an equal share
+// of its key blocks.  A split writes its normalised fp32 partial output and
+// base-2 LSE with device-coherent stores, waits for them, and draws a ticket
+// of (row block, KV head); the last split to arrive merges the KS partials
+// into the fp16 output and resets the ticket, so the workspace needs no clear
+// between calls.
 //
 // The reference runs a materialized gather + SDPA per request for every
 // multi-token chunk (src/flexengine/inference/attention/paged.py:27-40,
