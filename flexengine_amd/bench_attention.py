@@ -13,6 +13,8 @@ stream -- and prints one JSON line per config:
 * C4 (mixed step): the ragged prefill launch in TFLOP/s over the valid
   query-key pairs against the 2.5 PFLOP/s fp16 MFMA peak, the 48 decode rows
   in GB/s, and the whole step.
+
+Calls are replayed from a HIP graph, so each figure is GPU time per call.
 """
 from __future__ import annotations
 
@@ -28,18 +30,30 @@ HBM_PEAK = 8.0e12
 MFMA_FP16_PEAK = 2.5e15
 
 
-def _timed(fn, iters: int) -> float:
-    """Mean seconds per call of fn(i) over `iters` calls, HIP events on the current stream."""
-    for i in range(3):
+def _timed(fn, iters: int, variants: int) -> float:
+    """Mean GPU seconds per call of fn(i), i cycling over `variants` inputs.
+
+    The `variants` calls are captured once into a HIP graph (after an eager warm-up
+    that also sizes the workspaces) and the graph is replayed, so the figure is the
+    GPU's time per call, not the host's launch rate; HIP events on the replay stream.
+    """
+    for i in range(variants):
         fn(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(variants):
+            fn(i)
+    reps = max(2, iters // variants)
+    graph.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for i in range(iters):
-        fn(i)
+    for _ in range(reps):
+        graph.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / 1e3 / iters
+    return start.elapsed_time(end) / 1e3 / (reps * variants)
 
 
 def _pools(w, copies: int):
@@ -55,7 +69,7 @@ def bench_decode(name: str, w, iters: int, copies: int, unique_bytes: int | None
         kp, vp = pools[i % len(pools)]
         ops.paged_decode(d.q, kp, vp, d.block_tables, d.context_lens, out=out)
 
-    sec = _timed(step, iters)
+    sec = _timed(step, iters, len(pools))
     logical = w.algorithmic_bytes(logical=True)
     res = {"config": name, "kernel": "fe_paged_decode", "us_per_call": round(sec * 1e6, 2),
            "batch": w.batch, "context_tokens": int(w.context_lens.sum()),
@@ -90,9 +104,9 @@ def bench_c4(iters: int, copies: int) -> dict:
         prefill(i)
         decode(i)
 
-    t_pre = _timed(prefill, iters)
-    t_dec = _timed(decode, iters)
-    t_all = _timed(both, iters)
+    t_pre = _timed(prefill, iters, len(pools))
+    t_dec = _timed(decode, iters, len(pools))
+    t_all = _timed(both, iters, len(pools))
     flops = w.flops()
     dbytes = w.decode.algorithmic_bytes()
     return {"config": "C4", "prefill_us": round(t_pre * 1e6, 2), "prefill_flops": flops,
@@ -105,7 +119,7 @@ def bench_c4(iters: int, copies: int) -> dict:
 
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    p.add_argument("--iters", type=int, default=50)
+    p.add_argument("--iters", type=int, default=200)
     p.add_argument("--copies", type=int, default=4, help="rotating KV pool copies")
     p.add_argument("--configs", default="c1,c3,c4")
     args = p.parse_args(argv)

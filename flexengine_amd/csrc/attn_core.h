@@ -315,8 +315,11 @@ struct TileListCore {
   // Issues the K/V loads of tile k; nothing here waits for data.  Past the end
   // of the list the descriptors have zero extent and touch no memory.
   __device__ __forceinline__ void load_tile(int k, f16x8 (&kk)[C::NK], f16x8 (&vv)[C::NK]) const {
-    const int64_t base = tile_base(k);
-    const int rows = tile_rows(k);
+    load_at(tile_base(k), tile_rows(k), kk, vv);
+  }
+  // The same for a tile given by its element offset (kv head included) and keys.
+  __device__ __forceinline__ void load_at(int64_t base, int rows, f16x8 (&kk)[C::NK],
+                                          f16x8 (&vv)[C::NK]) const {
     const __amdgpu_buffer_rsrc_t kr = tile_rsrc(k_pool, base, rows);
     const __amdgpu_buffer_rsrc_t vr = tile_rsrc(v_pool, base, rows);
     const uint32_t ko = k_off0();
@@ -333,10 +336,13 @@ struct TileListCore {
   // returns the new bytes.
   __device__ __forceinline__ void write_new_row(int k, int r, const f16* knew_row,
                                                 const f16* vnew_row) const {
+    write_new_row_at(tile_base(k), r, knew_row, vnew_row);
+  }
+  __device__ __forceinline__ void write_new_row_at(int64_t base, int r, const f16* knew_row,
+                                                   const f16* vnew_row) const {
     const int lane = lane_id();
     const int g = lane >> 4;
     const int n = lane & 15;
-    const int64_t base = tile_base(k);
     char* kb = reinterpret_cast<char*>(k_pool_w + base);
     char* vb = reinterpret_cast<char*>(v_pool_w + base);
     if (n == r) {
@@ -357,6 +363,11 @@ struct TileListCore {
 
   __device__ __forceinline__ void compute_tile(int k, const f16x8 (&kk)[C::NK],
                                                f16x8 (&vv)[C::NK]) {
+    compute_rows(tile_rows(k), kk, vv);
+  }
+  // One tile of `rows` valid keys (1..16) held in kk / vv.
+  __device__ __forceinline__ void compute_rows(int rows, const f16x8 (&kk)[C::NK],
+                                               f16x8 (&vv)[C::NK]) {
     const int lane = lane_id();
     const int vrow = lane / C::CPR;
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
@@ -376,7 +387,7 @@ struct TileListCore {
       }
     }
     compiler_fence();
-    softmax_pv_tile<D>(sacc, 0, tile_rows(k), scale_log2, stage, m_run, l_run, o);
+    softmax_pv_tile<D>(sacc, 0, rows, scale_log2, stage, m_run, l_run, o);
     compiler_fence();
   }
 

@@ -53,6 +53,17 @@ constexpr int kMaxGroup = 16;
 #ifndef FE_DECODE_WAVES_PER_EU
 #define FE_DECODE_WAVES_PER_EU 2
 #endif
+// LDS of the piece kernel: per-wave V staging, then every wave's parked state
+// (o, m, l) for the combine, and a ticket flag.
+template <int D>
+struct PieceLds {
+  static constexpr size_t stage = 0;
+  static constexpr size_t park = stage + (size_t)kWaves * TileCfg<D>::STAGE;
+  static constexpr size_t park_m = park + (size_t)kWaves * TileCfg<D>::NX * kWave * 16;
+  static constexpr size_t park_l = park_m + (size_t)kWaves * kWave * sizeof(float);
+  static constexpr size_t flag = park_l + (size_t)kWaves * kWave * sizeof(float);
+  static constexpr size_t bytes = flag + sizeof(int);
+};
 
 struct DecodeArgs {
   const f16* q;
@@ -190,6 +201,7 @@ void piece_decode_kernel(const DecodeArgs a) {
     }
     return;
   }
+  using Lds = PieceLds<D>;
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = lane_id();
@@ -214,7 +226,6 @@ void piece_decode_kernel(const DecodeArgs a) {
   float m_run, l_tot;
   f32x4 o[C::NX];
   if constexpr (PAGE16) {
-    // the wave's tiles t_first, t_first + 4, ... of the piece as a tile list
     TileListCore<D> core;
     core.k_pool = a.k_pool;
     core.v_pool = a.v_pool;
@@ -224,6 +235,7 @@ void piece_decode_kernel(const DecodeArgs a) {
     core.hoff = h * D;
     core.scale_log2 = a.scale_log2;
     core.stage = smem + w * C::STAGE;
+    // the wave's tiles t_first, t_first + 4, ... of the piece as a tile list
     const int ntiles = t_first < t_end ? (t_end - t_first + kWaves - 1) / kWaves : 0;
     core.ntiles = ntiles;
     {
@@ -269,47 +281,51 @@ void piece_decode_kernel(const DecodeArgs a) {
     for (int x = 0; x < C::NX; ++x) o[x] = core.o[x];
   }
 
-  // ---- combine the four waves: waves 1..3 park their state in LDS (lane-major,
-  // conflict-free), wave 0 combines in its own register layout: lane (g, n)
-  // holds O[head n][16x + 4g + i], so the per-head scale factors are per lane.
-  f32x4* park = reinterpret_cast<f32x4*>(smem + kWaves * C::STAGE);  // [3][NX][64]
-  float* park_m = reinterpret_cast<float*>(park + (kWaves - 1) * C::NX * kWave);
-  float* park_l = park_m + (kWaves - 1) * kWave;
-  int* flag = reinterpret_cast<int*>(park_l + (kWaves - 1) * kWave);
-  if (w > 0) {
-#pragma unroll
-    for (int x = 0; x < C::NX; ++x) park[((w - 1) * C::NX + x) * kWave + lane] = o[x];
-    park_m[(w - 1) * kWave + lane] = m_run;
-    park_l[(w - 1) * kWave + lane] = l_tot;
-  }
-  __syncthreads();
   const bool split = pc.nsplit > 1;
-  if (w == 0) {
-    float M = m_run;
+  f32x4* park = reinterpret_cast<f32x4*>(smem + Lds::park);  // [4][NX][64]
+  float* park_m = reinterpret_cast<float*>(smem + Lds::park_m);
+  float* park_l = reinterpret_cast<float*>(smem + Lds::park_l);
+  int* flag = reinterpret_cast<int*>(smem + Lds::flag);
+  // ---- combine the four waves: every wave parks (o, m, l) in LDS (lane-major,
+  // conflict-free); wave w then combines output tiles [w*XW, (w+1)*XW) of all
+  // four in the register layout of the loop: lane (g, n) holds
+  // O[head n][16x + 4g + i], so the per-head scale factors are per lane.
+  {
 #pragma unroll
-    for (int v = 0; v < kWaves - 1; ++v) M = fmaxf(M, park_m[v * kWave + lane]);
-    const float sc0 = m_run == kNegInf ? 0.f : exp2f(m_run - M);
-    float den = sc0 * l_tot;
+    for (int x = 0; x < C::NX; ++x) park[(w * C::NX + x) * kWave + lane] = o[x];
+    park_m[w * kWave + lane] = m_run;
+    park_l[w * kWave + lane] = l_tot;
+    __syncthreads();
+    float M = kNegInf;
 #pragma unroll
-    for (int x = 0; x < C::NX; ++x) o[x] *= sc0;
+    for (int v = 0; v < kWaves; ++v) M = fmaxf(M, park_m[v * kWave + lane]);
+    float sc[kWaves];
+    float den = 0.f;
 #pragma unroll
-    for (int v = 0; v < kWaves - 1; ++v) {
+    for (int v = 0; v < kWaves; ++v) {
       const float mv = park_m[v * kWave + lane];
-      const float sc = mv == kNegInf ? 0.f : exp2f(mv - M);
-      den += sc * park_l[v * kWave + lane];
-#pragma unroll
-      for (int x = 0; x < C::NX; ++x) o[x] += sc * park[(v * C::NX + x) * kWave + lane];
+      sc[v] = mv == kNegInf ? 0.f : exp2f(mv - M);
+      den += sc[v] * park_l[v * kWave + lane];
     }
     const float inv = 1.f / den;
+    constexpr int XW = C::NX / kWaves;  // output tiles per wave
+    f32x4 ox[XW];
+#pragma unroll
+    for (int xi = 0; xi < XW; ++xi) {
+      const int x = w * XW + xi;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) acc += sc[v] * park[(v * C::NX + x) * kWave + lane];
+      ox[xi] = acc * inv;
+    }
     if (n < G) {
       const int hq = h * G + n;
       if (!split) {
         f16* orow = a.out + ((int64_t)b * a.Hq + hq) * D + 4 * g;
 #pragma unroll
-        for (int x = 0; x < C::NX; ++x)
-          *reinterpret_cast<f16x4*>(orow + 16 * x) =
-              f16x4{(f16)(o[x][0] * inv), (f16)(o[x][1] * inv), (f16)(o[x][2] * inv),
-                    (f16)(o[x][3] * inv)};
+        for (int xi = 0; xi < XW; ++xi)
+          *reinterpret_cast<f16x4*>(orow + 16 * (w * XW + xi)) =
+              f16x4{(f16)ox[xi][0], (f16)ox[xi][1], (f16)ox[xi][2], (f16)ox[xi][3]};
       } else {
         // device-coherent (sc1) 16-byte stores of this piece's partial output
         const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
@@ -317,22 +333,22 @@ void piece_decode_kernel(const DecodeArgs a) {
             0x00020000);
         const uint32_t off = (uint32_t)((n * D + 4 * g) * sizeof(float));
 #pragma unroll
-        for (int x = 0; x < C::NX; ++x)
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[x] * inv), r,
-                                                 off + 16 * x * sizeof(float), 0, kSc1);
-        if (g == 0) store_coherent(a.ws_lse + (int64_t)item * a.Hq + hq, M + log2f(den));
+        for (int xi = 0; xi < XW; ++xi)
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, ox[xi]), r,
+              off + 16 * (w * XW + xi) * (uint32_t)sizeof(float), 0, kSc1);
+        if (w == 0 && g == 0) store_coherent(a.ws_lse + (int64_t)item * a.Hq + hq, M + log2f(den));
       }
     }
   }
   if (!split) return;
 
   // ---- split-K: the last piece of (b, h) to finish merges all pieces ----
-  if (w == 0) {
-    wait_stores();  // this piece's partials are complete at the device-coherent level
-    if (lane == 0)
-      *flag = __hip_atomic_fetch_add(a.tickets + b * a.Hkv + h, 1, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT) == pc.nsplit - 1;
-  }
+  wait_stores();  // this wave's partials are complete at the device-coherent level
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *flag = __hip_atomic_fetch_add(a.tickets + b * a.Hkv + h, 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT) == pc.nsplit - 1;
   __syncthreads();
   if (!*flag) return;
   if (threadIdx.x == 0)
@@ -741,9 +757,7 @@ inline int effective_target(int batch, int kv_heads, int max_context, int target
 
 template <int D>
 size_t piece_lds_bytes() {
-  // V staging of the four waves, then the parked state of waves 1..3 and a flag
-  return (size_t)kWaves * TileCfg<D>::STAGE +
-         (size_t)(kWaves - 1) * (TileCfg<D>::NX * kWave * 16 + 2 * kWave * sizeof(float)) + 16;
+  return PieceLds<D>::bytes;
 }
 
 // FE_DECODE_LEAN selects the partition of the block-size-16 path: 1 = equal
