@@ -9,7 +9,8 @@ stream -- and prints one JSON line per config:
 
 * C1 (B=8, 14/2 heads, D 64, L ~ U{16..512}): decode latency and GB/s.
 * C3 (B=256 in 8 groups sharing a 2048-token prefix): decode time, GB/s over
-  the compulsory unique bytes, and the "effective" GB/s over the logical bytes.
+  the compulsory unique bytes, and the "effective" GB/s over the logical bytes,
+  for the plain decode and for the shared-prefix (cascade) decode.
 * C4 (mixed step): the ragged prefill launch in TFLOP/s over the valid
   query-key pairs against the 2.5 PFLOP/s fp16 MFMA peak, the 48 decode rows
   in GB/s, and the whole step.
@@ -60,18 +61,26 @@ def _pools(w, copies: int):
     return [(w.k_pool, w.v_pool)] + [(w.k_pool.clone(), w.v_pool.clone()) for _ in range(copies - 1)]
 
 
-def bench_decode(name: str, w, iters: int, copies: int, unique_bytes: int | None = None) -> dict:
+def bench_decode(name: str, w, iters: int, copies: int, unique_bytes: int | None = None,
+                 shared_prefix: bool = False) -> dict:
     d = w.to("cuda:0")
     pools = _pools(d, copies)
     out = torch.empty_like(d.q)
+    if shared_prefix:
+        go, pl = d.meta["group_offsets"].to("cuda:0"), d.meta["prefix_lens"].to("cuda:0")
 
     def step(i):
         kp, vp = pools[i % len(pools)]
-        ops.paged_decode(d.q, kp, vp, d.block_tables, d.context_lens, out=out)
+        if shared_prefix:
+            ops.paged_decode_shared_prefix(d.q, kp, vp, d.block_tables, d.context_lens, go, pl,
+                                           out=out)
+        else:
+            ops.paged_decode(d.q, kp, vp, d.block_tables, d.context_lens, out=out)
 
     sec = _timed(step, iters, len(pools))
     logical = w.algorithmic_bytes(logical=True)
-    res = {"config": name, "kernel": "fe_paged_decode", "us_per_call": round(sec * 1e6, 2),
+    kernel = "fe_paged_decode_shared_prefix" if shared_prefix else "fe_paged_decode"
+    res = {"config": name, "kernel": kernel, "us_per_call": round(sec * 1e6, 2),
            "batch": w.batch, "context_tokens": int(w.context_lens.sum()),
            "bytes": logical, "GB_s": round(logical / sec / 1e9, 1),
            "pct_hbm_peak": round(100 * logical / sec / HBM_PEAK, 1)}
@@ -136,6 +145,8 @@ def main(argv=None) -> int:
         # compulsory bytes: every distinct K/V row once, plus q and out
         unique = w.unique_tokens * 2 * hkv * d * 2 + 2 * w.q.numel() * 2
         print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique)), flush=True)
+        print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique,
+                                      shared_prefix=True)), flush=True)
     if "c4" in cfgs:
         print(json.dumps(bench_c4(args.iters, args.copies)), flush=True)
     return 0

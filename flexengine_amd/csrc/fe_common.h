@@ -79,6 +79,10 @@ __device__ __forceinline__ f16x4 hi4(f16x8 v) { return f16x4{v[4], v[5], v[6], v
 // Pieces are numbered sequence-major; piece ids run over [0, sum_b splits_b) <=
 // target + batch.  Every function below is evaluated by a whole wave and
 // returns wave-uniform values.
+//
+// With a shared-prefix (cascade) decode, sequence b's keys before tok0[b] are
+// attended elsewhere, and only its suffix [tok0[b], L_b) is partitioned here
+// (quads_b counts the suffix).  tok0 == nullptr means tok0[b] = 0.
 
 __device__ __forceinline__ int clamp_len(int L) { return L > 0 ? L : 0; }
 
@@ -102,13 +106,24 @@ __device__ __forceinline__ int wave_max_i(int v) {
 // cut into more than kMaxPieces pieces (the merge holds their weights in LDS).
 constexpr int kMaxPieces = 64;
 
-__device__ __forceinline__ int split_chunk_quads(const int32_t* ctx, int B, int max_len,
-                                                 int target) {
+// First key of sequence b's suffix (0 without a shared prefix); <= its length.
+__device__ __forceinline__ int suffix_start(const int32_t* tok0, int b, int L) {
+  if (tok0 == nullptr) return 0;
+  const int t = tok0[b];
+  return t > 0 ? (t < L ? t : L) : 0;
+}
+
+__device__ __forceinline__ int split_chunk_quads(const int32_t* ctx, const int32_t* tok0, int B,
+                                                 int max_len, int target) {
   const int lane = lane_id();
   int total = 0, longest = 0;
   for (int base = 0; base < B; base += kWave) {
     const int b = base + lane;
-    const int nq = b < B ? (seq_len(ctx, b, max_len) + 63) >> 6 : 0;
+    int nq = 0;
+    if (b < B) {
+      const int L = seq_len(ctx, b, max_len);
+      nq = (L - suffix_start(tok0, b, L) + 63) >> 6;
+    }
     total += wave_sum_i(nq);
     const int m = wave_max_i(nq);
     longest = longest > m ? longest : m;
@@ -129,20 +144,23 @@ struct Piece {
   int split;     // index of this piece within the sequence
   int nsplit;    // pieces of this sequence
   int L;         // context length of the sequence
+  int tok0;      // first key of the sequence's suffix (> 0: a shared prefix precedes it)
   int tok_begin; // first key position of the piece
   int tok_end;   // one past the last key position of the piece
 };
 
 // Finds the piece with id `item`; false when item is past the last piece, in
 // which case `total` receives the number of pieces.
-__device__ __forceinline__ bool locate_piece(const int32_t* ctx, int B, int max_len, int chunk,
-                                             int item, Piece& pc, int& total) {
+__device__ __forceinline__ bool locate_piece(const int32_t* ctx, const int32_t* tok0, int B,
+                                             int max_len, int chunk, int item, Piece& pc,
+                                             int& total) {
   const int lane = lane_id();
   int carry = 0;
   for (int base = 0; base < B; base += kWave) {
     const int b = base + lane;
     const int L = b < B ? seq_len(ctx, b, max_len) : 0;
-    const int nq = (L + 63) >> 6;
+    const int t0 = b < B ? suffix_start(tok0, b, L) : 0;
+    const int nq = (L - t0 + 63) >> 6;
     const int ns = (nq + chunk - 1) / chunk;
     const int incl = wave_scan_incl_i(ns) + carry;
     const int excl = incl - ns;
@@ -151,10 +169,11 @@ __device__ __forceinline__ bool locate_piece(const int32_t* ctx, int B, int max_
       const int src = __builtin_ctzll(hit);
       pc.b = base + src;
       pc.L = readlane_i(L, src);
+      pc.tok0 = readlane_i(t0, src);
       pc.nsplit = readlane_i(ns, src);
       pc.split = item - readlane_i(excl, src);
-      pc.tok_begin = pc.split * chunk * 64;
-      const int e = (pc.split + 1) * chunk * 64;
+      pc.tok_begin = pc.tok0 + pc.split * chunk * 64;
+      const int e = pc.tok0 + (pc.split + 1) * chunk * 64;
       pc.tok_end = e < pc.L ? e : pc.L;
       return true;
     }
@@ -164,27 +183,38 @@ __device__ __forceinline__ bool locate_piece(const int32_t* ctx, int B, int max_
   return false;
 }
 
-// Number of pieces of sequence b and the id of its first piece.
-__device__ __forceinline__ void seq_pieces(const int32_t* ctx, int B, int max_len, int chunk,
-                                           int b, int& nsplit, int& first) {
-  const int lane = lane_id();
-  int carry = 0;
-  nsplit = 0;
-  first = 0;
-  for (int base = 0; base < B; base += kWave) {
-    const int bb = base + lane;
-    const int L = bb < B ? seq_len(ctx, bb, max_len) : 0;
-    const int nq = (L + 63) >> 6;
-    const int ns = (nq + chunk - 1) / chunk;
-    const int incl = wave_scan_incl_i(ns) + carry;
-    if (b >= base && b < base + kWave) {
-      nsplit = readlane_i(ns, b - base);
-      first = readlane_i(incl - ns, b - base);
-      return;
-    }
-    carry = readlane_i(incl, kWave - 1);
-  }
-}
+// ---- shared-prefix (cascade) decode: the prefix half, launched by
+// fe_paged_decode_shared_prefix (paged_decode.hip) and implemented with the
+// prefill kernel (prefill.hip).  Group s is the decode rows group_offsets[s]
+// .. group_offsets[s+1]-1; they share the first prefix_len[s] keys (whole
+// blocks) of row group_offsets[s]'s table.  Output per (row, query head):
+// the attention over the shared keys as fp32 (normalised) plus its base-2
+// LSE, and tok0[b] for every row: the first key its own decode attends (the
+// prefix end, or 0 when the row does not share a prefix). ----
+struct CascadePrefix {
+  const void* q;
+  int64_t q_stride;
+  const void* k_pool;
+  const void* v_pool;
+  int num_blocks;
+  const int32_t* tables;
+  int table_stride;
+  const int32_t* ctx;
+  const int32_t* group_offsets;
+  const int32_t* prefix_len;
+  int num_groups, batch, hq, hkv, d, bs;
+  float scale;
+  int* tickets;      // zero between calls (shared with the decode launch)
+  float* pre_o;      // [batch * hq][d]
+  float* pre_lse;    // [batch * hq]
+  int32_t* tok0;     // [batch]
+  void* scratch;     // key-split partials, cascade_prefix_scratch_bytes
+};
+__attribute__((visibility("hidden"))) size_t cascade_prefix_scratch_bytes(int num_groups,
+                                                                          int batch, int hq,
+                                                                          int hkv, int d);
+__attribute__((visibility("hidden"))) int cascade_prefix_launch(const CascadePrefix& c,
+                                                                hipStream_t stream);
 
 }  // namespace fe
 

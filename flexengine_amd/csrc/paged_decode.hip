@@ -77,6 +77,12 @@ struct DecodeArgs {
   float* ws_o;       // [pieces, Hq, D]
   float* ws_lse;     // [pieces, Hq]  (base 2)
   int* tickets;      // [B, Hkv], zero between calls
+  // shared-prefix decode: sequence b attends only keys tok0[b].. here and
+  // merges the prefix attention (pre_o [B*Hq][D], base-2 pre_lse [B*Hq]) in;
+  // all three null otherwise
+  const int32_t* tok0;
+  const float* pre_o;
+  const float* pre_lse;
   int64_t q_stride;
   int64_t new_stride;
   int W, B, Hq, Hkv, G, BS, bs_log2, NB, target;
@@ -106,7 +112,7 @@ constexpr int kMergeBatch = 16;
 
 template <int D>
 __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, int first,
-                                             int ns) {
+                                             int ns, bool pre = false) {
   const int G = a.G;
   const int n4 = G * D / 4;
   const int o_step = a.Hq * D;  // floats per slot
@@ -147,6 +153,19 @@ __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, 
         den += wv;
       }
       M = newM;
+    }
+    if (pre) {
+      // the shared-prefix part, written by the launch before this one
+      const int64_t r = (int64_t)b * a.Hq + h * G;
+      const float lv = a.pre_lse[r + hh];
+      const f32x4 ov = *reinterpret_cast<const f32x4*>(a.pre_o + r * D + e4 * 4);
+      if (lv != kNegInf) {
+        const float newM = fmaxf(M, lv);
+        const float alpha = M == kNegInf ? 0.f : exp2f(M - newM);
+        num = num * alpha + exp2f(lv - newM) * ov;
+        den = den * alpha + exp2f(lv - newM);
+        M = newM;
+      }
     }
     const float inv = 1.f / den;
     *reinterpret_cast<f16x4*>(a.out + ((int64_t)b * a.Hq + h * G) * D + e4 * 4) =
@@ -189,10 +208,10 @@ void piece_decode_kernel(const DecodeArgs a) {
 
   const int h = blockIdx.x % a.Hkv;
   const int item = blockIdx.x / a.Hkv;
-  const int chunk = split_chunk_quads(a.ctx, a.B, a.max_len, a.target);
+  const int chunk = split_chunk_quads(a.ctx, a.tok0, a.B, a.max_len, a.target);
   Piece pc;
   int total = 0;
-  if (!locate_piece(a.ctx, a.B, a.max_len, chunk, item, pc, total)) {
+  if (!locate_piece(a.ctx, a.tok0, a.B, a.max_len, chunk, item, pc, total)) {
     // spare workgroup: zero rows of inactive sequences
     const int b = item - total;
     if (b < a.B && seq_len(a.ctx, b, a.max_len) == 0) {
@@ -281,7 +300,8 @@ void piece_decode_kernel(const DecodeArgs a) {
     for (int x = 0; x < C::NX; ++x) o[x] = core.o[x];
   }
 
-  const bool split = pc.nsplit > 1;
+  // a sequence with a shared prefix always merges (its prefix part is a partial)
+  const bool split = pc.nsplit > 1 || pc.tok0 > 0;
   f32x4* park = reinterpret_cast<f32x4*>(smem + Lds::park);  // [4][NX][64]
   float* park_m = reinterpret_cast<float*>(smem + Lds::park_m);
   float* park_l = reinterpret_cast<float*>(smem + Lds::park_l);
@@ -353,7 +373,7 @@ void piece_decode_kernel(const DecodeArgs a) {
   if (!*flag) return;
   if (threadIdx.x == 0)
     __hip_atomic_store(a.tickets + b * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  merge_pieces<D>(a, b, h, item - pc.split, pc.nsplit);
+  merge_pieces<D>(a, b, h, item - pc.split, pc.nsplit, pc.tok0 > 0);
 }
 
 // ---- equal-tile ("lean") decode for block sizes divisible by 16 -------------
@@ -795,14 +815,18 @@ extern "C" size_t fe_paged_decode_workspace_size(int batch, int num_q_heads, int
          ws_lse_bytes(batch, num_q_heads, target);
 }
 
-extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
-                               const void* k_new, const void* v_new, int64_t new_batch_stride,
-                               void* k_pool, void* v_pool, int num_blocks,
-                               const int32_t* block_tables, int table_stride,
-                               const int32_t* context_lens, void* workspace,
-                               size_t workspace_bytes, int batch, int num_q_heads, int kv_heads,
-                               int head_dim, int block_size, float scale, int target_splits,
-                               fe_stream_t stream) {
+namespace {
+
+// Everything fe_paged_decode and fe_paged_decode_shared_prefix share: argument
+// checks, workspace carving and the decode launch.  `cascade` (null for plain
+// decode) is filled with the workspace regions of the shared-prefix half and
+// launched first.
+int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_new,
+                const void* v_new, int64_t new_batch_stride, void* k_pool, void* v_pool,
+                int num_blocks, const int32_t* block_tables, int table_stride,
+                const int32_t* context_lens, void* workspace, size_t workspace_bytes, int batch,
+                int num_q_heads, int kv_heads, int head_dim, int block_size, float scale,
+                int target_splits, CascadePrefix* cascade, hipStream_t stream) {
   FE_CHECK_ARG(batch >= 0 && num_q_heads > 0 && kv_heads > 0 && num_blocks > 0 &&
                table_stride > 0 && target_splits >= 0);
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
@@ -812,6 +836,8 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
   if ((int64_t)batch * kv_heads > kMaxTickets) return FE_ERR_UNSUPPORTED;
   const int bs_log2 = log2_exact(block_size);
   if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
+  // the shared-prefix split needs 16-token-aligned suffixes (block-size-16k path)
+  if (cascade && (block_size % kTile != 0 || FE_DECODE_LEAN)) return FE_ERR_UNSUPPORTED;
   if (batch == 0) return FE_OK;
   FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && context_lens);
   FE_CHECK_ARG((k_new == nullptr) == (v_new == nullptr));
@@ -831,7 +857,11 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
   if ((int64_t)(target + batch) * num_q_heads * head_dim * (int64_t)sizeof(float) >= ((int64_t)1 << 31))
     return FE_ERR_UNSUPPORTED;
   const size_t need = fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, max_len, target);
-  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+  const size_t need_all =
+      cascade ? fe_paged_decode_shared_prefix_workspace_size(batch, num_q_heads, kv_heads, head_dim,
+                                                             max_len, cascade->num_groups, target)
+              : need;
+  if (workspace == nullptr || workspace_bytes < need_all || !aligned16(workspace))
     return FE_ERR_WORKSPACE;
 
   DecodeArgs a;
@@ -849,6 +879,9 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
   a.ws_o = (float*)ws;
   ws += ws_o_bytes(batch, num_q_heads, head_dim, target);
   a.ws_lse = (float*)ws;
+  a.tok0 = nullptr;
+  a.pre_o = nullptr;
+  a.pre_lse = nullptr;
   a.q_stride = q_batch_stride;
   a.new_stride = new_batch_stride;
   a.W = table_stride;
@@ -862,8 +895,94 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
   a.target = target;
   a.max_len = max_len;
   a.scale_log2 = scale * kLog2e;
-  if (head_dim == 64) return launch_decode<64>(a, (hipStream_t)stream);
-  return launch_decode<128>(a, (hipStream_t)stream);
+  const hipStream_t s = (hipStream_t)stream;
+  if (cascade) {
+    char* cw = (char*)workspace + need;
+    CascadePrefix& c = *cascade;
+    c.q = q;
+    c.q_stride = q_batch_stride;
+    c.k_pool = k_pool;
+    c.v_pool = v_pool;
+    c.num_blocks = num_blocks;
+    c.tables = block_tables;
+    c.table_stride = table_stride;
+    c.ctx = context_lens;
+    c.batch = batch;
+    c.hq = num_q_heads;
+    c.hkv = kv_heads;
+    c.d = head_dim;
+    c.bs = block_size;
+    c.scale = scale;
+    c.tickets = a.tickets;  // each launch leaves the tickets it used at zero
+    c.tok0 = (int32_t*)cw;
+    cw += align256((size_t)batch * sizeof(int32_t));
+    c.pre_o = (float*)cw;
+    cw += align256((size_t)batch * num_q_heads * head_dim * sizeof(float));
+    c.pre_lse = (float*)cw;
+    cw += align256((size_t)batch * num_q_heads * sizeof(float));
+    c.scratch = cw;
+    const int rc = cascade_prefix_launch(c, s);
+    if (rc != FE_OK) return rc;
+    a.tok0 = c.tok0;
+    a.pre_o = c.pre_o;
+    a.pre_lse = c.pre_lse;
+  }
+  if (head_dim == 64) return launch_decode<64>(a, s);
+  return launch_decode<128>(a, s);
+}
+
+}  // namespace
+
+extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
+                               const void* k_new, const void* v_new, int64_t new_batch_stride,
+                               void* k_pool, void* v_pool, int num_blocks,
+                               const int32_t* block_tables, int table_stride,
+                               const int32_t* context_lens, void* workspace,
+                               size_t workspace_bytes, int batch, int num_q_heads, int kv_heads,
+                               int head_dim, int block_size, float scale, int target_splits,
+                               fe_stream_t stream) {
+  return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
+                     num_blocks, block_tables, table_stride, context_lens, workspace,
+                     workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
+                     target_splits, nullptr, (hipStream_t)stream);
+}
+
+extern "C" size_t fe_paged_decode_shared_prefix_workspace_size(int batch, int num_q_heads,
+                                                               int kv_heads, int head_dim,
+                                                               int max_context, int num_groups,
+                                                               int target_splits) {
+  if (batch < 0 || num_q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || max_context < 0 ||
+      num_groups < 0 || target_splits < 0 || num_q_heads % kv_heads)
+    return 0;
+  return fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, max_context, target_splits) +
+         align256((size_t)batch * sizeof(int32_t)) +
+         align256((size_t)batch * num_q_heads * head_dim * sizeof(float)) +
+         align256((size_t)batch * num_q_heads * sizeof(float)) +
+         cascade_prefix_scratch_bytes(num_groups, batch, num_q_heads, kv_heads, head_dim);
+}
+
+extern "C" int fe_paged_decode_shared_prefix(
+    const void* q, int64_t q_batch_stride, void* out, const void* k_new, const void* v_new,
+    int64_t new_batch_stride, void* k_pool, void* v_pool, int num_blocks,
+    const int32_t* block_tables, int table_stride, const int32_t* context_lens,
+    const int32_t* group_offsets, const int32_t* group_prefix_lens, int num_groups,
+    void* workspace, size_t workspace_bytes, int batch, int num_q_heads, int kv_heads,
+    int head_dim, int block_size, float scale, int target_splits, fe_stream_t stream) {
+  FE_CHECK_ARG(num_groups >= 0 && num_groups <= batch + 1);
+  if (num_groups == 0 || batch == 0)
+    return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
+                       num_blocks, block_tables, table_stride, context_lens, workspace,
+                       workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
+                       target_splits, nullptr, (hipStream_t)stream);
+  FE_CHECK_ARG(group_offsets && group_prefix_lens);
+  CascadePrefix c{};
+  c.group_offsets = group_offsets;
+  c.prefix_len = group_prefix_lens;
+  c.num_groups = num_groups;
+  return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
+                     num_blocks, block_tables, table_stride, context_lens, workspace,
+                     workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
+                     target_splits, &c, (hipStream_t)stream);
 }
 
 extern "C" int fe_lse_merge(const float* part_out, const float* part_lse, int num_splits,

@@ -45,6 +45,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kBlockKeys = 32;  // one 16x16x32 PV step per block
+constexpr int kMaxSplits = 8;   // key splits per row block (plan() clamps to it)
 
 template <int D, int RT>
 struct PCfg {
@@ -71,8 +72,19 @@ struct PrefillArgs {
   float* part_o;     // [KS][total_q * Hq][D] normalised partial outputs (KS > 1)
   float* part_lse;   // [KS][total_q * Hq] base-2 LSE of each partial
   int* tickets;      // [row blocks * Hkv], zero between calls
+  int64_t q_stride;  // elements from one query row (token or sequence) to the next
   int W, S, total_q, Hq, Hkv, G, BS, bs_log2, NB, KS;
   float scale_log2;
+  // shared-prefix (cascade) mode: "sequence" s is a group of decode rows
+  // q_off[s] .. q_off[s+1]-1 sharing the first prefix_len[s] keys of row
+  // q_off[s]'s table; the result per (row, query head) is an fp32 output
+  // normalised over those keys plus its base-2 LSE (pre_o, pre_lse), and
+  // tok0[b] (for every decode row b < total_q) receives the first key the
+  // row's own decode still has to attend.
+  const int32_t* prefix_len;
+  float* pre_o;      // [total_q * Hq][D]
+  float* pre_lse;    // [total_q * Hq]
+  int32_t* tok0;     // [total_q]
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -86,8 +98,20 @@ struct RowBlock {
   int ctx;    // context length (cached + new)
 };
 
+// Shared prefix of group s as the kernels use it: whole blocks only.
+__device__ __forceinline__ int group_prefix(const PrefillArgs& a, int s) {
+  return clamp_len(a.prefix_len[s]) & ~(a.BS - 1);
+}
+
+// Context length of decode row b in cascade mode, clamped to what the table
+// addresses (the decode kernel clamps the same way).
+__device__ __forceinline__ int member_len(const PrefillArgs& a, int b) {
+  const int L = clamp_len(a.ctx[b]);
+  return L < a.W * a.BS ? L : a.W * a.BS;
+}
+
 // Maps a workgroup id onto (sequence, row block); false past the last block.
-template <int ROWS>
+template <int ROWS, bool CASCADE>
 __device__ __forceinline__ bool locate_rows(const PrefillArgs& a, int item, RowBlock& rb) {
   const int lane = lane_id();
   int carry = 0;
@@ -95,8 +119,10 @@ __device__ __forceinline__ bool locate_rows(const PrefillArgs& a, int item, RowB
     const int s = base + lane;
     int q0 = 0, n = 0;
     if (s < a.S) {
-      q0 = a.q_off[s];
-      n = a.q_off[s + 1] - q0;
+      // rows outside [0, total_q) are dropped: every row the kernel touches
+      // (q, out, the context and table of a decode row) stays in its array
+      q0 = min(max(a.q_off[s], 0), a.total_q);
+      n = min(a.q_off[s + 1], a.total_q) - q0;
       n = n > 0 ? n : 0;
     }
     const int nb = (n * a.G + ROWS - 1) / ROWS;
@@ -109,7 +135,8 @@ __device__ __forceinline__ bool locate_rows(const PrefillArgs& a, int item, RowB
       rb.rb = item - readlane_i(excl, src);
       rb.n = readlane_i(n, src);
       rb.q0 = readlane_i(q0, src);
-      rb.ctx = __builtin_amdgcn_readfirstlane(clamp_len(a.ctx[rb.s]));
+      rb.ctx = __builtin_amdgcn_readfirstlane(CASCADE ? group_prefix(a, rb.s)
+                                                      : clamp_len(a.ctx[rb.s]));
       return true;
     }
     carry = readlane_i(incl, kWave - 1);
@@ -121,14 +148,36 @@ __device__ __forceinline__ f32x4 mfma32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-template <int D, int RT>
+// Cascade mode: the decode row b shares group s's prefix when its context
+// reaches past it; its own decode then starts at the prefix end.  Written by
+// the first workgroup for every decode row (0 = no shared prefix).
+__device__ void write_suffix_starts(const PrefillArgs& a) {
+  for (int b = threadIdx.x; b < a.total_q; b += kThreads) {
+    int lo = 0, hi = a.S;  // last group s with q_off[s] <= b
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) / 2;
+      if (a.q_off[mid] <= b) lo = mid; else hi = mid;
+    }
+    int t = 0;
+    if (a.S > 0 && a.q_off[lo] <= b && b < a.q_off[lo + 1]) {
+      const int pl = group_prefix(a, lo);
+      t = member_len(a, b) > pl ? pl : 0;
+    }
+    a.tok0[b] = t;
+  }
+}
+
+template <int D, int RT, bool CASCADE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void prefill_kernel(const PrefillArgs a) {
   using P = PCfg<D, RT>;
   extern __shared__ __align__(16) unsigned char smem[];
 
+  if constexpr (CASCADE) {
+    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) write_suffix_starts(a);
+  }
   RowBlock rb;
-  if (!locate_rows<P::ROWS>(a, blockIdx.x, rb)) return;
+  if (!locate_rows<P::ROWS, CASCADE>(a, blockIdx.x, rb)) return;
   const int h = blockIdx.y;
   const int G = a.G;
   const int tid = threadIdx.x;
@@ -138,10 +187,11 @@ void prefill_kernel(const PrefillArgs a) {
   const int n = lane & 15;
 
   const int total_rows = rb.n * G;
-  const int cached = rb.ctx >= rb.n ? rb.ctx - rb.n : 0;
+  const int cached = CASCADE ? 0 : (rb.ctx >= rb.n ? rb.ctx - rb.n : 0);
   const int r0 = rb.rb * P::ROWS;
   const int r_last = min(r0 + P::ROWS, total_rows) - 1;
-  const int key_end = cached + r_last / G + 1;                   // keys the row block reads
+  // keys the row block reads: causal up to its last position, or the prefix
+  const int key_end = CASCADE ? rb.ctx : cached + r_last / G + 1;
   // split ks of KS takes an equal share of the row block's key blocks
   const int ks = blockIdx.z;
   const int nblocks_all = (key_end + kBlockKeys - 1) / kBlockKeys;
@@ -149,26 +199,41 @@ void prefill_kernel(const PrefillArgs a) {
   const int kb_lo = min(ks * per_split, nblocks_all);
   const int kb_hi = min(kb_lo + per_split, nblocks_all);
   const int wr0 = r0 + w * 16 * RT;                               // first row of this wave
-  const int wave_pos_lo = cached + min(wr0, r_last) / G;          // its smallest position
-  // blocks whose last key is <= every row's position need no causal mask
-  const int unmasked_blocks = (wave_pos_lo + 1) / kBlockKeys;
 
-  // ---- this lane's rows: query vectors (B operand), positions ----
+  // ---- this lane's rows: query vectors (B operand), last key each may see
+  //      (its position; in cascade mode the prefix end, or -1 for a row whose
+  //      context does not reach past the prefix) ----
   f16x8 qv[RT][P::NC];
   int pos[RT];
   bool valid[RT];
+  int pos_lo = 0x7fffffff;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int row = wr0 + 16 * rt + n;
     valid[rt] = row < total_rows;
     const int rc = valid[rt] ? row : r_last;
-    pos[rt] = valid[rt] ? cached + rc / G : -1;
-    const f16* qrow = a.q + ((int64_t)(rb.q0 + rc / G) * a.Hq + h * G + rc % G) * D + 8 * g;
+    if constexpr (CASCADE) {
+      const int L = member_len(a, rb.q0 + rc / G);
+      pos[rt] = valid[rt] && L > rb.ctx ? rb.ctx - 1 : -1;
+    } else {
+      pos[rt] = valid[rt] ? cached + rc / G : -1;
+    }
+    if (valid[rt]) pos_lo = min(pos_lo, pos[rt]);
+    const f16* qrow = a.q + (int64_t)(rb.q0 + rc / G) * a.q_stride + (h * G + rc % G) * D + 8 * g;
 #pragma unroll
     for (int c = 0; c < P::NC; ++c) {
       const f16x8 v = ld16(qrow + 32 * c);
       qv[rt][c] = valid[rt] ? v : f16x8{};
     }
+  }
+
+  // blocks whose last key is <= every row's position need no mask
+  int unmasked_blocks;
+  if constexpr (CASCADE) {
+    pos_lo = -wave_max_i(-min(pos_lo, rb.ctx));
+    unmasked_blocks = __builtin_amdgcn_readfirstlane((pos_lo + 1) / kBlockKeys);
+  } else {
+    unmasked_blocks = (cached + min(wr0, r_last) / G + 1) / kBlockKeys;
   }
 
   float m_run[RT], l_run[RT];
@@ -185,7 +250,7 @@ void prefill_kernel(const PrefillArgs a) {
   //      t / CPR + KPL * i; keys at or past key_end are zero-filled.  The
   //      block ids a block needs are fetched one iteration before its K/V
   //      loads, so no table access sits in front of a K/V load. ----
-  const int32_t* trow = a.tables + (int64_t)rb.s * a.W;
+  const int32_t* trow = a.tables + (int64_t)(CASCADE ? rb.q0 : rb.s) * a.W;
   const int chunk = tid % P::CPR;
   const int krow = tid / P::CPR;
   f16x8 kst[P::LOADS], vst[P::LOADS];
@@ -320,6 +385,12 @@ void prefill_kernel(const PrefillArgs a) {
   //      (device-coherent stores), draw a ticket; the last split of the row
   //      block merges all of them.  Lane (g,n) holds O[row n][dims 16x+4g+i]. ----
   const bool split = a.KS > 1;
+  const int64_t split_stride = (int64_t)a.total_q * a.Hq;  // rows per split
+  // (only used when split; the host keeps KS * rows * D floats under 2 GiB)
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      a.part_o, 0, split ? (int)(a.KS * split_stride * D * 4) : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
+      a.part_lse, 0, split ? (int)(a.KS * split_stride * 4) : 0, 0x00020000);
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     float l = l_run[rt] + shfl_xor_f(l_run[rt], 16);
@@ -328,7 +399,12 @@ void prefill_kernel(const PrefillArgs a) {
     const int row = wr0 + 16 * rt + n;
     const int64_t orow_idx = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    if (!split) {
+    if (CASCADE && !split) {
+      float* orow = a.pre_o + orow_idx * D + 4 * g;
+#pragma unroll
+      for (int x = 0; x < P::NX; ++x) *reinterpret_cast<f32x4*>(orow + 16 * x) = o[rt][x] * inv;
+      if (g == 0) a.pre_lse[orow_idx] = l > 0.f ? m_run[rt] + log2f(l) : kNegInf;
+    } else if (!split) {
       f16* orow = a.out + orow_idx * D + 4 * g;
 #pragma unroll
       for (int x = 0; x < P::NX; ++x)
@@ -336,16 +412,18 @@ void prefill_kernel(const PrefillArgs a) {
             f16x4{(f16)(o[rt][x][0] * inv), (f16)(o[rt][x][1] * inv),
                   (f16)(o[rt][x][2] * inv), (f16)(o[rt][x][3] * inv)};
     } else {
-      const int64_t prow = (int64_t)ks * a.total_q * a.Hq + orow_idx;
-      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-          a.part_o + prow * D, 0, D * (int)sizeof(float), 0x00020000);
+      // device-coherent stores through one wave-uniform descriptor per array
+      // (the host keeps the partial arrays under 2 GiB)
+      const uint32_t prow = (uint32_t)((int64_t)ks * a.total_q * a.Hq + orow_idx);
 #pragma unroll
       for (int x = 0; x < P::NX; ++x)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[rt][x] * inv), r,
-                                               (uint32_t)((16 * x + 4 * g) * sizeof(float)), 0, kSc1);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[rt][x] * inv), ro,
+                                               (prow * D + 16 * x + 4 * g) * (uint32_t)sizeof(float),
+                                               0, kSc1);
       if (g == 0)
-        __hip_atomic_store(a.part_lse + prow, l > 0.f ? m_run[rt] + log2f(l) : kNegInf,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_raw_buffer_store_b32(
+            __builtin_bit_cast(uint32_t, l > 0.f ? m_run[rt] + log2f(l) : kNegInf), rl,
+            prow * (uint32_t)sizeof(float), 0, kSc1);
     }
   }
   if (!split) return;
@@ -360,34 +438,47 @@ void prefill_kernel(const PrefillArgs a) {
   if (tid == 0)
     __hip_atomic_store(a.tickets + blockIdx.x * a.Hkv + h, 0, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
-  // merge: thread -> (row of the block, 4 consecutive dims)
-  const int64_t split_stride = (int64_t)a.total_q * a.Hq;
-  for (int u = tid; u < P::ROWS * (D / 4); u += kThreads) {
-    const int row = r0 + u / (D / 4);
-    if (row > r_last) break;
-    const int d4 = (u % (D / 4)) * 4;
+  // merge: thread -> (row of the block, 4 consecutive dims).  All KS LSEs and
+  // partial outputs of a row are loaded at once (indices past KS repeat the
+  // last split and get weight 0), so a row costs one round trip to memory.
+  constexpr int TPR = D / 4;             // threads per row
+  constexpr int RPS = kThreads / TPR;    // rows per pass
+  const int d4 = (tid % TPR) * 4;
+  for (int row = r0 + tid / TPR; row <= r_last; row += RPS) {
     const int64_t orow_idx = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
+    float lse[kMaxSplits];
+    f32x4 ov[kMaxSplits];
+#pragma unroll
+    for (int k = 0; k < kMaxSplits; ++k) {
+      const int kc = k < a.KS ? k : a.KS - 1;
+      const uint32_t prow = (uint32_t)(kc * split_stride + orow_idx);
+      lse[k] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rl, prow * (uint32_t)sizeof(float), 0, kSc1));
+      ov[k] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     ro, (prow * D + d4) * (uint32_t)sizeof(float), 0, kSc1));
+    }
     float M = kNegInf;
-    for (int k = 0; k < a.KS; ++k)
-      M = fmaxf(M, __hip_atomic_load(a.part_lse + k * split_stride + orow_idx, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT));
+#pragma unroll
+    for (int k = 0; k < kMaxSplits; ++k)
+      if (k < a.KS) M = fmaxf(M, lse[k]);
     f32x4 num = {0.f, 0.f, 0.f, 0.f};
     float den = 0.f;
-    for (int k = 0; k < a.KS; ++k) {
-      const int64_t prow = k * split_stride + orow_idx;
-      const float lse = __hip_atomic_load(a.part_lse + prow, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-      if (lse == kNegInf) continue;
-      const float wgt = exp2f(lse - M);
-      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-          a.part_o + prow * D, 0, D * (int)sizeof(float), 0x00020000);
-      num += wgt * __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                 r, (uint32_t)(d4 * sizeof(float)), 0, kSc1));
+#pragma unroll
+    for (int k = 0; k < kMaxSplits; ++k) {
+      const float wgt = k < a.KS && lse[k] != kNegInf ? exp2f(lse[k] - M) : 0.f;
+      num += wgt * ov[k];
       den += wgt;
     }
     const float inv = den > 0.f ? 1.f / den : 0.f;
-    *reinterpret_cast<f16x4*>(a.out + orow_idx * D + d4) =
-        f16x4{(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv), (f16)(num[3] * inv)};
+    if constexpr (CASCADE) {
+      *reinterpret_cast<f32x4*>(a.pre_o + orow_idx * D + d4) = num * inv;
+      if (d4 == 0) a.pre_lse[orow_idx] = den > 0.f ? M + log2f(den) : kNegInf;
+    } else {
+      *reinterpret_cast<f16x4*>(a.out + orow_idx * D + d4) =
+          f16x4{(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
+                (f16)(num[3] * inv)};
+    }
   }
 }
 
@@ -399,10 +490,10 @@ inline int log2_exact(int x) {
   return l;
 }
 
-template <int D, int RT>
+template <int D, int RT, bool CASCADE = false>
 void launch_prefill(const PrefillArgs& a, int blocks, hipStream_t stream) {
   using P = PCfg<D, RT>;
-  hipLaunchKernelGGL((prefill_kernel<D, RT>), dim3(blocks, a.Hkv, a.KS), dim3(kThreads),
+  hipLaunchKernelGGL((prefill_kernel<D, RT, CASCADE>), dim3(blocks, a.Hkv, a.KS), dim3(kThreads),
                      2 * P::STAGE, stream, a);
 }
 
@@ -425,7 +516,11 @@ inline Plan plan(int num_seqs, int total_q, int num_q_heads, int kv_heads) {
   p.blocks = (int)(((int64_t)total_q * G + per - 1) / per) + num_seqs;
   const int64_t wgs = (int64_t)((rows + per - 1) / per) * 1;
   int ks = (int)((1024 + wgs - 1) / (wgs > 0 ? wgs : 1));
-  p.ks = ks < 1 ? 1 : (ks > 8 ? 8 : ks);
+  p.ks = ks < 1 ? 1 : (ks > kMaxSplits ? kMaxSplits : ks);
+  // the split partials are addressed with 32-bit offsets (at most ~128K rows
+  // split at all, ~256 MB)
+  if (p.ks > 1 && (int64_t)p.ks * rows * 128 * (int64_t)sizeof(float) >= ((int64_t)1 << 31))
+    p.ks = 1;
   return p;
 }
 
@@ -489,6 +584,11 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   a.NB = num_blocks;
   a.KS = p.ks;
   a.scale_log2 = scale * kLog2e;
+  a.q_stride = (int64_t)num_q_heads * head_dim;
+  a.prefix_len = nullptr;
+  a.pre_o = nullptr;
+  a.pre_lse = nullptr;
+  a.tok0 = nullptr;
   hipStream_t s = (hipStream_t)stream;
   if (head_dim == 64) {
     if (p.rt == 2) launch_prefill<64, 2>(a, p.blocks, s); else launch_prefill<64, 1>(a, p.blocks, s);
@@ -497,3 +597,56 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   }
   return FE_LAUNCH_STATUS();
 }
+
+namespace fe {
+
+size_t cascade_prefix_scratch_bytes(int num_groups, int batch, int hq, int hkv, int d) {
+  const Plan p = plan(num_groups, batch, hq, hkv);
+  if (p.ks == 1) return 0;
+  const size_t rows = (size_t)p.ks * batch * hq;
+  return align256(rows * d * sizeof(float)) + align256(rows * sizeof(float));
+}
+
+int cascade_prefix_launch(const CascadePrefix& c, hipStream_t stream) {
+  const Plan p = plan(c.num_groups, c.batch, c.hq, c.hkv);
+  if ((int64_t)p.blocks * c.hkv > kMaxTickets) return FE_ERR_UNSUPPORTED;
+  PrefillArgs a;
+  a.q = (const f16*)c.q;
+  a.out = nullptr;
+  a.k_pool = (const f16*)c.k_pool;
+  a.v_pool = (const f16*)c.v_pool;
+  a.tables = c.tables;
+  a.q_off = c.group_offsets;
+  a.ctx = c.ctx;
+  a.tickets = c.tickets;
+  const size_t rows = (size_t)p.ks * c.batch * c.hq;
+  a.part_o = (float*)c.scratch;
+  a.part_lse = p.ks > 1 ? (float*)((char*)c.scratch + align256(rows * c.d * sizeof(float)))
+                        : nullptr;
+  a.q_stride = c.q_stride;
+  a.W = c.table_stride;
+  a.S = c.num_groups;
+  a.total_q = c.batch;
+  a.Hq = c.hq;
+  a.Hkv = c.hkv;
+  a.G = c.hq / c.hkv;
+  a.BS = c.bs;
+  a.bs_log2 = log2_exact(c.bs);
+  a.NB = c.num_blocks;
+  a.KS = p.ks;
+  a.scale_log2 = c.scale * kLog2e;
+  a.prefix_len = c.prefix_len;
+  a.pre_o = c.pre_o;
+  a.pre_lse = c.pre_lse;
+  a.tok0 = c.tok0;
+  if (c.d == 64) {
+    if (p.rt == 2) launch_prefill<64, 2, true>(a, p.blocks, stream);
+    else launch_prefill<64, 1, true>(a, p.blocks, stream);
+  } else {
+    if (p.rt == 2) launch_prefill<128, 2, true>(a, p.blocks, stream);
+    else launch_prefill<128, 1, true>(a, p.blocks, stream);
+  }
+  return FE_LAUNCH_STATUS();
+}
+
+}  // namespace fe

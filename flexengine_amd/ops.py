@@ -150,18 +150,8 @@ def decode_workspace(device: torch.device, nbytes: int, kind: str = "decode") ->
     return ws
 
 
-def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
-                 block_tables: torch.Tensor, context_lens: torch.Tensor, *,
-                 scale: float | None = None, k_new: torch.Tensor | None = None,
-                 v_new: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                 workspace: torch.Tensor | None = None, target_splits: int = 0) -> torch.Tensor:
-    """Single-token paged decode attention over one layer's pools.
-
-    q [B, Hq, D] fp16 (rows may be strided, heads contiguous); pools
-    [NB, BS, Hkv, D]; block_tables int32 [B, W]; context_lens int32 [B]
-    (0 = inactive row -> zeros).  With k_new/v_new ([B, Hkv, D]) the new token's
-    K/V are written to the pool at position context_lens-1 in the same launch.
-    """
+def _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_new, out):
+    """Checks of the decode entry points; returns the normalised arguments."""
     dev = _require_gpu(q, k_pool, v_pool, block_tables, context_lens, k_new, v_new, out)
     nb, bs, hkv, d = _check_pool(k_pool, v_pool)
     if q.ndim != 3 or q.shape[2] != d or q.dtype != FP16:
@@ -192,12 +182,71 @@ def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
         raise ValueError("out must be a contiguous float16 [batch, num_q_heads, head_dim]")
     if scale is None:
         scale = 1.0 / math.sqrt(d)
+    return dev, nb, bs, hkv, d, batch, hq, block_tables, context_lens, new_stride, out, scale
+
+
+def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                 block_tables: torch.Tensor, context_lens: torch.Tensor, *,
+                 scale: float | None = None, k_new: torch.Tensor | None = None,
+                 v_new: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                 workspace: torch.Tensor | None = None, target_splits: int = 0) -> torch.Tensor:
+    """Single-token paged decode attention over one layer's pools.
+
+    q [B, Hq, D] fp16 (rows may be strided, heads contiguous); pools
+    [NB, BS, Hkv, D]; block_tables int32 [B, W]; context_lens int32 [B]
+    (0 = inactive row -> zeros).  With k_new/v_new ([B, Hkv, D]) the new token's
+    K/V are written to the pool at position context_lens-1 in the same launch.
+    """
+    (dev, nb, bs, hkv, d, batch, hq, block_tables, context_lens, new_stride, out,
+     scale) = _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_new, out)
     need = decode_workspace_bytes(batch, hq, d, block_tables.shape[1] * bs, target_splits)
     if workspace is None:
         workspace = decode_workspace(dev, need)
     _lib.call("fe_paged_decode", q.data_ptr(), q.stride(0), out.data_ptr(), _ptr(k_new),
               _ptr(v_new), new_stride, k_pool.data_ptr(), v_pool.data_ptr(), nb,
               block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(),
+              workspace.data_ptr(), workspace.numel() * workspace.element_size(), batch, hq, hkv,
+              d, bs, float(scale), int(target_splits), _stream(dev))
+    return out
+
+
+def paged_decode_shared_prefix(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                               block_tables: torch.Tensor, context_lens: torch.Tensor,
+                               group_offsets: torch.Tensor, group_prefix_lens: torch.Tensor, *,
+                               scale: float | None = None, k_new: torch.Tensor | None = None,
+                               v_new: torch.Tensor | None = None,
+                               out: torch.Tensor | None = None,
+                               workspace: torch.Tensor | None = None,
+                               target_splits: int = 0) -> torch.Tensor:
+    """paged_decode for a batch whose sequences form groups sharing prefix blocks.
+
+    Group s is the batch rows group_offsets[s] .. group_offsets[s+1]-1 (int32
+    [S+1], ascending; rows outside every group decode normally); its first
+    group_prefix_lens[s] keys (int32 [S], rounded down to whole blocks) are the
+    blocks at the start of row group_offsets[s]'s table, shared by every member.
+    Same result as paged_decode: the shared keys are attended once per group,
+    the private suffixes per row, merged by log-sum-exp (fe_paged_decode_shared_prefix).
+    """
+    (dev, nb, bs, hkv, d, batch, hq, block_tables, context_lens, new_stride, out,
+     scale) = _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_new, out)
+    group_offsets = _int32(group_offsets, "group_offsets")
+    group_prefix_lens = _int32(group_prefix_lens, "group_prefix_lens")
+    if group_offsets.ndim != 1 or group_prefix_lens.ndim != 1 or \
+            group_offsets.shape[0] != group_prefix_lens.shape[0] + 1:
+        raise ValueError("group_offsets must be [S+1] and group_prefix_lens [S]")
+    if group_offsets.device != dev or group_prefix_lens.device != dev:
+        raise ValueError("group arrays must be on the GPU")
+    ngroups = group_prefix_lens.shape[0]
+    need = int(_lib.load().fe_paged_decode_shared_prefix_workspace_size(
+        batch, hq, hkv, d, block_tables.shape[1] * bs, ngroups, int(target_splits)))
+    if workspace is None:
+        workspace = decode_workspace(dev, need)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace too small: need {need} bytes")
+    _lib.call("fe_paged_decode_shared_prefix", q.data_ptr(), q.stride(0), out.data_ptr(),
+              _ptr(k_new), _ptr(v_new), new_stride, k_pool.data_ptr(), v_pool.data_ptr(), nb,
+              block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(),
+              group_offsets.data_ptr(), group_prefix_lens.data_ptr(), ngroups,
               workspace.data_ptr(), workspace.numel() * workspace.element_size(), batch, hq, hkv,
               d, bs, float(scale), int(target_splits), _stream(dev))
     return out

@@ -147,6 +147,85 @@ def make_decode_workload(name: str, seed: int, batch: int, hq: int, hkv: int, d:
                           unique_tokens=int(ctx.sum()), meta={"seed": seed})
 
 
+def shared_prefix_workload(seed: int, groups: list[tuple[int, int]], singles: int = 0,
+                           hq: int = 12, hkv: int = 2, d: int = 128, block_size: int = 16,
+                           tail: tuple[int, int] = (1, 300),
+                           member_lens: dict[int, int] | None = None,
+                           with_new_kv: bool = False) -> DecodeWorkload:
+    """Decode rows in groups that share prefix blocks, then rows of their own.
+
+    groups: (members, prefix_tokens) per group; the group's first
+    prefix_tokens // block_size blocks are shared by all its members (a prefix
+    that is not a whole number of blocks shares only the whole blocks, as
+    FlexEngine's prefix cache does), each member continues with a private tail
+    of U{tail} tokens.  member_lens overrides the length of batch row b (a
+    context that ends inside the prefix, or 0 = inactive).  `singles` rows with
+    no shared prefix follow the groups.  meta holds group_offsets and
+    prefix_lens (the prefix_tokens as given) for fe_paged_decode_shared_prefix.
+    """
+    gen = torch.Generator().manual_seed(seed)
+    member_lens = member_lens or {}
+    lengths, shared_of = [], []
+    offsets = [0]
+    for g, (m, p) in enumerate(groups):
+        shared = p // block_size * block_size
+        for _ in range(m):
+            b = len(lengths)
+            t = int(torch.randint(tail[0], tail[1] + 1, (1,), generator=gen))
+            lengths.append(member_lens.get(b, shared + t))
+            shared_of.append(g)
+        offsets.append(len(lengths))
+    for _ in range(singles):
+        b = len(lengths)
+        t = int(torch.randint(tail[0], tail[1] + 1, (1,), generator=gen))
+        lengths.append(member_lens.get(b, t))
+        shared_of.append(-1)
+    batch = len(lengths)
+    shared_pages = [p // block_size for _, p in groups]
+    # pages each row owns privately (beyond its group's shared pages)
+    own = []
+    for b, n in enumerate(lengths):
+        sp = shared_pages[shared_of[b]] if shared_of[b] >= 0 else 0
+        own.append(max(0, math.ceil(n / block_size) - sp))
+    nb = sum(shared_pages) + sum(own) + 1
+    width = max(1, max((shared_pages[shared_of[b]] if shared_of[b] >= 0 else 0) + own[b]
+                       for b in range(batch)))
+    q = _randn(gen, batch, hq, d)
+    k_pool = _randn(gen, nb, block_size, hkv, d)
+    v_pool = _randn(gen, nb, block_size, hkv, d)
+    perm = torch.randperm(nb, generator=gen).to(torch.int32)
+    tables = torch.zeros((batch, width), dtype=torch.int32)
+    at = 0
+    group_blocks = []
+    for sp in shared_pages:
+        group_blocks.append(perm[at:at + sp])
+        at += sp
+    for b in range(batch):
+        row = []
+        if shared_of[b] >= 0:
+            row.extend(group_blocks[shared_of[b]].tolist())
+        row.extend(perm[at:at + own[b]].tolist())
+        at += own[b]
+        if not row:
+            row = [int(perm[-1])]
+        tables[b, :len(row)] = torch.tensor(row, dtype=torch.int32)
+        tables[b, len(row):] = row[-1]
+    k_new = v_new = None
+    if with_new_kv:
+        k_new = _randn(gen, batch, hkv, d)
+        v_new = _randn(gen, batch, hkv, d)
+    ctx = torch.tensor(lengths, dtype=torch.int32)
+    unique = sum(sp * block_size for sp in shared_pages) + sum(
+        max(0, n - (shared_pages[shared_of[b]] * block_size if shared_of[b] >= 0 else 0))
+        for b, n in enumerate(lengths))
+    return DecodeWorkload("shared-prefix", q, k_pool, v_pool, tables, ctx, k_new, v_new,
+                          unique_tokens=unique,
+                          meta={"seed": seed,
+                                "group_offsets": torch.tensor(offsets, dtype=torch.int32),
+                                "prefix_lens": torch.tensor([p for _, p in groups],
+                                                            dtype=torch.int32)})
+
+
 def c1_workload() -> DecodeWorkload:
     """C1: Qwen2.5-0.5B heads (14/2/64), B=8, L ~ U{16..512}, 256-block pool."""
     gen = torch.Generator().manual_seed(1)
@@ -197,7 +276,10 @@ def c3_workload(groups: int = 8, per_group: int = 32, prefix: int = 2048) -> Dec
     return DecodeWorkload("C3", q, k_pool, v_pool, tables, ctx, None, None,
                           unique_tokens=groups * prefix + sum(tails),
                           meta={"seed": 3, "groups": groups, "per_group": per_group,
-                                "prefix": prefix})
+                                "prefix": prefix,
+                                "group_offsets": torch.arange(0, batch + 1, per_group,
+                                                              dtype=torch.int32),
+                                "prefix_lens": torch.full((groups,), prefix, dtype=torch.int32)})
 
 
 def c4_workload() -> PrefillWorkload:

@@ -142,6 +142,47 @@ int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
                     fe_stream_t stream);
 
 /*
+ * Bytes of device workspace fe_paged_decode_shared_prefix needs; zero-filled
+ * before first use, reusable like fe_paged_decode's.
+ */
+size_t fe_paged_decode_shared_prefix_workspace_size(int batch, int num_q_heads, int kv_heads,
+                                                    int head_dim, int max_context,
+                                                    int num_groups, int target_splits);
+
+/*
+ * fe_paged_decode for a batch in which groups of sequences share a prefix
+ * of KV blocks (FlexEngine's prefix cache attaches the same physical blocks
+ * to every request that reuses a prompt: PrefixCache.insert / attach_prefix,
+ * src/flexengine/engine/kv_cache/prefix.py:75-96,
+ * src/flexengine/engine/kv_cache/allocator.py:83-94).  Same result as
+ * fe_paged_decode on the same arguments, computed in cascade:
+ *   group s = sequences group_offsets[s] .. group_offsets[s+1]-1 (device
+ *   arrays; ascending offsets, groups contiguous in the batch), whose first
+ *   P_s = group_prefix_lens[s] keys (rounded down to whole blocks) are the
+ *   blocks of row group_offsets[s]'s table.  The shared keys are attended
+ *   once per group, all members' query heads together (a matrix-core
+ *   product, K/V read once per group instead of once per sequence); each
+ *   sequence's own decode covers only keys P_s .. L-1 and merges the two by
+ *   their log-sum-exp.  A member whose context does not reach past P_s is
+ *   decoded without sharing.  Sequences outside every group are decoded as
+ *   by fe_paged_decode.  The caller guarantees that members' tables really
+ *   hold the group's blocks in their first P_s / block_size entries, and a
+ *   decode-step write (k_new) must not target a shared block (the reference
+ *   refuses such writes, allocator.py:124-125).  Block size a multiple of 16.
+ */
+int fe_paged_decode_shared_prefix(const void* q, int64_t q_batch_stride, void* out,
+                                  const void* k_new, const void* v_new, int64_t new_batch_stride,
+                                  void* k_pool, void* v_pool, int num_blocks,
+                                  const int32_t* block_tables, int table_stride,
+                                  const int32_t* context_lens,
+                                  const int32_t* group_offsets, const int32_t* group_prefix_lens,
+                                  int num_groups,
+                                  void* workspace, size_t workspace_bytes,
+                                  int batch, int num_q_heads, int kv_heads, int head_dim,
+                                  int block_size, float scale, int target_splits,
+                                  fe_stream_t stream);
+
+/*
  * Log-sum-exp merge of split attention results:
  *   LSE[r]   = log(sum_s exp(part_lse[s, r]))
  *   out[r,:] = sum_s exp(part_lse[s, r] - LSE[r]) * part_out[s, r, :]

@@ -90,6 +90,21 @@ def test_host_side_validation_rejects_before_launch(lib):
     assert rc == _lib.FE_ERR_INVALID_ARGUMENT
     rc = lib.fe_write_kv(null, null, 256, null, null, 4, null, null, 3, 2, 128, 16, null)
     assert rc == _lib.FE_ERR_INVALID_ARGUMENT
+    # shared-prefix decode: block size 8 cannot split at 16-token tiles; missing
+    # group arrays; a negative group count
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    rc = lib.fe_paged_decode_shared_prefix(null, 1536, null, null, null, 0, null, null, 1, null, 1,
+                                           null, fake, fake, 1, null, 0, 1, 12, 2, 128, 8, 0.1, 0,
+                                           null)
+    assert rc == _lib.FE_ERR_UNSUPPORTED
+    rc = lib.fe_paged_decode_shared_prefix(null, 1536, null, null, null, 0, null, null, 1, null, 1,
+                                           null, null, null, 1, null, 0, 1, 12, 2, 128, 16, 0.1, 0,
+                                           null)
+    assert rc == _lib.FE_ERR_INVALID_ARGUMENT
+    rc = lib.fe_paged_decode_shared_prefix(null, 1536, null, null, null, 0, null, null, 1, null, 1,
+                                           null, null, null, -1, null, 0, 1, 12, 2, 128, 16, 0.1, 0,
+                                           null)
+    assert rc == _lib.FE_ERR_INVALID_ARGUMENT
     # empty work is a successful no-op
     assert lib.fe_write_kv(null, null, 256, null, null, 4, null, null, 0, 2, 128, 16, null) == 0
     assert lib.fe_lse_merge(null, null, 1, 0, 128, null, null, null) == 0
@@ -107,6 +122,11 @@ def test_workspace_size_grows_with_batch_and_target(lib):
     small = lib.fe_prefill_workspace_size(4, 1377, 12, 2, 128)
     assert big >= 65536 * 4 and small > 65536 * 4
     assert lib.fe_prefill_workspace_size(1, 10, 12, 5, 128) == 0
+    # the shared-prefix decode adds its prefix outputs (and key-split partials)
+    sp = lib.fe_paged_decode_shared_prefix_workspace_size(256, 12, 2, 128, 4096, 8, 0)
+    plain = lib.fe_paged_decode_workspace_size(256, 12, 128, 4096, 0)
+    assert sp >= plain + 256 * 12 * 128 * 4 and sp % 256 == 0
+    assert lib.fe_paged_decode_shared_prefix_workspace_size(256, 12, 5, 128, 4096, 8, 0) == 0
     # very long tables raise the split target (pieces stay <= 4096 keys)
     d = lib.fe_paged_decode_workspace_size(64, 12, 128, 1 << 20, 0)
     assert d > a

@@ -306,3 +306,79 @@ def test_split_merge_repeated_calls_are_stable():
             assert (first[target] == got).all(), "results differ between identical calls"
         else:
             first[target] = got
+
+
+# --------------------------------------------------------------------------------------
+# shared-prefix (cascade) decode: same results as the plain decode on the same tables
+# --------------------------------------------------------------------------------------
+
+def run_shared_prefix(w: workloads.DecodeWorkload, fuse: bool = False, target_splits: int = 0):
+    d = w.to(DEV)
+    out = ops.paged_decode_shared_prefix(
+        d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens,
+        d.meta["group_offsets"].to(DEV), d.meta["prefix_lens"].to(DEV),
+        k_new=d.k_new if fuse else None, v_new=d.v_new if fuse else None,
+        target_splits=target_splits)
+    torch.cuda.synchronize()
+    return out.cpu(), d
+
+
+def test_shared_prefix_c3_shape_matches_oracle_and_plain_decode():
+    w = workloads.c3_workload(groups=2, per_group=8)
+    got, _ = run_shared_prefix(w)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what="cascade C3 (2x8)")
+    plain, _ = run_decode(w)
+    assert_attention_close(got.numpy(), plain.numpy().astype(np.float64), what="cascade vs plain")
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", [(12, 2, 128, 16), (14, 2, 64, 16), (8, 1, 128, 32),
+                                          (16, 4, 64, 16)])
+def test_shared_prefix_edge_cases(hq, hkv, d, bs):
+    """Groups of 3 (prefix 40 tokens: only whole blocks are shared), 1 and 0
+    members, a group of 5 in which one member's context ends exactly at the
+    prefix, one inside it and one is inactive, and rows outside every group."""
+    groups = [(3, 40), (1, 64), (0, 32), (5, 512)]
+    w = workloads.shared_prefix_workload(11, groups, singles=3, hq=hq, hkv=hkv, d=d,
+                                         block_size=bs, member_lens={5: 512, 6: 505, 7: 0})
+    got, _ = run_shared_prefix(w)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what=f"edge cases {hq}/{hkv}/{d} bs{bs}")
+    assert not got[7].any(), "inactive member must give exact zeros"
+
+
+def test_shared_prefix_fused_page_write_is_bit_exact():
+    """The decoded token lies past the shared prefix: written into the member's
+    private block in the same call, byte-exact, and attended."""
+    w = workloads.shared_prefix_workload(12, [(6, 256), (4, 1024)], singles=2, with_new_kv=True,
+                                         tail=(1, 200))
+    got, d = run_shared_prefix(w, fuse=True)
+    exp, kp, vp = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what="cascade + fused write")
+    assert np.array_equal(d.k_pool.cpu().numpy().view(np.int16), kp.view(np.int16))
+    assert np.array_equal(d.v_pool.cpu().numpy().view(np.int16), vp.view(np.int16))
+
+
+def test_shared_prefix_without_groups_is_the_plain_decode():
+    w = workloads.c2_workload(batch=16)
+    d = w.to(DEV)
+    empty = torch.zeros(1, dtype=torch.int32, device=DEV)
+    got = ops.paged_decode_shared_prefix(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens,
+                                         empty, empty[:0])
+    plain = ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens)
+    assert torch.equal(got, plain)
+
+
+def test_shared_prefix_full_c3_against_plain_decode_and_repeatable():
+    """Full C3 (8 groups x 32 sharing 2048 tokens): the cascade agrees with the
+    plain decode to the contract tolerance and is bit-identical across calls."""
+    w = workloads.c3_workload()
+    d = w.to(DEV)
+    go, pl = d.meta["group_offsets"].to(DEV), d.meta["prefix_lens"].to(DEV)
+    outs = [ops.paged_decode_shared_prefix(d.q, d.k_pool, d.v_pool, d.block_tables,
+                                           d.context_lens, go, pl) for _ in range(3)]
+    plain = ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens)
+    torch.cuda.synchronize()
+    assert_attention_close(outs[0].cpu().numpy(), plain.cpu().numpy().astype(np.float64),
+                           what="full C3 cascade vs plain")
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
