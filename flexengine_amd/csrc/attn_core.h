@@ -234,33 +234,36 @@ struct TileCore {
 
 // Fast path for block sizes that are multiples of 16: the 16 keys of a tile
 // share one physical block, so a tile is fully described by wave-uniform
-// values -- the pool row of its first key and its key count.  The wave's tiles
+// values -- the pool row of its first key and its key count.  A wave's tiles
 // form a list held one per lane (lane k: tile k, k < 64), filled from the block
 // tables before the first load, so no table access sits between two tiles'
-// K/V loads.  Consecutive tiles may belong to different sequences: the caller
-// sees every tile end and flushes / resets the accumulators at a sequence
-// boundary (see run()).
+// K/V loads.
 template <int D>
 struct TileListCore {
   using C = TileCfg<D>;
 
   const f16* k_pool;
   const f16* v_pool;
-  f16* k_pool_w;          // writable aliases for the fused page write
-  f16* v_pool_w;
   int rs;                 // elements per pool row (kv_heads * D)
   int hoff;               // kv_head * D
   float scale_log2;
   unsigned char* stage;   // per-wave LDS tile, C::STAGE bytes
+  int ntiles;             // tiles in the list (<= 64)
+  int row_vec;            // lane k < ntiles: pool row (block * BS + offset) of tile k's first key
+  int rows_vec;           // lane k < ntiles: keys in tile k (1..16)
+
+  // The decoded token's K/V row (row new_row of tile new_tile; -1: not in this
+  // list) comes from these registers instead of the pool, so no load waits on
+  // the page write; the caller writes the row to the pool (store_new_row).
+  int new_tile;
+  int new_row;
+  f16x8 knew[C::NK];      // lane (g, n): chunks 4s+g of the new K row
+  f16x8 vnew;             // lane l: chunk l % CPR of the new V row
 
   f16x8 qv[C::NK];
   float m_run;
   float l_run;
   f32x4 o[C::NX];
-
-  int ntiles;             // tiles in the list (<= 64)
-  int row_vec;            // lane k < ntiles: pool row (block * BS + offset) of tile k's first key
-  int rows_vec;           // lane k < ntiles: keys in tile k (1..16)
 
   __device__ __forceinline__ void init_acc() {
     m_run = kNegInf;
@@ -282,13 +285,13 @@ struct TileListCore {
   // Tile loads are raw buffer loads: a scalar descriptor per tile (base = row
   // 0 of the tile for this KV head, extent = the tile's keys) and a
   // loop-invariant 32-bit byte offset per lane.  Rows past the extent read as
-  // zeros, so stale pool contents beyond a context never reach the accumulators.
+  // zeros, so stale pool contents beyond a context never reach the
+  // accumulators, and a tile past the list loads nothing.
   __device__ __forceinline__ uint32_t k_off0() const {
     const int lane = lane_id();
     return (uint32_t)(((lane & 15) * rs + (lane >> 4) * 8) * 2);
   }
   __device__ __forceinline__ static uint32_t k_soff(int s) { return (uint32_t)(s * 64); }
-  __device__ __forceinline__ uint32_t k_off(int s) const { return k_off0() + k_soff(s); }
   __device__ __forceinline__ uint32_t v_off0() const {
     const int lane = lane_id();
     return (uint32_t)(((lane / C::CPR) * rs + (lane % C::CPR) * 8) * 2);
@@ -312,14 +315,10 @@ struct TileListCore {
     return __builtin_amdgcn_make_buffer_rsrc(p, 0, nrec, 0x00020000);
   }
 
-  // Issues the K/V loads of tile k; nothing here waits for data.  Past the end
-  // of the list the descriptors have zero extent and touch no memory.
+  // Issues the K/V loads of tile k; nothing here waits for data.
   __device__ __forceinline__ void load_tile(int k, f16x8 (&kk)[C::NK], f16x8 (&vv)[C::NK]) const {
-    load_at(tile_base(k), tile_rows(k), kk, vv);
-  }
-  // The same for a tile given by its element offset (kv head included) and keys.
-  __device__ __forceinline__ void load_at(int64_t base, int rows, f16x8 (&kk)[C::NK],
-                                          f16x8 (&vv)[C::NK]) const {
+    const int64_t base = tile_base(k);
+    const int rows = tile_rows(k);
     const __amdgpu_buffer_rsrc_t kr = tile_rsrc(k_pool, base, rows);
     const __amdgpu_buffer_rsrc_t vr = tile_rsrc(v_pool, base, rows);
     const uint32_t ko = k_off0();
@@ -330,46 +329,17 @@ struct TileListCore {
     for (int j = 0; j < C::NK; ++j) vv[j] = buf_ld16(vr, vo, v_soff(j));
   }
 
-  // Fused page write of a decoded token (row r of tile k): each lane that will
-  // load a 16-byte chunk of that row first stores the new chunk to the same
-  // address, so its later load (same thread, same address, program order)
-  // returns the new bytes.
-  __device__ __forceinline__ void write_new_row(int k, int r, const f16* knew_row,
-                                                const f16* vnew_row) const {
-    write_new_row_at(tile_base(k), r, knew_row, vnew_row);
-  }
-  __device__ __forceinline__ void write_new_row_at(int64_t base, int r, const f16* knew_row,
-                                                   const f16* vnew_row) const {
+  // One tile held in kk / vv: scores, V staging, softmax and PV.
+  __device__ __forceinline__ void compute_tile(int k, f16x8 (&kk)[C::NK], f16x8 (&vv)[C::NK]) {
     const int lane = lane_id();
-    const int g = lane >> 4;
-    const int n = lane & 15;
-    char* kb = reinterpret_cast<char*>(k_pool_w + base);
-    char* vb = reinterpret_cast<char*>(v_pool_w + base);
-    if (n == r) {
+    const int vrow = lane / C::CPR;
+    if (k == new_tile) {  // wave-uniform: substitute the decoded token's row
+      const bool krow = (lane & 15) == new_row;
 #pragma unroll
-      for (int s = 0; s < C::NK; ++s)
-        *reinterpret_cast<f16x8*>(kb + k_off(s)) = ld16(knew_row + (4 * s + g) * 8);
+      for (int s = 0; s < C::NK; ++s) kk[s] = krow ? knew[s] : kk[s];
+#pragma unroll
+      for (int j = 0; j < C::NK; ++j) vv[j] = j * C::RPI + vrow == new_row ? vnew : vv[j];
     }
-    const int vrow = lane / C::CPR;
-#pragma unroll
-    for (int j = 0; j < C::NK; ++j)
-      if (j * C::RPI + vrow == r)
-        *reinterpret_cast<f16x8*>(vb + v_off0() + v_soff(j)) = ld16(vnew_row + (lane % C::CPR) * 8);
-    // The same lanes load these addresses later: a wave's memory operations to
-    // one address are performed in order, so only the compiler needs holding
-    // back (it may not move the buffer loads above these stores).
-    compiler_fence();
-  }
-
-  __device__ __forceinline__ void compute_tile(int k, const f16x8 (&kk)[C::NK],
-                                               f16x8 (&vv)[C::NK]) {
-    compute_rows(tile_rows(k), kk, vv);
-  }
-  // One tile of `rows` valid keys (1..16) held in kk / vv.
-  __device__ __forceinline__ void compute_rows(int rows, const f16x8 (&kk)[C::NK],
-                                               f16x8 (&vv)[C::NK]) {
-    const int lane = lane_id();
-    const int vrow = lane / C::CPR;
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < C::NK; ++s) {
@@ -387,42 +357,43 @@ struct TileListCore {
       }
     }
     compiler_fence();
-    softmax_pv_tile<D>(sacc, 0, rows, scale_log2, stage, m_run, l_run, o);
+    softmax_pv_tile<D>(sacc, 0, tile_rows(k), scale_log2, stage, m_run, l_run, o);
     compiler_fence();
   }
 
-  // Walks the list with NSTAGE register stages: while tile k is computed, the
-  // loads of tiles k+1 .. k+NSTAGE-1 are in flight.  Loads are issued
-  // unconditionally (zero-extent past the end), so the loop has no join points
-  // and every wait is exact.  After each tile, tile_end(k) runs; it returns
-  // false to stop (it must at k == ntiles - 1).  The prologue loads of the
-  // first NSTAGE-1 tiles are issued by prologue() so the caller can place
-  // other work between them and the loop.
-  template <int NSTAGE>
-  struct Buffers {
-    f16x8 k[NSTAGE][C::NK];
-    f16x8 v[NSTAGE][C::NK];
-  };
-
-  template <int NSTAGE>
-  __device__ __forceinline__ void prologue(Buffers<NSTAGE>& buf) const {
-#pragma unroll
-    for (int u = 0; u < NSTAGE - 1; ++u) load_tile(u, buf.k[u], buf.v[u]);
+  // Two register stages: while tile k is computed, the loads of tile k+1 are
+  // in flight.  Loads are issued unconditionally (zero extent past the end of
+  // the list), so the loop has no join points and every wait is exact.
+  __device__ __forceinline__ void run() {
+    f16x8 ka[C::NK], va[C::NK], kb[C::NK], vb[C::NK];
+    load_tile(0, ka, va);
+    for (int k = 0;; k += 2) {
+      load_tile(k + 1, kb, vb);
+      if (k >= ntiles) break;
+      compute_tile(k, ka, va);
+      load_tile(k + 2, ka, va);
+      if (k + 1 >= ntiles) break;
+      compute_tile(k + 1, kb, vb);
+    }
   }
 
-  template <int NSTAGE, class TileEnd>
-  __device__ __forceinline__ void run(Buffers<NSTAGE>& buf, TileEnd& tile_end) {
-    static_assert(NSTAGE >= 2, "need at least two register stages");
-    int k = 0;
-    while (true) {
+  // Writes the decoded token's K/V row to the pool (the wave holding its tile).
+  __device__ __forceinline__ void store_new_row(f16* k_pool_w, f16* v_pool_w) const {
+    if (new_tile < 0) return;
+    const int lane = lane_id();
+    const int64_t base = tile_base(new_tile);
+    char* kb = reinterpret_cast<char*>(k_pool_w + base);
+    char* vb = reinterpret_cast<char*>(v_pool_w + base);
+    if ((lane & 15) == new_row) {
 #pragma unroll
-      for (int u = 0; u < NSTAGE; ++u) {
-        load_tile(k + NSTAGE - 1, buf.k[(u + NSTAGE - 1) % NSTAGE], buf.v[(u + NSTAGE - 1) % NSTAGE]);
-        compute_tile(k, buf.k[u], buf.v[u]);
-        if (!tile_end(*this, k)) return;
-        ++k;
-      }
+      for (int s = 0; s < C::NK; ++s)
+        *reinterpret_cast<f16x8*>(kb + k_off0() + k_soff(s)) = knew[s];
     }
+    const int vrow = lane / C::CPR;
+#pragma unroll
+    for (int j = 0; j < C::NK; ++j)
+      if (j * C::RPI + vrow == new_row)
+        *reinterpret_cast<f16x8*>(vb + v_off0() + v_soff(j)) = vnew;
   }
 
   __device__ __forceinline__ float l_total() const {

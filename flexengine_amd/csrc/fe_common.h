@@ -26,25 +26,46 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }
 
+__device__ __forceinline__ int readlane_i(int v, int lane) {
+  return __builtin_amdgcn_readlane(v, lane);
+}
+
+// Cross-lane integer reductions and scans on DPP row operations (VALU, a few
+// cycles each) instead of LDS-routed shuffles: within each row of 16 lanes,
+// then across the four rows with readlane.
+namespace dpp {
+constexpr int kQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141; // lane i <- 7-i within each 8 lanes
+constexpr int kRowMirror = 0x140;     // lane i <- 15-i within each row
+constexpr int kRowShr = 0x110;        // + n: lane i <- i-n within the row
+template <int CTRL>
+__device__ __forceinline__ int mov(int v) {
+  // bound_ctrl: a source outside the row reads as 0
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+}  // namespace dpp
+
+// Sum over all 64 lanes (wave-uniform result).
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+  v += dpp::mov<dpp::kQuadXor1>(v);
+  v += dpp::mov<dpp::kQuadXor2>(v);
+  v += dpp::mov<dpp::kRowHalfMirror>(v);
+  v += dpp::mov<dpp::kRowMirror>(v);
+  return (readlane_i(v, 0) + readlane_i(v, 16)) + (readlane_i(v, 32) + readlane_i(v, 48));
 }
 
 // Inclusive prefix sum across the 64 lanes.
 __device__ __forceinline__ int wave_scan_incl_i(int v) {
+  v += dpp::mov<dpp::kRowShr + 1>(v);
+  v += dpp::mov<dpp::kRowShr + 2>(v);
+  v += dpp::mov<dpp::kRowShr + 4>(v);
+  v += dpp::mov<dpp::kRowShr + 8>(v);
+  const int r0 = readlane_i(v, 15);
+  const int r1 = r0 + readlane_i(v, 31);
+  const int r2 = r1 + readlane_i(v, 47);
   const int lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    int up = __shfl_up(v, d, kWave);
-    if (lane >= d) v += up;
-  }
-  return v;
-}
-
-__device__ __forceinline__ int readlane_i(int v, int lane) {
-  return __builtin_amdgcn_readlane(v, lane);
+  return v + (lane < 16 ? 0 : (lane < 32 ? r0 : (lane < 48 ? r1 : r2)));
 }
 
 // ---- 16-byte global accesses ------------------------------------------------
@@ -77,8 +98,8 @@ __device__ __forceinline__ f16x4 hi4(f16x8 v) { return f16x4{v[4], v[5], v[6], v
 //   quads_b = ceil(L_b / 64), chunk = max(1, ceil(sum_b quads_b / target)),
 //   splits_b = ceil(quads_b / chunk).
 // Pieces are numbered sequence-major; piece ids run over [0, sum_b splits_b) <=
-// target + batch.  Every function below is evaluated by a whole wave and
-// returns wave-uniform values.
+// target + batch.  find_piece is evaluated by a whole wave and returns
+// wave-uniform values.
 //
 // With a shared-prefix (cascade) decode, sequence b's keys before tok0[b] are
 // attended elsewhere, and only its suffix [tok0[b], L_b) is partitioned here
@@ -93,17 +114,18 @@ __device__ __forceinline__ int seq_len(const int32_t* ctx, int b, int max_len) {
   return L < max_len ? L : max_len;
 }
 
+// Maximum over all 64 lanes (wave-uniform result).
 __device__ __forceinline__ int wave_max_i(int v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const int o = __shfl_xor(v, m, kWave);
-    v = v > o ? v : o;
-  }
-  return v;
+  v = max(v, dpp::mov<dpp::kQuadXor1>(v));
+  v = max(v, dpp::mov<dpp::kQuadXor2>(v));
+  v = max(v, dpp::mov<dpp::kRowHalfMirror>(v));
+  v = max(v, dpp::mov<dpp::kRowMirror>(v));
+  return max(max(readlane_i(v, 0), readlane_i(v, 16)), max(readlane_i(v, 32), readlane_i(v, 48)));
 }
 
-// Chunk size in quads.  Besides ~target pieces in total, no sequence may be
-// cut into more than kMaxPieces pieces (the merge holds their weights in LDS).
+// Chunk size in quads.  Besides ~target pieces in total, no sequence is cut
+// into more than kMaxPieces pieces, which bounds the merge of one sequence to
+// four rounds of 16 partials.
 constexpr int kMaxPieces = 64;
 
 // First key of sequence b's suffix (0 without a shared prefix); <= its length.
@@ -111,32 +133,6 @@ __device__ __forceinline__ int suffix_start(const int32_t* tok0, int b, int L) {
   if (tok0 == nullptr) return 0;
   const int t = tok0[b];
   return t > 0 ? (t < L ? t : L) : 0;
-}
-
-__device__ __forceinline__ int split_chunk_quads(const int32_t* ctx, const int32_t* tok0, int B,
-                                                 int max_len, int target) {
-  const int lane = lane_id();
-  int total = 0, longest = 0;
-  for (int base = 0; base < B; base += kWave) {
-    const int b = base + lane;
-    int nq = 0;
-    if (b < B) {
-      const int L = seq_len(ctx, b, max_len);
-      nq = (L - suffix_start(tok0, b, L) + 63) >> 6;
-    }
-    total += wave_sum_i(nq);
-    const int m = wave_max_i(nq);
-    longest = longest > m ? longest : m;
-  }
-  // the shuffle reductions leave the same value in every lane; readfirstlane
-  // tells the compiler they are wave-uniform, so every bound and address
-  // derived from them stays in scalar registers
-  total = __builtin_amdgcn_readfirstlane(total);
-  longest = __builtin_amdgcn_readfirstlane(longest);
-  int chunk = (total + target - 1) / target;
-  const int floor_chunk = (longest + kMaxPieces - 1) / kMaxPieces;
-  chunk = chunk > floor_chunk ? chunk : floor_chunk;
-  return chunk > 0 ? chunk : 1;
 }
 
 struct Piece {
@@ -150,16 +146,50 @@ struct Piece {
 };
 
 // Finds the piece with id `item`; false when item is past the last piece, in
-// which case `total` receives the number of pieces.
-__device__ __forceinline__ bool locate_piece(const int32_t* ctx, const int32_t* tok0, int B,
-                                             int max_len, int chunk, int item, Piece& pc,
-                                             int& total) {
+// which case `total` receives the number of pieces.  Two passes over the
+// sequences (quad totals -> chunk, then a prefix sum of pieces); the lengths
+// of the first 64 sequences are loaded once and kept in registers for both,
+// so a batch of up to 64 costs one round trip to memory.
+__device__ __forceinline__ bool find_piece(const int32_t* ctx, const int32_t* tok0, int B,
+                                           int max_len, int target, int item, Piece& pc,
+                                           int& total) {
   const int lane = lane_id();
+  int L0 = 0, s0 = 0;
+  if (lane < B) {
+    L0 = seq_len(ctx, lane, max_len);
+    s0 = suffix_start(tok0, lane, L0);
+  }
+  const int nq0 = (L0 - s0 + 63) >> 6;
+  int sum = wave_sum_i(nq0), longest = wave_max_i(nq0);
+  for (int base = kWave; base < B; base += kWave) {
+    const int b = base + lane;
+    int nq = 0;
+    if (b < B) {
+      const int L = seq_len(ctx, b, max_len);
+      nq = (L - suffix_start(tok0, b, L) + 63) >> 6;
+    }
+    sum += wave_sum_i(nq);
+    const int m = wave_max_i(nq);
+    longest = longest > m ? longest : m;
+  }
+  // the shuffle reductions leave the same value in every lane; readfirstlane
+  // tells the compiler they are wave-uniform, so every bound and address
+  // derived from them stays in scalar registers
+  sum = __builtin_amdgcn_readfirstlane(sum);
+  longest = __builtin_amdgcn_readfirstlane(longest);
+  int chunk = (sum + target - 1) / target;
+  const int floor_chunk = (longest + kMaxPieces - 1) / kMaxPieces;
+  chunk = chunk > floor_chunk ? chunk : floor_chunk;
+  chunk = chunk > 0 ? chunk : 1;
+
   int carry = 0;
   for (int base = 0; base < B; base += kWave) {
     const int b = base + lane;
-    const int L = b < B ? seq_len(ctx, b, max_len) : 0;
-    const int t0 = b < B ? suffix_start(tok0, b, L) : 0;
+    int L = L0, t0 = s0;
+    if (base > 0) {
+      L = b < B ? seq_len(ctx, b, max_len) : 0;
+      t0 = b < B ? suffix_start(tok0, b, L) : 0;
+    }
     const int nq = (L - t0 + 63) >> 6;
     const int ns = (nq + chunk - 1) / chunk;
     const int incl = wave_scan_incl_i(ns) + carry;

@@ -45,11 +45,7 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kDefaultWorkgroups = FE_DECODE_WORKGROUPS;
 constexpr int kMaxGroup = 16;
 
-// Register stages of the K/V prefetch pipeline and the occupancy the register
-// allocation is held to (waves per SIMD); tuned on MI355X for head_dim 128.
-#ifndef FE_DECODE_STAGES
-#define FE_DECODE_STAGES 2
-#endif
+// The occupancy the register allocation is held to (waves per SIMD).
 #ifndef FE_DECODE_WAVES_PER_EU
 #define FE_DECODE_WAVES_PER_EU 2
 #endif
@@ -126,22 +122,25 @@ __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, 
     float M = kNegInf, den = 0.f;
     f32x4 num = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < ns; s0 += kMergeBatch) {
+      // only the live slots are loaded (nb is wave-uniform)
+      const int nb = ns - s0 < kMergeBatch ? ns - s0 : kMergeBatch;
       float lv[kMergeBatch];
       f32x4 ov[kMergeBatch];
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
-        const int sidx = s0 + u < ns ? s0 + u : ns - 1;  // clamped: always a written slot
-        lv[u] = load_coherent(lse_base + (int64_t)sidx * a.Hq + hh);
-        ov[u] = __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       ro, (uint32_t)((sidx * o_step + e4 * 4) * sizeof(float)), 0, kSc1));
+        lv[u] = kNegInf;
+        ov[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (u < nb) {
+          const int sidx = s0 + u;
+          lv[u] = load_coherent(lse_base + (int64_t)sidx * a.Hq + hh);
+          ov[u] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         ro, (uint32_t)((sidx * o_step + e4 * 4) * sizeof(float)), 0, kSc1));
+        }
       }
       float bm = kNegInf;
 #pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) {
-        if (s0 + u >= ns) lv[u] = kNegInf;
-        bm = fmaxf(bm, lv[u]);
-      }
+      for (int u = 0; u < kMergeBatch; ++u) bm = fmaxf(bm, lv[u]);
       const float newM = fmaxf(M, bm);
       const float alpha = M == kNegInf ? 0.f : exp2f(M - newM);
       num *= alpha;
@@ -208,10 +207,9 @@ void piece_decode_kernel(const DecodeArgs a) {
 
   const int h = blockIdx.x % a.Hkv;
   const int item = blockIdx.x / a.Hkv;
-  const int chunk = split_chunk_quads(a.ctx, a.tok0, a.B, a.max_len, a.target);
   Piece pc;
   int total = 0;
-  if (!locate_piece(a.ctx, a.tok0, a.B, a.max_len, chunk, item, pc, total)) {
+  if (!find_piece(a.ctx, a.tok0, a.B, a.max_len, a.target, item, pc, total)) {
     // spare workgroup: zero rows of inactive sequences
     const int b = item - total;
     if (b < a.B && seq_len(a.ctx, b, a.max_len) == 0) {
@@ -245,16 +243,14 @@ void piece_decode_kernel(const DecodeArgs a) {
   float m_run, l_tot;
   f32x4 o[C::NX];
   if constexpr (PAGE16) {
+    // the wave's tiles t_first, t_first + 4, ... of the piece as a tile list
     TileListCore<D> core;
     core.k_pool = a.k_pool;
     core.v_pool = a.v_pool;
-    core.k_pool_w = a.k_pool;
-    core.v_pool_w = a.v_pool;
     core.rs = a.Hkv * D;
     core.hoff = h * D;
     core.scale_log2 = a.scale_log2;
     core.stage = smem + w * C::STAGE;
-    // the wave's tiles t_first, t_first + 4, ... of the piece as a tile list
     const int ntiles = t_first < t_end ? (t_end - t_first + kWaves - 1) / kWaves : 0;
     core.ntiles = ntiles;
     {
@@ -265,22 +261,28 @@ void piece_decode_kernel(const DecodeArgs a) {
       core.row_vec = blk * a.BS + (tok & (a.BS - 1));
       core.rows_vec = lane < ntiles ? (rem < kTile ? rem : kTile) : 0;
     }
-    if (a.k_new != nullptr) {
-      const int tn = (pc.L - 1) / kTile - t_first;  // list index of the decoded token's tile
-      if (tn >= 0 && tn % kWaves == 0 && tn / kWaves < ntiles)
-        core.write_new_row(tn / kWaves, (pc.L - 1) & (kTile - 1),
-                           a.k_new + (int64_t)b * a.new_stride + (int64_t)h * D,
-                           a.v_new + (int64_t)b * a.new_stride + (int64_t)h * D);
+    core.new_tile = -1;
+    core.new_row = 0;
+    if (a.k_new != nullptr && pc.tok_end == pc.L) {
+      // the piece holds the decoded token (position L-1); the wave whose list
+      // holds its tile takes the row from k_new / v_new, loaded here
+      // alongside the tables
+      const int tn = (pc.L - 1) / kTile - t_first;
+      if (tn >= 0 && tn % kWaves == 0) {
+        core.new_tile = tn / kWaves;
+        core.new_row = (pc.L - 1) & (kTile - 1);
+        const f16* kr = a.k_new + (int64_t)b * a.new_stride + (int64_t)h * D;
+        const f16* vr = a.v_new + (int64_t)b * a.new_stride + (int64_t)h * D;
+#pragma unroll
+        for (int s = 0; s < C::NK; ++s) core.knew[s] = ld16(kr + (4 * s + g) * 8);
+        core.vnew = ld16(vr + (lane % C::CPR) * 8);
+      }
     }
 #pragma unroll
     for (int s = 0; s < C::NK; ++s) core.qv[s] = qv[s];
     core.init_acc();
-    if (ntiles > 0) {
-      typename TileListCore<D>::template Buffers<FE_DECODE_STAGES> buf;
-      core.prologue(buf);
-      auto more = [&](TileListCore<D>&, int k) { return k + 1 < ntiles; };
-      core.template run<FE_DECODE_STAGES>(buf, more);
-    }
+    core.run();
+    core.store_new_row(a.k_pool, a.v_pool);
     m_run = core.m_run;
     l_tot = core.l_total();
 #pragma unroll
@@ -376,345 +378,6 @@ void piece_decode_kernel(const DecodeArgs a) {
   merge_pieces<D>(a, b, h, item - pc.split, pc.nsplit, pc.tok0 > 0);
 }
 
-// ---- equal-tile ("lean") decode for block sizes divisible by 16 -------------
-//
-// The keys of every sequence are cut into 16-token tiles; per KV head the tiles
-// of all sequences, in sequence order, form one list of T tiles.  Workgroup j
-// (of P per KV head) takes the contiguous range [j*ceil(T/P), ...) whatever the
-// sequence boundaries, so every workgroup -- and every CU -- gets the same
-// number of tiles within one.  Wave w of the workgroup takes a contiguous
-// quarter of the range; consecutive tiles of a wave can belong to different
-// sequences, and at each sequence boundary the wave's state (o, m, l) for that
-// sequence is flushed:
-//   - the wave saw the whole sequence: normalise and write the output row;
-//   - the sequence started in an earlier wave of this workgroup: park the state
-//     in LDS for that wave;
-//   - the sequence continues in a later wave of this workgroup: keep it in
-//     registers, and after the loop merge in the later waves' parked states;
-//   - otherwise (or after that merge) the sequence spans several workgroups:
-//     write a partial output and its LSE to slot j + b, draw a ticket, and the
-//     last of its ceil-divided pieces merges them (merge_pieces).
-// A workgroup has at most two such pieces: the sequences at either end of its
-// range.  Slots j + b are distinct for distinct (range, sequence) pairs since
-// both indices only grow along the tile list.
-template <int D>
-struct LeanLds {
-  using C = TileCfg<D>;
-  static constexpr size_t park = (size_t)kWaves * C::STAGE;
-  static constexpr size_t park_m = park + (size_t)(kWaves - 1) * C::NX * kWave * 16;
-  static constexpr size_t park_l = park_m + (size_t)(kWaves - 1) * kWave * sizeof(float);
-  static constexpr size_t flags = park_l + (size_t)(kWaves - 1) * kWave * sizeof(float);
-  static constexpr size_t bytes = flags + 8 * sizeof(int);
-};
-
-template <int D>
-__device__ __forceinline__ void store_rows_final(const DecodeArgs& a, int b, int h,
-                                                 const f32x4 (&o)[TileCfg<D>::NX], float inv,
-                                                 int lane) {
-  const int g = lane >> 4;
-  const int n = lane & 15;
-  if (n < a.G) {
-    f16* orow = a.out + ((int64_t)b * a.Hq + h * a.G + n) * D + 4 * g;
-#pragma unroll
-    for (int x = 0; x < TileCfg<D>::NX; ++x)
-      *reinterpret_cast<f16x4*>(orow + 16 * x) =
-          f16x4{(f16)(o[x][0] * inv), (f16)(o[x][1] * inv), (f16)(o[x][2] * inv),
-                (f16)(o[x][3] * inv)};
-  }
-}
-
-// Partial output (normalised) and base-2 LSE of one piece, written with
-// device-coherent (sc1) stores.
-template <int D>
-__device__ __forceinline__ void store_rows_partial(const DecodeArgs& a, int slot, int h,
-                                                   const f32x4 (&o)[TileCfg<D>::NX], float inv,
-                                                   float lse, int lane) {
-  const int g = lane >> 4;
-  const int n = lane & 15;
-  const int G = a.G;
-  if (n < G) {
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        a.ws_o + ((int64_t)slot * a.Hq + h * G) * D, 0, G * D * (int)sizeof(float), 0x00020000);
-    const uint32_t off = (uint32_t)((n * D + 4 * g) * sizeof(float));
-#pragma unroll
-    for (int x = 0; x < TileCfg<D>::NX; ++x)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[x] * inv), r,
-                                             off + 16 * x * sizeof(float), 0, kSc1);
-    if (g == 0) store_coherent(a.ws_lse + (int64_t)slot * a.Hq + h * G + n, lse);
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void zero_row(const DecodeArgs& a, int b, int h) {
-  f16* row = a.out + ((int64_t)b * a.Hq + h * a.G) * D;
-  for (int e = lane_id() * 8; e < a.G * D; e += kWave * 8) st16(row + e, f16x8{});
-}
-
-// Query vectors of sequence b for the MFMA B operand: lane (g, n) holds chunks
-// 4s+g of query head n of the group (zeros for n >= G).
-template <int D>
-__device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int h, int lane,
-                                       f16x8 (&qv)[TileCfg<D>::NK]) {
-  const int g = lane >> 4;
-  const int n = lane & 15;
-  const int nn = n < a.G ? n : a.G - 1;
-  const f16* qr = a.q + (int64_t)b * a.q_stride + (int64_t)(h * a.G + nn) * D + g * 8;
-#pragma unroll
-  for (int s = 0; s < TileCfg<D>::NK; ++s) {
-    const f16x8 v = ld16(qr + s * 32);
-    qv[s] = n < a.G ? v : f16x8{};
-  }
-}
-
-template <int D>
-__global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(FE_DECODE_WAVES_PER_EU, 8)))
-void lean_decode_kernel(const DecodeArgs a) {
-  using C = TileCfg<D>;
-  using Lds = LeanLds<D>;
-  using Core = TileListCore<D>;
-  extern __shared__ __align__(16) unsigned char smem[];
-
-  const int h = blockIdx.x % a.Hkv;
-  const int j = blockIdx.x / a.Hkv;
-  const int P = a.target;  // ranges per KV head
-  const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = lane_id();
-
-  int* mflag = reinterpret_cast<int*>(smem + Lds::flags);  // [2][b, first, ns]
-  if (tid < 6) mflag[tid] = -1;  // read only after later barriers
-
-  // ---- tiles in total; zero rows of inactive sequences b = j (mod P).  The
-  //      first 64 sequences stay in registers for the second pass. ----
-  const int L0 = lane < a.B ? seq_len(a.ctx, lane, a.max_len) : 0;
-  const int nt0 = (L0 + kTile - 1) / kTile;
-  const int incl0 = wave_scan_incl_i(nt0);
-  int T = readlane_i(incl0, kWave - 1);
-  for (int base = 0; base < a.B; base += kWave) {
-    const int bb = base + lane;
-    const int L = base == 0 ? L0 : (bb < a.B ? seq_len(a.ctx, bb, a.max_len) : 0);
-    if (base > 0) T += wave_sum_i((L + kTile - 1) / kTile);
-    if (w == 0) {
-      unsigned long long z = __ballot(bb < a.B && L == 0 && bb % P == j);
-      while (z) {
-        const int zb = base + __builtin_ctzll(z);
-        z &= z - 1;
-        zero_row<D>(a, zb, h);
-      }
-    }
-  }
-  T = __builtin_amdgcn_readfirstlane(T);
-  if (T == 0) return;
-  const int tpr = (T + P - 1) / P;
-  const int r0 = j * tpr;
-  if (r0 >= T) return;
-  const int r1 = min(r0 + tpr, T);
-  // wave w: a contiguous sub-range; the first (len % 4) waves take one more tile
-  const int len = r1 - r0;
-  const int qw = len / kWaves;
-  const int qr = len % kWaves;
-  auto wave_begin = [&](int v) { return r0 + v * qw + (v < qr ? v : qr); };
-  const int wa = wave_begin(w);
-  const int we = wave_begin(w + 1);
-  const int ntiles = we - wa;  // <= 64: the host keeps ceil(T/P) <= 256
-
-  // ---- lane k: sequence, first tile and length of the sequence of tile wa+k;
-  //      the sequences at both ends of the workgroup's range ----
-  int seq_v = 0, s0_v = 0, len_v = 0;
-  int S0_first = 0, S1_last = 0;
-  auto visit = [&](int base, int L, int nt, int incl) __attribute__((always_inline)) {
-    const int excl = incl - nt;
-    unsigned long long mk = __ballot(nt > 0 && excl < we && incl > wa);
-    while (mk) {
-      const int i = __builtin_ctzll(mk);
-      mk &= mk - 1;
-      const int sb = readlane_i(excl, i);
-      const int lb = readlane_i(L, i);
-      if (wa + lane >= sb) {
-        seq_v = base + i;
-        s0_v = sb;
-        len_v = lb;
-      }
-    }
-    const unsigned long long m0 = __ballot(excl <= r0 && r0 < incl);
-    if (m0) S0_first = readlane_i(excl, __builtin_ctzll(m0));
-    const unsigned long long m1 = __ballot(excl < r1 && r1 <= incl);
-    if (m1) S1_last = readlane_i(incl, __builtin_ctzll(m1));
-  };
-  visit(0, L0, nt0, incl0);
-  for (int base = kWave, carry = readlane_i(incl0, kWave - 1); base < a.B && carry < r1;
-       base += kWave) {
-    const int bb = base + lane;
-    const int L = bb < a.B ? seq_len(a.ctx, bb, a.max_len) : 0;
-    const int nt = (L + kTile - 1) / kTile;
-    const int incl = wave_scan_incl_i(nt) + carry;
-    visit(base, L, nt, incl);
-    carry = readlane_i(incl, kWave - 1);
-  }
-  const bool wg_partial = S0_first < r0 || S1_last > r1;  // some sequence leaves the range
-
-  // ---- query vectors of the wave's first two sequences, block ids of its
-  //      tiles, and the new K/V rows of the sequences ending in its tiles ----
-  Core core;
-  core.k_pool = a.k_pool;
-  core.v_pool = a.v_pool;
-  core.k_pool_w = a.k_pool;
-  core.v_pool_w = a.v_pool;
-  core.rs = a.Hkv * D;
-  core.hoff = h * D;
-  core.scale_log2 = a.scale_log2;
-  core.stage = smem + w * C::STAGE;
-  core.ntiles = ntiles;
-  const int b_seg0 = readlane_i(seq_v, 0);
-  const unsigned long long second = __ballot(lane < ntiles && seq_v != b_seg0);
-  const int b_seg1 = second ? readlane_i(seq_v, __builtin_ctzll(second)) : -1;
-  f16x8 qn[C::NK];
-  if (ntiles > 0) load_q<D>(a, b_seg0, h, lane, core.qv);
-  if (b_seg1 >= 0) load_q<D>(a, b_seg1, h, lane, qn);
-  int blk = 0;
-  if (lane < ntiles) {
-    const int tok = (wa + lane - s0_v) * kTile;
-    blk = clamp_block(a.tables[(int64_t)seq_v * a.W + (tok >> a.bs_log2)], a.NB);
-  }
-  {
-    const int tok = (wa + lane - s0_v) * kTile;
-    const int rem = len_v - tok;
-    core.row_vec = blk * a.BS + (tok & (a.BS - 1));
-    core.rows_vec = lane < ntiles ? (rem < kTile ? rem : kTile) : 0;
-  }
-  if (a.k_new != nullptr) {
-    // tiles holding a sequence's last key: write the decoded token's K/V row
-    unsigned long long mk =
-        __ballot(lane < ntiles && wa + lane == s0_v + (len_v + kTile - 1) / kTile - 1);
-    while (mk) {
-      const int k = __builtin_ctzll(mk);
-      mk &= mk - 1;
-      const int bn = readlane_i(seq_v, k);
-      const int r = (readlane_i(len_v, k) - 1) & (kTile - 1);
-      core.write_new_row(k, r, a.k_new + (int64_t)bn * a.new_stride + (int64_t)h * D,
-                         a.v_new + (int64_t)bn * a.new_stride + (int64_t)h * D);
-    }
-  }
-
-  f32x4* park = reinterpret_cast<f32x4*>(smem + Lds::park);
-  float* park_m = reinterpret_cast<float*>(smem + Lds::park_m);
-  float* park_l = reinterpret_cast<float*>(smem + Lds::park_l);
-  int keep_b = -1, keep_S0 = 0, keep_S1 = 0;
-  int pend_b[2] = {-1, -1}, pend_first[2] = {0, 0}, pend_ns[2] = {0, 0};
-  auto add_pending = [&](int b, int S0, int S1) __attribute__((always_inline)) {
-    const int first = S0 / tpr + b;
-    const int ns = (S1 - 1) / tpr - S0 / tpr + 1;
-    if (S1 > r1) {
-      pend_b[1] = b; pend_first[1] = first; pend_ns[1] = ns;
-    } else {
-      pend_b[0] = b; pend_first[0] = first; pend_ns[0] = ns;
-    }
-  };
-
-  if (ntiles > 0) {
-    typename Core::template Buffers<FE_DECODE_STAGES> buf;
-    core.prologue(buf);
-    core.init_acc();
-    auto tile_end = [&](Core& c, int k) __attribute__((always_inline)) -> bool {
-      const int b = readlane_i(seq_v, k);
-      const bool last = k + 1 >= ntiles;
-      if (!last && readlane_i(seq_v, k + 1) == b) return true;
-      // The wave's tiles of sequence b end here.  The lane index goes through
-      // an opaque copy so that the addresses derived from it are computed
-      // here, on this rarely taken path, instead of being hoisted out of the
-      // loop and held in registers across it.
-      int ol = lane;
-      asm volatile("" : "+v"(ol));
-      const int S0 = readlane_i(s0_v, k);
-      const int S1 = S0 + (readlane_i(len_v, k) + kTile - 1) / kTile;
-      const float l_tot = c.l_total();
-      if (S0 >= wa && S1 <= we) {
-        store_rows_final<D>(a, b, h, c.o, 1.f / l_tot, ol);
-      } else if (S0 < wa && w > 0) {
-#pragma unroll
-        for (int x = 0; x < C::NX; ++x) park[((w - 1) * C::NX + x) * kWave + ol] = c.o[x];
-        park_m[(w - 1) * kWave + ol] = c.m_run;
-        park_l[(w - 1) * kWave + ol] = l_tot;
-      } else if (S1 > we && we < r1) {
-        keep_b = b;  // the accumulators stay in c until the later waves have parked
-        keep_S0 = S0;
-        keep_S1 = S1;
-      } else {
-        store_rows_partial<D>(a, j + b, h, c.o, 1.f / l_tot, c.m_run + log2f(l_tot), ol);
-        add_pending(b, S0, S1);
-      }
-      if (last) return false;
-      c.init_acc();
-      const int bn = readlane_i(seq_v, k + 1);
-      if (bn == b_seg1) {
-#pragma unroll
-        for (int s = 0; s < C::NK; ++s) c.qv[s] = qn[s];
-      } else {
-        load_q<D>(a, bn, h, ol, c.qv);
-      }
-      return true;
-    };
-    core.template run<FE_DECODE_STAGES>(buf, tile_end);
-  }
-  __syncthreads();  // parked states are visible
-
-  if (keep_b >= 0) {
-    // merge the parked states of the later waves that saw sequence keep_b
-    const int end_t = min(keep_S1, r1);
-    float M = core.m_run;
-    for (int v = w + 1; v < kWaves && wave_begin(v) < end_t; ++v)
-      M = fmaxf(M, park_m[(v - 1) * kWave + lane]);
-    const float sc0 = core.m_run == kNegInf ? 0.f : exp2f(core.m_run - M);
-    float den = sc0 * core.l_total();
-#pragma unroll
-    for (int x = 0; x < C::NX; ++x) core.o[x] *= sc0;
-    for (int v = w + 1; v < kWaves && wave_begin(v) < end_t; ++v) {
-      const float mv = park_m[(v - 1) * kWave + lane];
-      const float sc = mv == kNegInf ? 0.f : exp2f(mv - M);
-      den += sc * park_l[(v - 1) * kWave + lane];
-#pragma unroll
-      for (int x = 0; x < C::NX; ++x) core.o[x] += sc * park[((v - 1) * C::NX + x) * kWave + lane];
-    }
-    if (keep_S0 >= r0 && keep_S1 <= r1) {
-      store_rows_final<D>(a, keep_b, h, core.o, 1.f / den, lane);
-    } else {
-      store_rows_partial<D>(a, j + keep_b, h, core.o, 1.f / den, M + log2f(den), lane);
-      add_pending(keep_b, keep_S0, keep_S1);
-    }
-  }
-  if (!wg_partial) return;
-
-  // ---- pieces shared with other workgroups: the last of each merges ----
-  if (pend_b[0] >= 0 || pend_b[1] >= 0) {
-    wait_stores();  // this wave's partials are complete at the device-coherent level
-    if (lane == 0) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (pend_b[s] >= 0 &&
-            __hip_atomic_fetch_add(a.tickets + pend_b[s] * a.Hkv + h, 1, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT) == pend_ns[s] - 1) {
-          mflag[3 * s] = pend_b[s];
-          mflag[3 * s + 1] = pend_first[s];
-          mflag[3 * s + 2] = pend_ns[s];
-        }
-      }
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int mb = __builtin_amdgcn_readfirstlane(mflag[3 * s]);
-    if (mb >= 0) {
-      if (tid == 0)
-        __hip_atomic_store(a.tickets + mb * a.Hkv + h, 0, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      merge_pieces<D>(a, mb, h, __builtin_amdgcn_readfirstlane(mflag[3 * s + 1]),
-                      __builtin_amdgcn_readfirstlane(mflag[3 * s + 2]));
-    }
-  }
-}
-
 // General LSE merge of S partial results (natural-log LSE at the boundary).
 __global__ __launch_bounds__(kThreads) void lse_merge_kernel(const float* __restrict__ po,
                                                              const float* __restrict__ plse,
@@ -760,46 +423,26 @@ inline size_t ws_lse_bytes(int batch, int hq, int target) {
   return align256((size_t)(target + batch) * hq * sizeof(float));
 }
 
-// Pieces (ranges) per KV head the kernel aims for.  Raised above the request
-// when the tables allow very long contexts, so that no wave gets more than 64
-// tiles (one block-id fetch per wave): a piece of the generic path holds at
-// most 64 quads, a range of the equal-tile path at most 256 tiles.
+// Pieces per KV head the kernel aims for.  Raised above the request when the
+// tables allow very long contexts, so that no piece holds more than 64 quads
+// (256 tiles: one staged pool row per thread of the workgroup).
 inline int effective_target(int batch, int kv_heads, int max_context, int target_splits) {
   const int target =
       target_splits > 0 ? target_splits : (kDefaultWorkgroups + kv_heads - 1) / kv_heads;
   const int64_t max_quads = ((int64_t)max_context + 63) / 64;
-  const int64_t max_tiles = ((int64_t)max_context + kTile - 1) / kTile;
-  int64_t need = ((int64_t)batch * max_quads + 63) / 64;
-  const int64_t need_tiles = ((int64_t)batch * max_tiles + 255) / 256;
-  need = need > need_tiles ? need : need_tiles;
+  const int64_t need = ((int64_t)batch * max_quads + 63) / 64;
   return need > target ? (int)need : target;
 }
 
 template <int D>
-size_t piece_lds_bytes() {
-  return PieceLds<D>::bytes;
-}
-
-// FE_DECODE_LEAN selects the partition of the block-size-16 path: 1 = equal
-// tile ranges per workgroup (lean_decode_kernel), 0 = per-sequence pieces.
-#ifndef FE_DECODE_LEAN
-#define FE_DECODE_LEAN 0
-#endif
-
-template <int D>
 int launch_decode(const DecodeArgs& a, hipStream_t stream) {
-  const dim3 piece_grid((a.target + 2 * a.B) * a.Hkv);
-  if (a.BS % kTile == 0) {
-    if (FE_DECODE_LEAN)
-      hipLaunchKernelGGL((lean_decode_kernel<D>), dim3(a.target * a.Hkv), dim3(kThreads),
-                         LeanLds<D>::bytes, stream, a);
-    else
-      hipLaunchKernelGGL((piece_decode_kernel<D, true>), piece_grid, dim3(kThreads),
-                         piece_lds_bytes<D>(), stream, a);
-  } else {
-    hipLaunchKernelGGL((piece_decode_kernel<D, false>), piece_grid, dim3(kThreads),
-                       piece_lds_bytes<D>(), stream, a);
-  }
+  const dim3 grid((a.target + 2 * a.B) * a.Hkv);
+  if (a.BS % kTile == 0)
+    hipLaunchKernelGGL((piece_decode_kernel<D, true>), grid, dim3(kThreads), PieceLds<D>::bytes,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((piece_decode_kernel<D, false>), grid, dim3(kThreads), PieceLds<D>::bytes,
+                       stream, a);
   return FE_LAUNCH_STATUS();
 }
 
@@ -837,7 +480,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   const int bs_log2 = log2_exact(block_size);
   if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
   // the shared-prefix split needs 16-token-aligned suffixes (block-size-16k path)
-  if (cascade && (block_size % kTile != 0 || FE_DECODE_LEAN)) return FE_ERR_UNSUPPORTED;
+  if (cascade && block_size % kTile != 0) return FE_ERR_UNSUPPORTED;
   if (batch == 0) return FE_OK;
   FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && context_lens);
   FE_CHECK_ARG((k_new == nullptr) == (v_new == nullptr));
