@@ -84,6 +84,8 @@ struct DecodeArgs {
   int W, B, Hq, Hkv, G, BS, bs_log2, NB, target;
   int max_len;       // W * BS: longest context the tables can address
   float scale_log2;  // softmax scale * log2(e)
+  int nwg;           // balanced kernel: workgroups sharing the tile order (= grid size)
+  int states;        // balanced kernel: parked-state slots in LDS
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -378,6 +380,614 @@ void piece_decode_kernel(const DecodeArgs a) {
   merge_pieces<D>(a, b, h, item - pc.split, pc.nsplit, pc.tok0 > 0);
 }
 
+// ---- balanced decode (block sizes that are multiples of 16) ----------------------
+//
+// Work is cut at 16-token tile granularity over one global order of all
+// (sequence, KV head, tile) triples -- sequence-major, then KV head, then
+// tile -- so every workgroup receives the same number of tiles whatever the
+// context-length mix.  The grid is one 512-thread workgroup (8 waves) per
+// compute unit, and each workgroup asks for more than half of the CU's LDS so
+// that no CU receives two: the HBM bandwidth a CU achieves does not grow with
+// the number of workgroups it holds, so equal bytes per CU is what balances
+// the launch.
+//
+// Workgroup w owns tiles [w*T/N, (w+1)*T/N) of the order (T tiles in total, N
+// workgroups), and each of its waves a contiguous eighth of that range.  A
+// wave's tiles may cross from one (sequence, KV head) "segment" into the
+// next: it parks the finished segment's state (o, m, l of its live query
+// heads) in an LDS slot and goes on without waiting for the other waves, its
+// next tile's loads still in flight.  After the loop the workgroup meets once
+// and combines every segment from the slots of the waves that touched it.  A
+// segment entirely inside the range is written directly as fp16; the first
+// and last segment of a range can be shared with the neighbouring
+// workgroups, and those go through the split-K ticket protocol of the piece
+// kernel (partials with device-coherent stores, the last contributing
+// workgroup merges).  The queries of all segments of the range are staged in
+// LDS during set-up, alongside the block-table loads.  A range with more
+// segments than there are slots (many very short sequences) falls back to
+// combining each segment as soon as all waves are past it, with a barrier
+// per segment.
+constexpr int kBThreads = 512;
+constexpr int kBWaves = kBThreads / kWave;
+constexpr int kBMaxBatch = 2048;      // per-sequence arrays kept in LDS
+constexpr int kBMaxTilesPerWave = 64; // a wave's tile list is held one tile per lane
+constexpr int kBMinLds = 84 * 1024;   // > half of a CU's 160 KB: one workgroup per CU
+
+// Compact parked state of one wave for one segment: o of the G live columns
+// ([NX][4][G] x 16 bytes, the MFMA register layout), then m[G] and l[G].
+__host__ __device__ constexpr int bstate_bytes(int D, int G) {
+  return ((D / 16) * 4 * G * 16 + 2 * G * 4 + 15) & ~15;
+}
+
+template <int D>
+struct BLds {
+  static constexpr size_t stage = 0;
+  static constexpr size_t misc = stage + (size_t)kBWaves * TileCfg<D>::STAGE;  // 64 ints
+  static constexpr size_t arrays = misc + 64 * sizeof(int);
+  // arrays: tile prefix P[B+1], context lengths Ls[B], suffix starts S0[B];
+  // then each wave's second-segment queries [8][NK][64 lanes] x 16 bytes,
+  // then parked states [states][bstate_bytes]
+  static constexpr size_t kQw = (size_t)TileCfg<D>::NK * kWave * 16;
+  __host__ __device__ static size_t qw_off(int B) {
+    return (arrays + (size_t)(3 * B + 1) * sizeof(int) + 15) & ~size_t(15);
+  }
+  __host__ __device__ static size_t states_off(int B) { return qw_off(B) + kBWaves * kQw; }
+  static size_t bytes(int B, int G, int states) {
+    const size_t n = states_off(B) + (size_t)states * bstate_bytes(D, G);
+    return n > (size_t)kBMinLds ? n : (size_t)kBMinLds;
+  }
+};
+
+template <int D>
+__global__ __launch_bounds__(kBThreads) void balanced_decode_kernel(const DecodeArgs a) {
+  using C = TileCfg<D>;
+  using Lds = BLds<D>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  int* misc = reinterpret_cast<int*>(smem + Lds::misc);
+  int* P = reinterpret_cast<int*>(smem + Lds::arrays);
+  int* Ls = P + a.B + 1;
+  int* S0 = Ls + a.B;
+  unsigned char* states = smem + Lds::states_off(a.B);
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = lane_id();
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int G = a.G;
+  const int Hkv = a.Hkv;
+  const int SB = bstate_bytes(D, G);
+  unsigned char* qw = smem + Lds::qw_off(a.B) + w * Lds::kQw;  // this wave's query area
+
+  // ---- tiles of every sequence and their exclusive prefix sum, in LDS ----
+  int carry = 0;
+  for (int base = 0; base < a.B; base += kBThreads) {
+    const int b = base + tid;
+    int L = 0, t0 = 0;
+    if (b < a.B) {
+      L = seq_len(a.ctx, b, a.max_len);
+      t0 = suffix_start(a.tok0, b, L);
+      Ls[b] = L;
+      S0[b] = t0;
+    }
+    const int nt = (L - t0 + kTile - 1) / kTile;
+    const int incl = wave_scan_incl_i(nt);
+    if (lane == kWave - 1) misc[w] = incl;
+    __syncthreads();
+    int off = carry, tot = 0;
+#pragma unroll
+    for (int v = 0; v < kBWaves; ++v) {
+      const int c = misc[v];
+      off += v < w ? c : 0;
+      tot += c;
+    }
+    if (b < a.B) P[b] = off + incl - nt;
+    carry += tot;
+    __syncthreads();
+  }
+  carry = __builtin_amdgcn_readfirstlane(carry);
+  if (tid == 0) P[a.B] = carry;
+  __syncthreads();
+
+  // rows of inactive sequences are zeros (every launched workgroup takes a share)
+  for (int b = blockIdx.x; b < a.B; b += gridDim.x) {
+    if (Ls[b] == 0) {
+      for (int e = tid; e < a.Hq * D; e += kBThreads) a.out[(int64_t)b * a.Hq * D + e] = (f16)0.f;
+    }
+  }
+  const int T = Hkv * carry;
+  // at least one tile per wave: tiny batches use fewer workgroups
+  int nwg = a.nwg;
+  if (T / kBWaves < nwg) nwg = T / kBWaves > 0 ? T / kBWaves : 1;
+  const int wg = blockIdx.x;
+  if (T == 0 || wg >= nwg) return;
+  const int lo = (int)((int64_t)wg * T / nwg);
+  const int hi = (int)((int64_t)(wg + 1) * T / nwg);
+
+  // the workgroup whose range holds tile x
+  auto wg_of = [&](int x) { return (int)(((int64_t)(x + 1) * nwg + T - 1) / T) - 1; };
+  auto seg_start = [&](int sg) {
+    const int b = sg / Hkv;
+    return Hkv * P[b] + (sg - b * Hkv) * (P[b + 1] - P[b]);
+  };
+
+  // ---- this wave's contiguous share of the range, one tile per lane ----
+  const int R = hi - lo;  // >= kBWaves unless the whole batch has fewer tiles
+  const int wlo = lo + (w * R) / kBWaves;
+  const int whi = lo + ((w + 1) * R) / kBWaves;
+  const int ntiles = whi - wlo;
+  // One pass of binary searches: lane k < ntiles locates tile wlo + k; lanes
+  // 0..7 (8..15) also locate the first (last) tile of wave lane % 8, so every
+  // wave knows all waves' segments -- its state slots -- without a barrier.
+  int b1, b2;
+  {
+    const int x1 = wlo + (lane < ntiles ? lane : 0);
+    const int v = lane & (kBWaves - 1);
+    const int x2 = lane < kBWaves ? lo + (v * R) / kBWaves : lo + ((v + 1) * R) / kBWaves - 1;
+    int l1 = 0, r1 = a.B - 1, l2 = 0, r2 = a.B - 1;
+    while (l1 < r1 || l2 < r2) {
+      const int m1 = (l1 + r1 + 1) >> 1, m2 = (l2 + r2 + 1) >> 1;
+      const int p1 = Hkv * P[m1], p2 = Hkv * P[m2];
+      if (l1 < r1) {
+        if (p1 <= x1) l1 = m1;
+        else r1 = m1 - 1;
+      }
+      if (l2 < r2) {
+        if (p2 <= x2) l2 = m2;
+        else r2 = m2 - 1;
+      }
+    }
+    b1 = l1;
+    b2 = l2;
+  }
+  int row_vec = 0, rows_vec = 0, seg_vec = 0x7fffffff, newrow_vec = -1;
+  if (lane < ntiles) {
+    const int b = b1;
+    const int nt = P[b + 1] - P[b];
+    const int r = wlo + lane - Hkv * P[b];
+    const int h = r / nt;
+    const int t = r - h * nt;
+    const int L = Ls[b];
+    const int tok = S0[b] + kTile * t;
+    const int rem = L - tok;
+    const int blk = clamp_block(a.tables[(int64_t)b * a.W + (tok >> a.bs_log2)], a.NB);
+    row_vec = blk * a.BS + (tok & (a.BS - 1));
+    rows_vec = rem < kTile ? rem : kTile;
+    seg_vec = b * Hkv + h;
+    if (a.k_new != nullptr && rem <= kTile) newrow_vec = rem - 1;
+  }
+  auto load_qg = [&](int sg, f16x8 (&dst)[C::NK]) {
+    const int hh = n < G ? n : G - 1;
+    const int b = sg / Hkv;
+    const f16* qrow = a.q + (int64_t)b * a.q_stride + (int64_t)((sg - b * Hkv) * G + hh) * D;
+#pragma unroll
+    for (int s = 0; s < C::NK; ++s) {
+      const f16x8 v = ld16(qrow + (4 * s + g) * 8);
+      dst[s] = n < G ? v : f16x8{};
+    }
+  };
+  // the wave's first two segments (their queries load alongside the tables);
+  // a wave without tiles (ranges shorter than 8) has none
+  const int sa = ntiles > 0 ? __builtin_amdgcn_readlane(seg_vec, 0) : 0x7fffffff;
+  int s2 = 0x7fffffff;
+  {
+    const unsigned long long other = __ballot(lane < ntiles && seg_vec != sa);
+    if (other) s2 = __builtin_amdgcn_readlane(seg_vec, __builtin_ctzll(other));
+  }
+  int bnd = -1;  // -1: wave lane % 8 holds no tiles
+  {
+    const int nt = P[b2 + 1] - P[b2];
+    const int v = lane & (kBWaves - 1);
+    const int vlo = lo + (v * R) / kBWaves;
+    const int vhi = lo + ((v + 1) * R) / kBWaves;
+    const int x2 = lane < kBWaves ? vlo : vhi - 1;
+    if (vhi > vlo) bnd = b2 * Hkv + (x2 - Hkv * P[b2]) / (nt > 0 ? nt : 1);
+  }
+  int wsa[kBWaves], wsb[kBWaves], wslot[kBWaves];
+  int nstates = 0, s_first = 0x7fffffff, s_last = -1;
+#pragma unroll
+  for (int v = 0; v < kBWaves; ++v) {
+    wsa[v] = __builtin_amdgcn_readlane(bnd, v);
+    wsb[v] = __builtin_amdgcn_readlane(bnd, kBWaves + v);
+    if (wsa[v] < 0) {
+      wsa[v] = 0x7fffffff;
+      wsb[v] = -1;
+    }
+    wslot[v] = nstates;
+    if (wsb[v] >= wsa[v]) {
+      nstates += wsb[v] - wsa[v] + 1;
+      s_first = wsa[v] < s_first ? wsa[v] : s_first;
+      s_last = wsb[v];
+    }
+  }
+  int sb = -1, slot0 = 0;
+#pragma unroll
+  for (int v = 0; v < kBWaves; ++v) {
+    if (v == w) {
+      sb = wsb[v];
+      slot0 = wslot[v];
+    }
+  }
+  // slot mode: every wave's states fit the LDS state slots; otherwise one
+  // barrier per segment (slots 0..7)
+  const bool slots = nstates <= a.states;
+  f16x8 qv[C::NK], q2[C::NK];
+  int cur = slots ? sa : s_first;
+  if (!slots || ntiles > 0) load_qg(cur, qv);
+  if (!slots || sb == sa) s2 = 0x7fffffff;
+  if (s2 != 0x7fffffff) load_qg(s2, q2);
+
+  auto seg_tiles = [&](int sg) {
+    const int b = sg / Hkv;
+    return P[b + 1] - P[b];
+  };
+  // next segment after sg holding at least one tile (sequences with no keys hold none)
+  auto next_seg = [&](int sg) {
+    for (++sg; sg <= s_last; ++sg)
+      if (seg_tiles(sg) > 0) break;
+    return sg;
+  };
+
+  const int rs = Hkv * D;
+  unsigned char* stage = smem + Lds::stage + w * C::STAGE;
+  auto tile_rows = [&](int k) {
+    const int r = __builtin_amdgcn_readlane(rows_vec, k & (kWave - 1));
+    return k < ntiles ? r : 0;
+  };
+  auto tile_seg = [&](int k) { return __builtin_amdgcn_readlane(seg_vec, k & (kWave - 1)); };
+  auto tile_base = [&](int k) {
+    const int s = tile_seg(k);
+    const int h = s - (s / Hkv) * Hkv;
+    return (int64_t)__builtin_amdgcn_readlane(row_vec, k & (kWave - 1)) * rs + h * D;
+  };
+  auto tile_newrow = [&](int k) {
+    return k < ntiles ? __builtin_amdgcn_readlane(newrow_vec, k & (kWave - 1)) : -1;
+  };
+  auto rsrc = [&](const f16* pool, int64_t base, int rows) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(pool + base);
+    const uint32_t lo32 = __builtin_amdgcn_readfirstlane((uint32_t)addr);
+    const uint32_t hi32 = __builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32));
+    const int nrec = __builtin_amdgcn_readfirstlane(rows * rs * 2);
+    void* p = reinterpret_cast<void*>(((uint64_t)hi32 << 32) | lo32);
+    return __builtin_amdgcn_make_buffer_rsrc(p, 0, nrec, 0x00020000);
+  };
+  const uint32_t k_off0 = (uint32_t)(((lane & 15) * rs + (lane >> 4) * 8) * 2);
+  const uint32_t v_off0 = (uint32_t)(((lane / C::CPR) * rs + (lane % C::CPR) * 8) * 2);
+  const int vrow = lane / C::CPR;
+
+  // Issues the K/V loads of tile k (zero extent past the list).  The tile
+  // holding the decoded token takes that row from k_new / v_new instead of
+  // the pool, in the same batch of loads.
+  auto load_tile = [&](int k, f16x8 (&kk)[C::NK], f16x8 (&vv)[C::NK]) {
+    const int64_t base = tile_base(k);
+    const int rows = tile_rows(k);
+    const __amdgpu_buffer_rsrc_t kr = rsrc(a.k_pool, base, rows);
+    const __amdgpu_buffer_rsrc_t vr = rsrc(a.v_pool, base, rows);
+    const int nr = tile_newrow(k);
+    if (nr < 0) {
+#pragma unroll
+      for (int s = 0; s < C::NK; ++s)
+        kk[s] = __builtin_bit_cast(
+            f16x8, __builtin_amdgcn_raw_buffer_load_b128(kr, k_off0, s * 64, kStreamPolicy));
+#pragma unroll
+      for (int j = 0; j < C::NK; ++j)
+        vv[j] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                              vr, v_off0, j * C::RPI * rs * 2, kStreamPolicy));
+    } else {
+      const int sg = tile_seg(k);
+      const int b = sg / Hkv;
+      const int h = sg - b * Hkv;
+      const f16* kn = a.k_new + (int64_t)b * a.new_stride + h * D;
+      const f16* vn = a.v_new + (int64_t)b * a.new_stride + h * D;
+#pragma unroll
+      for (int s = 0; s < C::NK; ++s) {
+        if ((lane & 15) == nr)
+          kk[s] = ld16(kn + (4 * s + g) * 8);
+        else
+          kk[s] = __builtin_bit_cast(
+              f16x8, __builtin_amdgcn_raw_buffer_load_b128(kr, k_off0, s * 64, kStreamPolicy));
+      }
+#pragma unroll
+      for (int j = 0; j < C::NK; ++j) {
+        if (j * C::RPI + vrow == nr)
+          vv[j] = ld16(vn + (lane % C::CPR) * 8);
+        else
+          vv[j] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                vr, v_off0, j * C::RPI * rs * 2, kStreamPolicy));
+      }
+    }
+  };
+
+  // ---- per-segment state ----
+  auto load_q = [&](int sg) {
+    if (sg == s2) {
+#pragma unroll
+      for (int s = 0; s < C::NK; ++s) qv[s] = *reinterpret_cast<const f16x8*>(qw + (s * kWave + lane) * 16);
+    } else {
+      load_qg(sg, qv);
+    }
+  };
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 o[C::NX];
+  auto reset = [&]() {
+    m_run = kNegInf;
+    l_run = 0.f;
+#pragma unroll
+    for (int x = 0; x < C::NX; ++x) o[x] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  reset();
+
+  // parks this wave's state in a slot (live columns only)
+  auto park = [&](int slot) {
+    float l_tot = l_run + shfl_xor_f(l_run, 16);
+    l_tot += shfl_xor_f(l_tot, 32);
+    unsigned char* st = states + slot * SB;
+    if (n < G) {
+#pragma unroll
+      for (int x = 0; x < C::NX; ++x)
+        *reinterpret_cast<f32x4*>(st + ((x * 4 + g) * G + n) * 16) = o[x];
+      if (g == 0) {
+        float* ml = reinterpret_cast<float*>(st + C::NX * 4 * G * 16);
+        ml[n] = m_run;
+        ml[G + n] = l_tot;
+      }
+    }
+  };
+
+  // Combines segments s_first + j, j0 <= j < j1, from the parked slots of the
+  // waves that touched them and writes them: fp16 output for a segment inside
+  // the range, a partial (normalised o and base-2 LSE, device-coherent) for a
+  // shared one.  One thread per (segment, 16-byte output chunk).
+  auto combine = [&](int j0, int j1, bool by_wave) {
+    constexpr int kNE = C::NX * 4;  // 16-byte chunks of one query head's output
+    const int ne = kNE * G;
+    for (int it = tid; it < (j1 - j0) * ne; it += kBThreads) {
+      const int sg = s_first + j0 + it / ne;
+      if (seg_tiles(sg) == 0) continue;
+      const int e = it % ne;
+      const int nn = e % G;
+      const int xg = e / G;  // x * 4 + g: dims 16x + 4g .. +3
+      const int b = sg / Hkv;
+      const int h = sg - b * Hkv;
+      int sl[kBWaves];
+      float mv[kBWaves];
+      float M = kNegInf;
+#pragma unroll
+      for (int v = 0; v < kBWaves; ++v) {
+        const int slot = by_wave ? v : (wsa[v] <= sg && sg <= wsb[v] ? wslot[v] + sg - wsa[v] : -1);
+        sl[v] = slot;
+        mv[v] = slot >= 0 ? reinterpret_cast<const float*>(states + slot * SB + kNE * G * 16)[nn]
+                          : kNegInf;
+        M = fmaxf(M, mv[v]);
+      }
+      float den = 0.f;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int v = 0; v < kBWaves; ++v) {
+        if (mv[v] == kNegInf) continue;
+        const unsigned char* st = states + sl[v] * SB;
+        const float sc = exp2f(mv[v] - M);
+        den += sc * reinterpret_cast<const float*>(st + kNE * G * 16)[G + nn];
+        acc += sc * *reinterpret_cast<const f32x4*>(st + (xg * G + nn) * 16);
+      }
+      acc *= 1.f / den;
+      const float lse = M + log2f(den);
+      const int64_t r = (int64_t)b * a.Hq + h * G + nn;
+      const int d0 = (xg >> 2) * 16 + (xg & 3) * 4;
+      const int start = seg_start(sg);
+      if (start >= lo && start + seg_tiles(sg) <= hi) {
+        if (S0[b] > 0) {  // fold in the shared-prefix partial of the launch before
+          const float lp = a.pre_lse[r];
+          if (lp != kNegInf) {
+            const f32x4 op = *reinterpret_cast<const f32x4*>(a.pre_o + r * D + d0);
+            const float mx = fmaxf(lse, lp);
+            const float w1 = exp2f(lse - mx), w2 = exp2f(lp - mx);
+            acc = (w1 * acc + w2 * op) * (1.f / (w1 + w2));
+          }
+        }
+        *reinterpret_cast<f16x4*>(a.out + r * D + d0) =
+            f16x4{(f16)acc[0], (f16)acc[1], (f16)acc[2], (f16)acc[3]};
+      } else {
+        const int slot = 2 * wg + (sg == s_first ? 0 : 1);
+        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+            a.ws_o + (int64_t)slot * G * D, 0, G * D * (int)sizeof(float), 0x00020000);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), ro,
+                                               (uint32_t)((nn * D + d0) * sizeof(float)), 0,
+                                               kSc1);
+        if (xg == 0) store_coherent(a.ws_lse + slot * G + nn, lse);
+      }
+    }
+  };
+
+  // barrier mode: all waves park in slot w, meet, combine, move on together
+  auto finish = [&]() {
+    park(w);
+    __syncthreads();
+    combine(cur - s_first, cur - s_first + 1, true);
+    cur = next_seg(cur);
+    if (cur <= s_last) load_q(cur);
+    __syncthreads();
+    reset();
+  };
+
+  // One tile: scores, V staging, softmax and PV.  In slot mode a tile of a
+  // later segment first parks the current one.
+  auto step = [&](int k, f16x8 (&kk)[C::NK], f16x8 (&vv)[C::NK], bool switching) {
+    if (switching) {
+      const int sk = tile_seg(k);
+      if (sk != cur) {
+        park(slot0 + cur - sa);
+        cur = sk;
+        load_q(cur);
+        reset();
+      }
+    }
+    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < C::NK; ++s) {
+      sacc = mfma16(lo4(kk[s]), lo4(qv[s]), sacc);
+      sacc = mfma16(hi4(kk[s]), hi4(qv[s]), sacc);
+    }
+    compiler_fence();
+    {
+      const int cv = lane % C::CPR;
+#pragma unroll
+      for (int j = 0; j < C::NK; ++j) {
+        unsigned char* dst = stage + (j * C::RPI + vrow) * C::ROWB + cv * 16;
+        *reinterpret_cast<f16x8*>(dst) = vv[j];
+      }
+    }
+    compiler_fence();
+    softmax_pv_tile<D>(sacc, 0, tile_rows(k), a.scale_log2, stage, m_run, l_run, o);
+    compiler_fence();
+    const int nr = tile_newrow(k);
+    if (nr >= 0) {  // write the decoded token's row to the pool
+      char* kb = reinterpret_cast<char*>(a.k_pool + tile_base(k));
+      char* vb = reinterpret_cast<char*>(a.v_pool + tile_base(k));
+      if ((lane & 15) == nr) {
+#pragma unroll
+        for (int s = 0; s < C::NK; ++s)
+          *reinterpret_cast<f16x8*>(kb + k_off0 + s * 64) = kk[s];
+      }
+#pragma unroll
+      for (int j = 0; j < C::NK; ++j)
+        if (j * C::RPI + vrow == nr)
+          *reinterpret_cast<f16x8*>(vb + v_off0 + j * C::RPI * rs * 2) = vv[j];
+    }
+  };
+
+  // Tiles k0 .. k1-1 of the list with one tile of prefetch (loads past k1
+  // have zero extent, so every wait is exact).
+  auto run = [&](int k0, int k1, bool switching) {
+    f16x8 ka[C::NK], va[C::NK], kb[C::NK], vb[C::NK];
+    auto ld = [&](int k, f16x8 (&kk)[C::NK], f16x8 (&vv)[C::NK]) {
+      if (k < k1) load_tile(k, kk, vv);
+      else load_tile(ntiles, kk, vv);
+    };
+    ld(k0, ka, va);
+    if (switching && s2 != 0x7fffffff) {
+      // the second segment's queries go to the wave's LDS area once the first
+      // tile's loads are in flight (they were issued before those loads)
+#pragma unroll
+      for (int s = 0; s < C::NK; ++s)
+        *reinterpret_cast<f16x8*>(qw + (s * kWave + lane) * 16) = q2[s];
+    }
+    for (int k = k0;; k += 2) {
+      ld(k + 1, kb, vb);
+      if (k >= k1) break;
+      step(k, ka, va, switching);
+      ld(k + 2, ka, va);
+      if (k + 1 >= k1) break;
+      step(k + 1, kb, vb, switching);
+    }
+  };
+  if (slots) {
+    // one pipeline across the wave's segments; states parked as it goes
+    run(0, ntiles, true);
+    if (ntiles > 0) park(slot0 + cur - sa);
+    __syncthreads();
+    combine(0, s_last - s_first + 1, false);
+  } else {
+    // a pipeline per segment, the workgroup meeting after each
+    int k0 = 0;
+    while (cur <= s_last) {
+      const int k1 = k0 + __builtin_popcountll(__ballot(lane < ntiles && seg_vec == cur));
+      run(k0, k1, false);
+      k0 = k1;
+      finish();
+    }
+  }
+
+  // ---- split segments: the last contributing workgroup merges ----
+  // the segments combine() wrote as partials: s_first (side 0) and s_last
+  // (side 1) when they reach past the range
+  const bool st0 = seg_start(s_first) < lo || seg_start(s_first) + seg_tiles(s_first) > hi;
+  const bool st1 = s_last != s_first && seg_start(s_last) + seg_tiles(s_last) > hi;
+  if (!st0 && !st1) return;
+  wait_stores();
+  __syncthreads();
+  int* flag = misc + 40;
+  if (tid < 2) {
+    const int side = tid;
+    flag[side] = 0;
+    if (side == 0 ? st0 : st1) {
+      const int sg = side == 0 ? s_first : s_last;
+      const int start = seg_start(sg);
+      const int nsplit = wg_of(start + seg_tiles(sg) - 1) - wg_of(start) + 1;
+      flag[side] = __hip_atomic_fetch_add(a.tickets + sg, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+    }
+  }
+  __syncthreads();
+  const int n4 = G * D / 4;
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_o, 0, 2 * nwg * G * D * (int)sizeof(float), 0x00020000);
+  // both merges at once: item = side * n4 + e4
+  for (int item = tid; item < 2 * n4; item += kBThreads) {
+    const int side = item >= n4 ? 1 : 0;
+    if (!flag[side]) continue;
+    const int e4 = item - side * n4;
+    const int sg = side == 0 ? s_first : s_last;
+    const int b = sg / Hkv;
+    const int h = sg - b * Hkv;
+    const int start = seg_start(sg);
+    const int w0 = wg_of(start);
+    const int ns = wg_of(start + seg_tiles(sg) - 1) - w0 + 1;
+    // the first contributor kept the segment in side 1 when its range began earlier
+    const int side0 = (int)((int64_t)w0 * T / nwg) < start ? 1 : 0;
+    if (e4 == 0) __hip_atomic_store(a.tickets + sg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int hh = e4 * 4 / D;
+    float M = kNegInf, den = 0.f;
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < ns; s0 += kMergeBatch) {
+      const int nb = ns - s0 < kMergeBatch ? ns - s0 : kMergeBatch;
+      float lv[kMergeBatch];
+      f32x4 ov[kMergeBatch];
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        lv[u] = kNegInf;
+        ov[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (u < nb) {
+          const int c = s0 + u;
+          const int slot = 2 * (w0 + c) + (c == 0 ? side0 : 0);
+          lv[u] = load_coherent(a.ws_lse + slot * G + hh);
+          ov[u] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         ro, (uint32_t)((slot * G * D + e4 * 4) * sizeof(float)), 0, kSc1));
+        }
+      }
+      float bm = kNegInf;
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) bm = fmaxf(bm, lv[u]);
+      const float newM = fmaxf(M, bm);
+      const float alpha = M == kNegInf ? 0.f : exp2f(M - newM);
+      num *= alpha;
+      den *= alpha;
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const float wv = lv[u] == kNegInf ? 0.f : exp2f(lv[u] - newM);
+        num += wv * ov[u];
+        den += wv;
+      }
+      M = newM;
+    }
+    const int64_t r = (int64_t)b * a.Hq + h * G;
+    if (S0[b] > 0) {  // the shared-prefix part
+      const float lp = a.pre_lse[r + hh];
+      if (lp != kNegInf) {
+        const f32x4 op = *reinterpret_cast<const f32x4*>(a.pre_o + r * D + e4 * 4);
+        const float newM = fmaxf(M, lp);
+        const float alpha = M == kNegInf ? 0.f : exp2f(M - newM);
+        num = num * alpha + exp2f(lp - newM) * op;
+        den = den * alpha + exp2f(lp - newM);
+      }
+    }
+    const float inv = 1.f / den;
+    *reinterpret_cast<f16x4*>(a.out + r * D + e4 * 4) =
+        f16x4{(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
+              (f16)(num[3] * inv)};
+  }
+}
+
 // General LSE merge of S partial results (natural-log LSE at the boundary).
 __global__ __launch_bounds__(kThreads) void lse_merge_kernel(const float* __restrict__ po,
                                                              const float* __restrict__ plse,
@@ -434,8 +1044,83 @@ inline int effective_target(int batch, int kv_heads, int max_context, int target
   return need > target ? (int)need : target;
 }
 
+// Compute units and LDS bytes per workgroup of the current device (queried
+// once per device).
+struct DeviceLimits {
+  int cus;
+  int lds;
+};
+DeviceLimits device_limits() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  static DeviceLimits cache[64] = {};
+  if (dev >= 0 && dev < 64 && cache[dev].cus > 0) return cache[dev];
+  DeviceLimits d{0, 0};
+  if (hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      d.cus <= 0)
+    d.cus = 256;
+  if (hipDeviceGetAttribute(&d.lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) !=
+          hipSuccess ||
+      d.lds <= 0)
+    d.lds = 64 * 1024;
+  if (dev >= 0 && dev < 64) cache[dev] = d;
+  return d;
+}
+
+#ifndef FE_DECODE_BALANCED
+#define FE_DECODE_BALANCED 1
+#endif
+// Batches below this many rows run the piece kernel: on MI355X it measured
+// faster there (B = 8: 7.1 vs 11.5 us; B = 64, C2: 20.8 vs 25.0 us), and the
+// balanced kernel faster above (B = 256, C3: 137.7 vs 160.9 us plain, 83.6
+// vs 99.3 us with shared prefixes).
+#ifndef FE_DECODE_BALANCED_MIN_BATCH
+#define FE_DECODE_BALANCED_MIN_BATCH 128
+#endif
+
+// Launch shape of the balanced kernel for these sizes; nwg = 0 when the piece
+// kernel handles them (block size below 16, very large batches, LDS too
+// small, or partials that do not fit the workspace that
+// fe_paged_decode_workspace_size describes).
+struct BalancedPlan {
+  int nwg = 0;
+  int states = 0;
+  size_t lds = 0;
+};
+template <int D>
+BalancedPlan plan_balanced(int batch, int hkv, int G, int block_size, int max_len,
+                           size_t ws_limit) {
+  BalancedPlan p;
+  if (!FE_DECODE_BALANCED || block_size % kTile != 0 || batch > kBMaxBatch ||
+      batch < FE_DECODE_BALANCED_MIN_BATCH)
+    return p;
+  const DeviceLimits dl = device_limits();
+  const size_t cap = dl.lds < 160 * 1024 ? (size_t)dl.lds : (size_t)160 * 1024;
+  const size_t sb = bstate_bytes(D, G);
+  const size_t base = BLds<D>::states_off(batch);
+  if (base + (size_t)kBWaves * sb > cap) return p;  // the barrier fallback needs 8 slots
+  int states = (int)((cap - base) / sb);
+  if (states > 64) states = 64;
+  const int64_t tiles_max = (int64_t)hkv * batch * ((max_len + kTile - 1) / kTile);
+  const int64_t per_wg = (int64_t)kBWaves * kBMaxTilesPerWave;
+  int64_t n = dl.cus;
+  if ((tiles_max + per_wg - 1) / per_wg > n) n = (tiles_max + per_wg - 1) / per_wg;
+  const size_t need = kTicketBytes + align256((size_t)2 * n * G * D * sizeof(float)) +
+                      align256((size_t)2 * n * G * sizeof(float));
+  if (n > (1 << 20) || need > ws_limit) return p;
+  p.nwg = (int)n;
+  p.states = states;
+  p.lds = BLds<D>::bytes(batch, G, states);
+  return p;
+}
+
 template <int D>
 int launch_decode(const DecodeArgs& a, hipStream_t stream) {
+  if (a.nwg > 0) {
+    hipLaunchKernelGGL((balanced_decode_kernel<D>), dim3(a.nwg), dim3(kBThreads),
+                       BLds<D>::bytes(a.B, a.G, a.states), stream, a);
+    return FE_LAUNCH_STATUS();
+  }
   const dim3 grid((a.target + 2 * a.B) * a.Hkv);
   if (a.BS % kTile == 0)
     hipLaunchKernelGGL((piece_decode_kernel<D, true>), grid, dim3(kThreads), PieceLds<D>::bytes,
@@ -538,6 +1223,17 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   a.target = target;
   a.max_len = max_len;
   a.scale_log2 = scale * kLog2e;
+  // the balanced kernel's partials ([2N][G][D] and [2N][G]) replace the piece
+  // partials inside the same region of the workspace
+  {
+    const BalancedPlan bp =
+        head_dim == 64 ? plan_balanced<64>(batch, kv_heads, G, block_size, max_len, need)
+                       : plan_balanced<128>(batch, kv_heads, G, block_size, max_len, need);
+    a.nwg = bp.nwg;
+    a.states = bp.states;
+  }
+  if (a.nwg > 0)
+    a.ws_lse = a.ws_o + align256((size_t)2 * a.nwg * G * head_dim * sizeof(float)) / sizeof(float);
   const hipStream_t s = (hipStream_t)stream;
   if (cascade) {
     char* cw = (char*)workspace + need;

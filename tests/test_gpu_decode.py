@@ -382,3 +382,68 @@ def test_shared_prefix_full_c3_against_plain_decode_and_repeatable():
     assert_attention_close(outs[0].cpu().numpy(), plain.cpu().numpy().astype(np.float64),
                            what="full C3 cascade vs plain")
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+# --------------------------------------------------------------------------------------
+# balanced kernel: batches of 128 rows and more are cut into equal tile ranges per
+# workgroup, whatever their context lengths (fe_paged_decode picks it by batch size)
+# --------------------------------------------------------------------------------------
+
+def _with_lengths(seed, lengths, hq, hkv, d, bs=16, fuse=True):
+    """A decode workload whose rows have exactly `lengths` (0 = inactive row)."""
+    w = workloads.make_decode_workload("balanced", seed, len(lengths), hq, hkv, d,
+                                       [max(n, 1) for n in lengths], block_size=bs,
+                                       with_new_kv=fuse)
+    w.context_lens = torch.tensor(lengths, dtype=torch.int32)
+    return w
+
+
+def _random_lengths(seed, batch, lo, hi):
+    return np.random.default_rng(seed).integers(lo, hi + 1, size=batch).tolist()
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", [(12, 2, 128, 16), (14, 2, 64, 16), (16, 1, 128, 32),
+                                         (8, 8, 64, 64), (28, 4, 128, 16), (16, 2, 64, 32)])
+def test_balanced_ragged_batch_with_inactive_rows_and_page_write(hq, hkv, d, bs):
+    lengths = _random_lengths(hq * 13 + d + bs, 160, 1, 700)
+    lengths[1:5] = [1, 16, 17, 3000]
+    for b in range(0, 160, 17):
+        lengths[b] = 0
+    w = _with_lengths(hq + d + bs, lengths, hq, hkv, d, bs)
+    got, dv = run_decode(w)
+    exp, kp, vp = oracle_decode(w)
+    assert torch.count_nonzero(got[0]) == 0 and torch.count_nonzero(got[17]) == 0
+    assert_attention_close(got.numpy(), exp, what=f"balanced {hq}/{hkv}/{d} bs {bs}")
+    assert dv.k_pool.cpu().numpy().tobytes() == kp.tobytes()
+    assert dv.v_pool.cpu().numpy().tobytes() == vp.tobytes()
+
+
+def test_balanced_many_tiny_sequences():
+    """2048 rows of 0..40 tokens, group size 8: workgroup ranges hold many short
+    sequences (the per-segment barrier path when their states outnumber the slots)."""
+    w = _with_lengths(2048, _random_lengths(2048, 2048, 0, 40), 8, 1, 128, fuse=False)
+    got, _ = run_decode(w, fuse=False)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what="2048 tiny rows")
+
+
+def test_balanced_repeated_calls_are_identical_and_share_the_workspace():
+    w = _with_lengths(99, _random_lengths(99, 200, 100, 4000), 12, 2, 128, fuse=False)
+    small = workloads.make_decode_workload("small", 5, 3, 12, 2, 128, [700, 5, 2000])
+    exp, _, _ = oracle_decode(w)
+    exp_small, _, _ = oracle_decode(small)
+    d, ds = w.to(DEV), small.to(DEV)
+    ws = torch.zeros((ops.decode_workspace_bytes(200, 12, 128, w.block_tables.shape[1] * 16, 0),),
+                     dtype=torch.uint8, device=DEV)
+    first = None
+    for rep in range(6):
+        o = ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens,
+                             workspace=ws)
+        os_ = ops.paged_decode(ds.q, ds.k_pool, ds.v_pool, ds.block_tables, ds.context_lens,
+                               workspace=ws)
+        got = o.cpu().numpy()
+        assert_attention_close(got, exp, what=f"rep {rep}")
+        assert_attention_close(os_.cpu().numpy(), exp_small, what=f"small rep {rep}")
+        if first is None:
+            first = got
+        assert (first == got).all(), "results differ between identical calls"
