@@ -49,6 +49,12 @@ SIGNATURES: dict[str, tuple] = {
     "fe_silu_mul": (_i, [_p, _i64, _i, _p, _i, _i, _p]),
     "fe_gemm_skinny_splits": (_i, [_i, _i]),
     "fe_gemm_skinny": (_i, [_p, _i, _i, _p, _i, _p, _i, _p]),
+    "fe_gemm_fused_workspace_size": (_sz, [_i, _i, _i]),
+    "fe_gemm_f16": (_i, [_p, _p, _i, _p, _f, _i, _i, _p, _i, _p, _p, _p, _sz, _p]),
+    "fe_gemm_resid": (_i, [_p, _i, _i, _p, _i, _p, _p, _p, _p, _sz, _p]),
+    "fe_gemm_silu": (_i, [_p, _p, _i, _p, _f, _i, _i, _p, _i, _p, _p, _sz, _p]),
+    "fe_gemm_rope": (_i, [_p, _p, _i, _p, _f, _i, _i, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p,
+                          _p, _sz, _p]),
 }
 
 _LIB: ctypes.CDLL | None = None

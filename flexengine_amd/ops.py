@@ -392,3 +392,108 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     out = torch.empty((rows, inter), dtype=FP16, device=dev)
     _lib.call("fe_silu_mul", ptr, stride, splits, out.data_ptr(), rows, inter, _stream(dev))
     return out
+
+
+# ---------------------------------------------------------------------------------------
+# fused decode-step projections (fe_gemm_f16 / _resid / _silu / _rope)
+# ---------------------------------------------------------------------------------------
+
+class Normed:
+    """The operand of a fused projection given as its RMSNorm inputs: the residual
+    stream r [M, K] fp16, the per-tile sums of r^2 [tiles, M] fp32 that
+    gemm_resid wrote with it, the norm weight [K] and eps."""
+
+    def __init__(self, r: torch.Tensor, ss: torch.Tensor, weight: torch.Tensor, eps: float):
+        if ss.dtype != torch.float32 or ss.ndim != 2 or ss.shape[1] != r.shape[0]:
+            raise ValueError("ss must be float32 [tiles, rows]")
+        self.r, self.ss, self.weight, self.eps = r, ss, weight, float(eps)
+
+
+def _operand(x, weight: torch.Tensor):
+    """(x ptr, ss ptr, ss tiles, norm weight ptr, eps, M, K) of a plain fp16 operand
+    or a Normed one, checked against weight [N, K]."""
+    if isinstance(x, Normed):
+        r, ss_ptr, tiles, nw, eps = x.r, x.ss.data_ptr(), x.ss.shape[0], x.weight.data_ptr(), x.eps
+        if x.weight.shape != (r.shape[1],) or x.weight.dtype != FP16:
+            raise ValueError("norm weight must be float16 [K]")
+    else:
+        r, ss_ptr, tiles, nw, eps = x, None, 0, None, 0.0
+    if r.ndim != 2 or r.dtype != FP16 or not r.is_contiguous():
+        raise ValueError("operand must be contiguous float16 [M, K]")
+    if weight.ndim != 2 or weight.dtype != FP16 or not weight.is_contiguous() or weight.shape[1] != r.shape[1]:
+        raise ValueError("weight must be contiguous float16 [N, K]")
+    return r, ss_ptr, tiles, nw, eps
+
+
+def _fused_ws(dev: torch.device, m: int, n: int, k: int) -> torch.Tensor:
+    """The per-device workspace of the fused projections (split-K tickets + partial
+    tiles), grown when a larger shape needs more; zero-filled when created."""
+    need = int(_lib.load().fe_gemm_fused_workspace_size(m, n, k))
+    return decode_workspace(dev, need, kind="gemm")
+
+
+def gemm_f16(x, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """fp16(x @ weight^T + bias) for M <= 32 rows; x is fp16 [M, K] or Normed."""
+    r, ss, tiles, nw, eps = _operand(x, weight)
+    dev = _require_gpu(r, weight, bias)
+    out = torch.empty((r.shape[0], weight.shape[0]), dtype=FP16, device=dev)
+    ws = _fused_ws(dev, r.shape[0], weight.shape[0], r.shape[1])
+    _lib.call("fe_gemm_f16", r.data_ptr(), ss, tiles, nw, eps, r.shape[0], r.shape[1],
+              weight.data_ptr(), weight.shape[0], _ptr(bias), out.data_ptr(), ws.data_ptr(),
+              ws.numel(), _stream(dev))
+    return out
+
+
+def gemm_resid(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
+               out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(r, ss): r = fp16(fp16(x @ weight^T) + residual) [M, N] and the per-16-column
+    sums of r^2 [ceil(N/16), M] that the next fused projection normalises with."""
+    r_in, _, _, _, _ = _operand(x, weight)
+    dev = _require_gpu(r_in, weight, residual)
+    m, n = r_in.shape[0], weight.shape[0]
+    if residual.shape != (m, n) or residual.dtype != FP16 or not residual.is_contiguous():
+        raise ValueError("residual must be contiguous float16 [M, N]")
+    out = torch.empty((m, n), dtype=FP16, device=dev) if out is None else out
+    if out.data_ptr() == residual.data_ptr() or out.data_ptr() == r_in.data_ptr():
+        raise ValueError("out must not alias the residual or the operand")
+    ss = torch.empty(((n + 15) // 16, m), dtype=torch.float32, device=dev)
+    ws = _fused_ws(dev, m, n, r_in.shape[1])
+    _lib.call("fe_gemm_resid", r_in.data_ptr(), m, r_in.shape[1], weight.data_ptr(), n,
+              residual.data_ptr(), out.data_ptr(), ss.data_ptr(), ws.data_ptr(), ws.numel(),
+              _stream(dev))
+    return out, ss
+
+
+def gemm_silu(x, weight: torch.Tensor) -> torch.Tensor:
+    """fp16(silu(g) * u) [M, I] of the products with weight = [gate; up] [2I, K]."""
+    r, ss, tiles, nw, eps = _operand(x, weight)
+    dev = _require_gpu(r, weight)
+    if weight.shape[0] % 2:
+        raise ValueError("weight must stack gate and up rows")
+    out = torch.empty((r.shape[0], weight.shape[0] // 2), dtype=FP16, device=dev)
+    ws = _fused_ws(dev, r.shape[0], weight.shape[0], r.shape[1])
+    _lib.call("fe_gemm_silu", r.data_ptr(), ss, tiles, nw, eps, r.shape[0], r.shape[1],
+              weight.data_ptr(), weight.shape[0], out.data_ptr(), ws.data_ptr(), ws.numel(),
+              _stream(dev))
+    return out
+
+
+def gemm_rope(x, weight: torch.Tensor, bias: torch.Tensor | None, positions: torch.Tensor,
+              inv_freq: torch.Tensor, num_q_heads: int, kv_heads: int, head_dim: int):
+    """q [M, Hq, D], k, v [M, Hkv, D] of weight = [q; k; v] with bias and RoPE on q, k."""
+    r, ss, tiles, nw, eps = _operand(x, weight)
+    dev = _require_gpu(r, weight, bias, positions, inv_freq)
+    if weight.shape[0] != (num_q_heads + 2 * kv_heads) * head_dim:
+        raise ValueError("weight rows do not match the head configuration")
+    m = r.shape[0]
+    if positions.dtype != torch.int64 or positions.shape != (m,):
+        raise ValueError("positions must be int64 [rows]")
+    q = torch.empty((m, num_q_heads, head_dim), dtype=FP16, device=dev)
+    k = torch.empty((m, kv_heads, head_dim), dtype=FP16, device=dev)
+    v = torch.empty_like(k)
+    ws = _fused_ws(dev, m, weight.shape[0], r.shape[1])
+    _lib.call("fe_gemm_rope", r.data_ptr(), ss, tiles, nw, eps, m, r.shape[1], weight.data_ptr(),
+              _ptr(bias), positions.data_ptr(), inv_freq.data_ptr(), num_q_heads, kv_heads,
+              head_dim, q.data_ptr(), k.data_ptr(), v.data_ptr(), ws.data_ptr(), ws.numel(),
+              _stream(dev))
+    return q, k, v

@@ -81,6 +81,58 @@ int fe_gemm_skinny_splits(int N, int K);
 int fe_gemm_skinny(const void* x, int M, int K, const void* W, int N, float* partials,
                    int splits, fe_stream_t stream);
 
+/*
+ * Decode-step projections with their element-wise neighbours fused
+ * (M <= 32 rows, K a multiple of 32; the workgroups of a 16-row output tile
+ * reduce K among themselves -- split-K partial tiles meet in `workspace` and the
+ * last workgroup adds them in split order -- so results are final fp16 values,
+ * deterministic from call to call).  workspace: at least
+ * fe_gemm_fused_workspace_size(M, N, K) bytes, 256-byte aligned, zero-filled
+ * before its first use; every call leaves it ready for the next (calls that
+ * overlap in time need separate workspaces).
+ *
+ * Optional RMSNorm prologue, shared by fe_gemm_f16, fe_gemm_silu and
+ * fe_gemm_rope: with x_ss == NULL the operand is x [M, K] itself; otherwise x
+ * is the un-normalised residual stream r [M, K] and x_ss [ss_tiles][M] the
+ * per-tile sums of r^2 written by fe_gemm_resid, and the operand is
+ *   fp16(norm_w * fp16(r * rsqrt(sum_t x_ss[t][m] / K + eps)))
+ * (transformers' Qwen2RMSNorm, as fe_rmsnorm computes it).
+ */
+
+/* Workspace bytes of the fused projections for an [N, K] weight and M rows. */
+size_t fe_gemm_fused_workspace_size(int M, int N, int K);
+
+/* out [M, N] = fp16(operand @ W^T + bias); bias [N] may be NULL.  The LM head
+ * with the final norm (qwen2.py:185-186). */
+int fe_gemm_f16(const void* x, const float* x_ss, int ss_tiles, const void* norm_w, float eps,
+                int M, int K, const void* W, int N, const void* bias, void* out,
+                void* workspace, size_t workspace_bytes, fe_stream_t stream);
+
+/* r = fp16(fp16(x @ W^T) + residual), written to out [M, N] (may alias
+ * nothing the call reads), and out_ss [ceil(N/16)][M] = sum of r^2 over each
+ * 16-column tile: the o and down projections with the residual adds of
+ * qwen2.py:129-130,183-184, producing the next RMSNorm's input. */
+int fe_gemm_resid(const void* x, int M, int K, const void* W, int N, const void* residual,
+                  void* out, float* out_ss, void* workspace, size_t workspace_bytes,
+                  fe_stream_t stream);
+
+/* W = [gate; up] ([2I, K]); out [M, I] = fp16(fp16(silu(g)) * u) with
+ * g, u = fp16 of the gate / up products: the gate/up projection and act_fn
+ * product of HF Qwen2MLP (qwen2.py:130,184). */
+int fe_gemm_silu(const void* x, const float* x_ss, int ss_tiles, const void* norm_w, float eps,
+                 int M, int K, const void* W, int N, void* out, void* workspace,
+                 size_t workspace_bytes, fe_stream_t stream);
+
+/* W = [q; k; v] ([(Hq + 2 Hkv) * D, K]) with bias; writes q_out [M, Hq, D],
+ * k_out and v_out [M, Hkv, D] with RoPE on q and k exactly as fe_rope_qkv
+ * computes it (positions int64 [M], inv_freq fp32 [D/2]; D a multiple of 16):
+ * the q/k/v projection, split and _rope of qwen2.py:67-77,152-155. */
+int fe_gemm_rope(const void* x, const float* x_ss, int ss_tiles, const void* norm_w, float eps,
+                 int M, int K, const void* W, const void* bias, const int64_t* positions,
+                 const float* inv_freq, int num_q_heads, int kv_heads, int head_dim,
+                 void* q_out, void* k_out, void* v_out, void* workspace,
+                 size_t workspace_bytes, fe_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
