@@ -134,8 +134,14 @@ __device__ __forceinline__ int wave_max_i(int v) {
 
 // Chunk size in quads.  Besides ~target pieces in total, no sequence is cut
 // into more than kMaxPieces pieces, which bounds the merge of one sequence to
-// four rounds of 16 partials.
+// four rounds of 16 partials, and no piece holds fewer than kMinChunk quads
+// unless its sequence is shorter: at small batches, pieces of a quad or two
+// spend more on their merge than they gain in parallelism.
 constexpr int kMaxPieces = 64;
+#ifndef FE_MIN_CHUNK
+#define FE_MIN_CHUNK 3
+#endif
+constexpr int kMinChunk = FE_MIN_CHUNK;
 
 // First key of sequence b's suffix (0 without a shared prefix); <= its length.
 __device__ __forceinline__ int suffix_start(const int32_t* tok0, int b, int L) {
@@ -189,7 +195,7 @@ __device__ __forceinline__ bool find_piece(const int32_t* ctx, const int32_t* to
   int chunk = (sum + target - 1) / target;
   const int floor_chunk = (longest + kMaxPieces - 1) / kMaxPieces;
   chunk = chunk > floor_chunk ? chunk : floor_chunk;
-  chunk = chunk > 0 ? chunk : 1;
+  chunk = chunk > kMinChunk ? chunk : kMinChunk;
 
   int carry = 0;
   for (int base = 0; base < B; base += kWave) {
