@@ -103,6 +103,53 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
   }
 }
 
+// The same RMSNorm for fp16 rows (no partials), one wave per row: each lane
+// holds NCH 16-byte chunks of the row (hidden <= 512 * NCH), so the whole row
+// is one batch of loads and the sum of squares one cross-lane reduction -- no
+// LDS, no barrier.  Four rows per 256-thread workgroup.
+template <int NCH>
+__global__ __launch_bounds__(256) void rmsnorm_wave_kernel(
+    const f16* __restrict__ x, const f16* residual, f16* residual_out,  // may alias (in place)
+    const f16* __restrict__ weight, f16* __restrict__ out, int rows, int hidden, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t base = (int64_t)row * hidden;
+  f16x8 xv[NCH], rv[NCH], wv[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e0 = (c * kWave + lane) * 8;
+    const bool ok = e0 < hidden;
+    xv[c] = ok ? ld16(x + base + e0) : f16x8{};
+    rv[c] = ok && residual ? ld16(residual + base + e0) : f16x8{};
+    wv[c] = ok ? ld16(weight + e0) : f16x8{};
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const f16 r = residual ? (f16)((float)xv[c][e] + (float)rv[c][e]) : xv[c][e];
+      xv[c][e] = r;
+      ss += (float)r * (float)r;
+    }
+    const int e0 = (c * kWave + lane) * 8;
+    if (residual_out && e0 < hidden) st16(residual_out + base + e0, xv[c]);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, kWave);
+  const float inv = rsqrtf(ss / (float)hidden + eps);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e0 = (c * kWave + lane) * 8;
+    if (e0 >= hidden) continue;
+    f16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (f16)((float)wv[c][e] * round16((float)xv[c][e] * inv));
+    st16(out + base + e0, o);
+  }
+}
+
 // RoPE (rotate_half form) on the q and k heads of a fused projection row
 // [q: Hq*D | k: Hkv*D | v: Hkv*D]; v is copied.  One thread per (row, head,
 // pair i < D/2): angle = pos * inv_freq[i] in fp32, c = fp16(cos), s = fp16(sin),
@@ -168,6 +215,24 @@ extern "C" int fe_rmsnorm(const void* x, int x_splits, const void* residual, voi
   if (hidden > kNormThreads * kNormMaxPerThread) return FE_ERR_UNSUPPORTED;
   if (rows == 0) return FE_OK;
   FE_CHECK_ARG(x && weight && out);
+  const auto al = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (x_splits == 0 && hidden % 8 == 0 && al(x) && al(residual) && al(residual_out) &&
+      al(weight) && al(out)) {
+    const int nch = (hidden + 511) / 512;
+    const dim3 grid((rows + 3) / 4);
+#define FE_NORM_WAVE(N)                                                                        \
+  hipLaunchKernelGGL(rmsnorm_wave_kernel<N>, grid, dim3(256), 0, (hipStream_t)stream,           \
+                     (const f16*)x, (const f16*)residual, (f16*)residual_out, (const f16*)weight, \
+                     (f16*)out, rows, hidden, eps)
+    if (nch <= 1) FE_NORM_WAVE(1);
+    else if (nch <= 2) FE_NORM_WAVE(2);
+    else if (nch <= 3) FE_NORM_WAVE(3);
+    else if (nch <= 4) FE_NORM_WAVE(4);
+    else if (nch <= 8) FE_NORM_WAVE(8);
+    else FE_NORM_WAVE(16);
+#undef FE_NORM_WAVE
+    return FE_LAUNCH_STATUS();
+  }
   const Src src{x, hidden, x_splits, nullptr};
   const int per = (hidden + kNormThreads - 1) / kNormThreads;
 #define FE_NORM_LAUNCH(P)                                                                        \

@@ -37,15 +37,18 @@ def ulps(a, b):
 
 @pytest.mark.parametrize("rows,hidden", [(1, 1536), (5, 1536), (64, 896), (3, 8192)])
 def test_rmsnorm_matches_torch(rows, hidden):
+    """The sum of squares adds in another order than PyTorch's, so fp16(r * rsqrt(..))
+    can round one ulp apart for a rare element, which the weight multiply scales by |w|
+    (here N(0, 1)): at most 2 ulps, nearly all elements bit-identical."""
     x, res, w = randn(rows, hidden, seed=1), randn(rows, hidden, seed=2), randn(hidden, seed=3)
     out, _ = ops.rmsnorm(x, w, 1e-6)
     want, _ = torch_rmsnorm(x, w, 1e-6)
-    assert ulps(out, want) <= 1
+    assert ulps(out, want) <= 2 and (out == want).float().mean() > 0.999
     r = res.clone()
     out, r2 = ops.rmsnorm(x, w, 1e-6, residual=r)
     want, want_r = torch_rmsnorm(x, w, 1e-6, residual=res)
     assert r2 is r and torch.equal(r, want_r)          # residual add is bit-exact
-    assert ulps(out, want) <= 1
+    assert ulps(out, want) <= 2 and (out == want).float().mean() > 0.999
 
 
 def test_rmsnorm_reads_skinny_partials():
