@@ -14,9 +14,13 @@
 //             SILU   act = fp16(fp16(silu(gate)) * up) for W = [gate; up]
 //             ROPE   q, k, v of W = [q; k; v] with bias and rotate-half RoPE
 //
-// Work: one workgroup per 16-row tile of the output (no split-K across
-// workgroups, so every result is final inside its workgroup); its waves cut K
-// into contiguous slices and add their products through LDS.  The 16 weight
+// Work: one workgroup per 16-row tile of the output; its waves cut K into
+// contiguous slices and add their products through LDS.  When the tiles alone
+// leave the chip short of ~512 workgroups (q/k/v, o: 128 tiles), ks_for()
+// gives each tile several workgroups over disjoint K ranges: each writes its
+// fp32 partial tile with device-coherent stores and takes a per-tile ticket,
+// and the last one adds the partials in split order and runs the epilogue, so
+// the element-wise epilogue still sees the whole sum.  The 16 weight
 // rows of a tile are the A operand of v_mfma_f32_16x16x16_f16 loaded straight
 // from HBM (lane (g, n): row n, 16 bytes at k0 + 32j + 8g), x the B operand.
 // For SILU a tile holds 8 gate rows and the 8 up rows of the same columns, for

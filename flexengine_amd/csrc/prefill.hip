@@ -46,6 +46,10 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kBlockKeys = 32;  // one 16x16x32 PV step per block
 constexpr int kMaxSplits = 8;   // key splits per row block (plan() clamps to it)
+// Two 16-row tiles per wave (RT = 2) once the rows fill this many 128-row blocks;
+// below it the extra blocks of RT = 1 fill the CUs better (measured: 1377 new tokens
+// x 12 heads run slower with RT = 2).
+constexpr int kRt2Blocks = 512;
 
 template <int D, int RT>
 struct PCfg {
@@ -510,7 +514,7 @@ struct Plan {
 inline Plan plan(int num_seqs, int total_q, int num_q_heads, int kv_heads) {
   const int64_t rows = (int64_t)total_q * num_q_heads;  // (token, query head) rows
   Plan p;
-  p.rt = rows >= (int64_t)512 * PCfg<128, 2>::ROWS ? 2 : 1;
+  p.rt = rows >= (int64_t)kRt2Blocks * PCfg<128, 2>::ROWS ? 2 : 1;
   const int per = kWaves * 16 * p.rt;
   const int G = num_q_heads / kv_heads;
   p.blocks = (int)(((int64_t)total_q * G + per - 1) / per) + num_seqs;
