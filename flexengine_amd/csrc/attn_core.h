@@ -300,7 +300,7 @@ struct TileListCore {
   __device__ __forceinline__ static f16x8 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
                                                    uint32_t soff) {
     return __builtin_bit_cast(f16x8,
-                              __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kStreamPolicy));
+                              __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kPagePolicy));
   }
   __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const f16* pool, int64_t base,
                                                              int rows) const {

@@ -70,14 +70,17 @@ __device__ __forceinline__ int wave_scan_incl_i(int v) {
 
 // ---- 16-byte global accesses ------------------------------------------------
 
-// Cache policy of buffer loads that stream data read once per launch (the K/V
-// pages of a decode step, GEMM weights): nt (non-temporal, bit 1).  On MI355X
-// it raised a read-once stream of 67 MB of scattered 8 KiB pages from 4.7 to
-// 5.5 TB/s and a 268 MB linear read from 5.6 to 6.5 TB/s.
-#ifndef FE_STREAM_POLICY
-#define FE_STREAM_POLICY 2
-#endif
-constexpr int kStreamPolicy = FE_STREAM_POLICY;
+// Cache policies of the K/V page loads (buffer-instruction aux bits).
+// kPagePolicy (default caching) for kernels that read whole contexts: one page
+// can be read by many rows of a launch (a prefix cache maps a shared prefix into
+// every member's block table), and the L2 / Infinity Cache then serve the
+// repeats -- at B = 256 with 8 groups of 32 rows sharing 2048 tokens, 110 us per
+// decode step vs 162 us with non-temporal loads; read-once batches are
+// unaffected (B = 64: 20.8 us either way).
+// kStreamPolicy = nt (non-temporal, bit 1) for the cascade's suffix pass, whose
+// pages are private to one row and read once: 83 vs 89 us at the same shape.
+constexpr int kPagePolicy = 0;
+constexpr int kStreamPolicy = 2;
 
 __device__ __forceinline__ f16x8 ld16(const f16* p) {
   return *reinterpret_cast<const f16x8*>(p);

@@ -466,6 +466,7 @@ extern "C" int fe_gemm_resid(const void* x, int M, int K, const void* W, int N,
   const int rc = fill_common(a, x, nullptr, 0, nullptr, 0.f, M, K, W, N);
   if (rc != FE_OK || M == 0) return rc;
   FE_CHECK_ARG(residual && out && out_ss);
+  FE_CHECK_ARG(out != residual && out != x);  // the header: out aliases nothing read
   a.residual = (const f16*)residual;
   a.out = (f16*)out;
   a.out_ss = out_ss;

@@ -382,6 +382,9 @@ void piece_decode_kernel(const DecodeArgs a) {
 
 // ---- balanced decode (block sizes that are multiples of 16) ----------------------
 //
+// Runs the suffix pass of the shared-prefix decode at large batches (many short
+// private suffixes, each read once: its page loads are non-temporal).
+//
 // Work is cut at 16-token tile granularity over one global order of all
 // (sequence, KV head, tile) triples -- sequence-major, then KV head, then
 // tile -- so every workgroup receives the same number of tiles whatever the
@@ -1070,10 +1073,13 @@ DeviceLimits device_limits() {
 #ifndef FE_DECODE_BALANCED
 #define FE_DECODE_BALANCED 1
 #endif
-// Batches below this many rows run the piece kernel: on MI355X it measured
-// faster there (B = 8: 7.1 vs 11.5 us; B = 64, C2: 20.8 vs 25.0 us), and the
-// balanced kernel faster above (B = 256, C3: 137.7 vs 160.9 us plain, 83.6
-// vs 99.3 us with shared prefixes).
+// The balanced kernel runs the suffix pass of the shared-prefix decode for
+// batches of this many rows and more: there it measured faster than the piece
+// kernel (B = 256 with 8 groups of 32 sharing 2048 tokens: 83 vs 99 us per
+// step; its suffixes are many and short).  The plain decode keeps the piece
+// kernel at every batch size: with default-cached loads it measured faster
+// (same B = 256 batch without the cascade: 110 vs 115 us; B = 8: 7.1 vs
+// 11.5 us; B = 64: 20.8 vs 25.0 us).
 #ifndef FE_DECODE_BALANCED_MIN_BATCH
 #define FE_DECODE_BALANCED_MIN_BATCH 128
 #endif
@@ -1225,7 +1231,9 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   a.scale_log2 = scale * kLog2e;
   // the balanced kernel's partials ([2N][G][D] and [2N][G]) replace the piece
   // partials inside the same region of the workspace
-  {
+  a.nwg = 0;
+  a.states = 0;
+  if (cascade) {
     const BalancedPlan bp =
         head_dim == 64 ? plan_balanced<64>(batch, kv_heads, G, block_size, max_len, need)
                        : plan_balanced<128>(batch, kv_heads, G, block_size, max_len, need);

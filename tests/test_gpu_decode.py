@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from flexengine_amd import attention, ops, workloads
+from flexengine_amd import _lib, attention, ops, workloads
 from flexengine_amd.kv_cache import CacheLayout, PagedKVCache
 from oracle import paged_ref as R
 from tests.parity import assert_attention_close
@@ -385,8 +385,9 @@ def test_shared_prefix_full_c3_against_plain_decode_and_repeatable():
 
 
 # --------------------------------------------------------------------------------------
-# balanced kernel: batches of 128 rows and more are cut into equal tile ranges per
-# workgroup, whatever their context lengths (fe_paged_decode picks it by batch size)
+# large batches: the plain decode (piece kernel) at 160 and 2048 rows, and the
+# shared-prefix decode, whose suffix pass runs the balanced kernel from 128 rows
+# (equal tile ranges per workgroup, whatever the context-length mix)
 # --------------------------------------------------------------------------------------
 
 def _with_lengths(seed, lengths, hq, hkv, d, bs=16, fuse=True):
@@ -402,9 +403,12 @@ def _random_lengths(seed, batch, lo, hi):
     return np.random.default_rng(seed).integers(lo, hi + 1, size=batch).tolist()
 
 
-@pytest.mark.parametrize("hq,hkv,d,bs", [(12, 2, 128, 16), (14, 2, 64, 16), (16, 1, 128, 32),
-                                         (8, 8, 64, 64), (28, 4, 128, 16), (16, 2, 64, 32)])
-def test_balanced_ragged_batch_with_inactive_rows_and_page_write(hq, hkv, d, bs):
+LARGE_SHAPES = [(12, 2, 128, 16), (14, 2, 64, 16), (16, 1, 128, 32), (8, 8, 64, 64),
+                (28, 4, 128, 16), (16, 2, 64, 32)]
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", LARGE_SHAPES)
+def test_large_ragged_batch_with_inactive_rows_and_page_write(hq, hkv, d, bs):
     lengths = _random_lengths(hq * 13 + d + bs, 160, 1, 700)
     lengths[1:5] = [1, 16, 17, 3000]
     for b in range(0, 160, 17):
@@ -413,32 +417,71 @@ def test_balanced_ragged_batch_with_inactive_rows_and_page_write(hq, hkv, d, bs)
     got, dv = run_decode(w)
     exp, kp, vp = oracle_decode(w)
     assert torch.count_nonzero(got[0]) == 0 and torch.count_nonzero(got[17]) == 0
-    assert_attention_close(got.numpy(), exp, what=f"balanced {hq}/{hkv}/{d} bs {bs}")
+    assert_attention_close(got.numpy(), exp, what=f"large {hq}/{hkv}/{d} bs {bs}")
     assert dv.k_pool.cpu().numpy().tobytes() == kp.tobytes()
     assert dv.v_pool.cpu().numpy().tobytes() == vp.tobytes()
 
 
-def test_balanced_many_tiny_sequences():
-    """2048 rows of 0..40 tokens, group size 8: workgroup ranges hold many short
-    sequences (the per-segment barrier path when their states outnumber the slots)."""
+def test_large_batch_of_tiny_sequences():
     w = _with_lengths(2048, _random_lengths(2048, 2048, 0, 40), 8, 1, 128, fuse=False)
     got, _ = run_decode(w, fuse=False)
     exp, _, _ = oracle_decode(w)
     assert_attention_close(got.numpy(), exp, what="2048 tiny rows")
 
 
-def test_balanced_repeated_calls_are_identical_and_share_the_workspace():
-    w = _with_lengths(99, _random_lengths(99, 200, 100, 4000), 12, 2, 128, fuse=False)
+@pytest.mark.parametrize("hq,hkv,d,bs", LARGE_SHAPES)
+def test_balanced_cascade_ragged_batch_with_inactive_rows_and_page_write(hq, hkv, d, bs):
+    """160 rows: groups of 48, 32, 24 and 1 members (prefixes of 256, 64, 1000 and
+    512 tokens; whole blocks shared), then 55 rows of their own.  Inactive rows in a
+    group, as its only member, and outside; rows of 1, 16, 17 and 3000 tokens.  The
+    decoded token is written past each member's prefix, into its private block."""
+    groups = [(48, 256), (32, 64), (24, 1000), (1, 512)]
+    lens = {50: 0, 104: 0, 130: 0, 105: 1, 106: 16, 107: 17, 108: 3000}
+    w = workloads.shared_prefix_workload(hq * 13 + d + bs, groups, singles=55, hq=hq, hkv=hkv,
+                                         d=d, block_size=bs, tail=(1, 700), member_lens=lens,
+                                         with_new_kv=True)
+    assert w.batch == 160
+    got, dv = run_shared_prefix(w, fuse=True)
+    exp, kp, vp = oracle_decode(w)
+    for b in (50, 104, 130):
+        assert torch.count_nonzero(got[b]) == 0, f"inactive row {b}"
+    assert_attention_close(got.numpy(), exp, what=f"balanced cascade {hq}/{hkv}/{d} bs {bs}")
+    assert dv.k_pool.cpu().numpy().tobytes() == kp.tobytes()
+    assert dv.v_pool.cpu().numpy().tobytes() == vp.tobytes()
+
+
+def test_balanced_cascade_many_tiny_sequences():
+    """2048 rows, group size 8: 200 groups of 4 sharing one 16-token block with
+    suffixes of 0..40 tokens (members ending at or inside the prefix included), and
+    1248 rows of 0..40 tokens: workgroup ranges hold many short segments (the
+    per-segment barrier path when their states outnumber the slots)."""
+    w = workloads.shared_prefix_workload(2048, [(4, 16)] * 200, singles=1248, hq=8, hkv=1,
+                                         d=128, tail=(0, 40), member_lens={1: 5, 2: 0, 9: 16})
+    assert w.batch == 2048
+    got, _ = run_shared_prefix(w)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what="2048 tiny rows, cascade")
+    assert torch.count_nonzero(got[2]) == 0
+
+
+def test_balanced_cascade_repeated_calls_are_identical_and_share_the_workspace():
+    """The cascade at 200 rows and a 3-row plain decode alternate on one workspace
+    (its split tickets are shared): every call is right and the large one is
+    bit-identical from call to call."""
+    w = workloads.shared_prefix_workload(99, [(50, 512), (50, 1024)], singles=100,
+                                         tail=(100, 3000))
     small = workloads.make_decode_workload("small", 5, 3, 12, 2, 128, [700, 5, 2000])
     exp, _, _ = oracle_decode(w)
     exp_small, _, _ = oracle_decode(small)
     d, ds = w.to(DEV), small.to(DEV)
-    ws = torch.zeros((ops.decode_workspace_bytes(200, 12, 128, w.block_tables.shape[1] * 16, 0),),
-                     dtype=torch.uint8, device=DEV)
+    go, pl = d.meta["group_offsets"].to(DEV), d.meta["prefix_lens"].to(DEV)
+    need = _lib.load().fe_paged_decode_shared_prefix_workspace_size(
+        w.batch, 12, 2, 128, w.block_tables.shape[1] * 16, 2, 0)
+    ws = torch.zeros((need,), dtype=torch.uint8, device=DEV)
     first = None
     for rep in range(6):
-        o = ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens,
-                             workspace=ws)
+        o = ops.paged_decode_shared_prefix(d.q, d.k_pool, d.v_pool, d.block_tables,
+                                           d.context_lens, go, pl, workspace=ws)
         os_ = ops.paged_decode(ds.q, ds.k_pool, ds.v_pool, ds.block_tables, ds.context_lens,
                                workspace=ws)
         got = o.cpu().numpy()
