@@ -155,6 +155,7 @@ __device__ __forceinline__ int suffix_start(const int32_t* tok0, int b, int L) {
 
 struct Piece {
   int b;         // sequence
+  int id;        // piece id, sequence-major: the slot of its partial in a merge
   int split;     // index of this piece within the sequence
   int nsplit;    // pieces of this sequence
   int L;         // context length of the sequence
@@ -163,11 +164,22 @@ struct Piece {
   int tok_end;   // one past the last key position of the piece
 };
 
-// Finds the piece with id `item`; false when item is past the last piece, in
-// which case `total` receives the number of pieces.  Two passes over the
-// sequences (quad totals -> chunk, then a prefix sum of pieces); the lengths
-// of the first 64 sequences are loaded once and kept in registers for both,
-// so a batch of up to 64 costs one round trip to memory.
+// Finds the piece that workgroup slot `item` runs; false when item is past the
+// last piece, in which case `total` receives the number of pieces.
+//
+// Pieces are numbered sequence-major (sequence b's pieces are ids first_b ..
+// first_b + nsplit_b - 1, the slots of its merge) but handed out largest
+// first: slots 0.. take every piece of exactly `chunk` quads, then come the
+// sequences' remainders of at least chunk/2 quads, then the smaller ones.
+// Workgroups start in slot order as compute units free up, so the short
+// pieces fill the gaps left by compute units that finished early (the HBM
+// service a CU receives varies by several microseconds over a launch), and
+// the launch ends more evenly than in sequence order.
+//
+// Three passes over the sequences (quad totals -> chunk; piece counts per
+// class; the search); the lengths of the first 64 sequences are loaded once
+// and kept in registers, so a batch of up to 64 costs one round trip to
+// memory.
 __device__ __forceinline__ bool find_piece(const int32_t* ctx, const int32_t* tok0, int B,
                                            int max_len, int target, int item, Piece& pc,
                                            int& total) {
@@ -200,34 +212,66 @@ __device__ __forceinline__ bool find_piece(const int32_t* ctx, const int32_t* to
   chunk = chunk > floor_chunk ? chunk : floor_chunk;
   chunk = chunk > kMinChunk ? chunk : kMinChunk;
 
-  int carry = 0;
-  for (int base = 0; base < B; base += kWave) {
+  // quads of sequence base + lane (0 past the batch)
+  auto quads = [&](int base, int& L, int& t0) __attribute__((always_inline)) {
     const int b = base + lane;
-    int L = L0, t0 = s0;
-    if (base > 0) {
+    if (base == 0) {
+      L = L0;
+      t0 = s0;
+    } else {
       L = b < B ? seq_len(ctx, b, max_len) : 0;
       t0 = b < B ? suffix_start(tok0, b, L) : 0;
     }
-    const int nq = (L - t0 + 63) >> 6;
-    const int ns = (nq + chunk - 1) / chunk;
-    const int incl = wave_scan_incl_i(ns) + carry;
-    const int excl = incl - ns;
-    const unsigned long long hit = __ballot(b < B && item >= excl && item < incl);
+    return (L - t0 + 63) >> 6;
+  };
+  // size class of a sequence's last piece: 0 none, 1 at least chunk/2 quads, 2 smaller
+  auto rem_class = [&](int nq) __attribute__((always_inline)) {
+    const int r = nq % chunk;
+    return r == 0 ? 0 : (2 * r >= chunk ? 1 : 2);
+  };
+
+  int nfull = 0, nbig = 0;
+  for (int base = 0; base < B; base += kWave) {
+    int L, t0;
+    const int nq = quads(base, L, t0);
+    nfull += wave_sum_i(nq / chunk);
+    nbig += wave_sum_i(rem_class(nq) == 1 ? 1 : 0);
+  }
+  nfull = __builtin_amdgcn_readfirstlane(nfull);
+  nbig = __builtin_amdgcn_readfirstlane(nbig);
+  const int cls = item < nfull ? 0 : (item < nfull + nbig ? 1 : 2);
+  const int idx = item - (cls == 0 ? 0 : (cls == 1 ? nfull : nfull + nbig));
+
+  int carry = 0, carry_id = 0;
+  for (int base = 0; base < B; base += kWave) {
+    const int b = base + lane;
+    int L, t0;
+    const int nq = quads(base, L, t0);
+    const int nf = nq / chunk;
+    const int rc = rem_class(nq);
+    const int ns = nf + (rc != 0 ? 1 : 0);
+    const int cnt = cls == 0 ? nf : (rc == cls ? 1 : 0);
+    const int incl = wave_scan_incl_i(cnt) + carry;
+    const int excl = incl - cnt;
+    const int incl_id = wave_scan_incl_i(ns) + carry_id;
+    const unsigned long long hit = __ballot(b < B && idx >= excl && idx < incl);
     if (hit) {
       const int src = __builtin_ctzll(hit);
       pc.b = base + src;
       pc.L = readlane_i(L, src);
       pc.tok0 = readlane_i(t0, src);
       pc.nsplit = readlane_i(ns, src);
-      pc.split = item - readlane_i(excl, src);
+      pc.split = cls == 0 ? idx - readlane_i(excl, src) : readlane_i(nf, src);
+      pc.id = readlane_i(incl_id, src) - pc.nsplit + pc.split;
       pc.tok_begin = pc.tok0 + pc.split * chunk * 64;
       const int e = pc.tok0 + (pc.split + 1) * chunk * 64;
       pc.tok_end = e < pc.L ? e : pc.L;
       return true;
     }
     carry = readlane_i(incl, kWave - 1);
+    carry_id = readlane_i(incl_id, kWave - 1);
   }
-  total = carry;
+  total = carry_id;
   return false;
 }
 

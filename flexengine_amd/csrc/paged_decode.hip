@@ -353,7 +353,7 @@ void piece_decode_kernel(const DecodeArgs a) {
       } else {
         // device-coherent (sc1) 16-byte stores of this piece's partial output
         const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-            a.ws_o + ((int64_t)item * a.Hq + h * G) * D, 0, G * D * (int)sizeof(float),
+            a.ws_o + ((int64_t)pc.id * a.Hq + h * G) * D, 0, G * D * (int)sizeof(float),
             0x00020000);
         const uint32_t off = (uint32_t)((n * D + 4 * g) * sizeof(float));
 #pragma unroll
@@ -361,7 +361,7 @@ void piece_decode_kernel(const DecodeArgs a) {
           __builtin_amdgcn_raw_buffer_store_b128(
               __builtin_bit_cast(u32x4, ox[xi]), r,
               off + 16 * (w * XW + xi) * (uint32_t)sizeof(float), 0, kSc1);
-        if (w == 0 && g == 0) store_coherent(a.ws_lse + (int64_t)item * a.Hq + hq, M + log2f(den));
+        if (w == 0 && g == 0) store_coherent(a.ws_lse + (int64_t)pc.id * a.Hq + hq, M + log2f(den));
       }
     }
   }
@@ -377,7 +377,7 @@ void piece_decode_kernel(const DecodeArgs a) {
   if (!*flag) return;
   if (threadIdx.x == 0)
     __hip_atomic_store(a.tickets + b * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  merge_pieces<D>(a, b, h, item - pc.split, pc.nsplit, pc.tok0 > 0);
+  merge_pieces<D>(a, b, h, pc.id - pc.split, pc.nsplit, pc.tok0 > 0);
 }
 
 // ---- balanced decode (block sizes that are multiples of 16) ----------------------
