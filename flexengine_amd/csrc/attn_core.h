@@ -84,7 +84,7 @@ __device__ __forceinline__ void softmax_pv_tile(f32x4 sacc, int t0, int limit, f
   mx = fmaxf(mx, shfl_xor_f(mx, 32));
   if (__ballot(mx > m_run + kRescaleSlack)) {  // wave-uniform
     const float m_new = fmaxf(m_run, mx);
-    const float alpha = m_new == kNegInf ? 1.f : exp2f(m_run - m_new);
+    const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);
     l_run *= alpha;
 #pragma unroll
     for (int x = 0; x < C::NX; ++x) o[x] *= alpha;
@@ -93,7 +93,7 @@ __device__ __forceinline__ void softmax_pv_tile(f32x4 sacc, int t0, int limit, f
   const float m_use = m_run == kNegInf ? 0.f : m_run;
   float p[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = exp2f(sv[i] - m_use);
+  for (int i = 0; i < 4; ++i) p[i] = exp2_fast(sv[i] - m_use);
   l_run += (p[0] + p[1]) + (p[2] + p[3]);
   const f16x4 pb = {(f16)p[0], (f16)p[1], (f16)p[2], (f16)p[3]};
   const unsigned char* vb = stage + (4 * g + (n >> 2)) * C::ROWB + (n & 3) * 8;

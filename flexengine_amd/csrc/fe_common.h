@@ -82,6 +82,13 @@ __device__ __forceinline__ int wave_scan_incl_i(int v) {
 constexpr int kPagePolicy = 0;
 constexpr int kStreamPolicy = 2;
 
+// 2^x with the hardware instruction alone (v_exp_f32, ~1 ulp): exp2f adds a
+// range reduction per call so that results below 2^-126 stay denormal instead
+// of flushing to zero.  The softmax probabilities need no such values (they
+// become fp16 operands, whose smallest subnormal is 2^-24) and the reduction
+// cost about 4 VALU instructions per score in the prefill loop.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ f16x8 ld16(const f16* p) {
   return *reinterpret_cast<const f16x8*>(p);
 }

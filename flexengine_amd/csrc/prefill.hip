@@ -178,11 +178,18 @@ void prefill_kernel(const PrefillArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
 
   if constexpr (CASCADE) {
-    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) write_suffix_starts(a);
+    if (blockIdx.x == 0) write_suffix_starts(a);
   }
+  // workgroup i: (KV head, key split) pair i % P, row block i / P (P = Hkv * KS);
+  // the hardware places workgroup i on XCD i % 8, so when P divides 8 or is a
+  // multiple of it every XCD serves fixed pairs -- one KV head and one key
+  // range of every sequence -- and its L2 holds the K/V its row blocks share
+  const int npair = a.Hkv * a.KS;
+  const int item = blockIdx.x / npair;
+  const int pair = blockIdx.x - item * npair;
   RowBlock rb;
-  if (!locate_rows<P::ROWS, CASCADE>(a, blockIdx.x, rb)) return;
-  const int h = blockIdx.y;
+  if (!locate_rows<P::ROWS, CASCADE>(a, item, rb)) return;
+  const int h = pair % a.Hkv;
   const int G = a.G;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -197,7 +204,7 @@ void prefill_kernel(const PrefillArgs a) {
   // keys the row block reads: causal up to its last position, or the prefix
   const int key_end = CASCADE ? rb.ctx : cached + r_last / G + 1;
   // split ks of KS takes an equal share of the row block's key blocks
-  const int ks = blockIdx.z;
+  const int ks = pair / a.Hkv;
   const int nblocks_all = (key_end + kBlockKeys - 1) / kBlockKeys;
   const int per_split = (nblocks_all + a.KS - 1) / a.KS;
   const int kb_lo = min(ks * per_split, nblocks_all);
@@ -251,7 +258,7 @@ void prefill_kernel(const PrefillArgs a) {
   }
 
   // ---- K/V block staging: thread t loads 16-byte chunk t % CPR of key rows
-  //      t / CPR + KPL * i; keys at or past key_end are zero-filled.  The
+  //      t / CPR + KPL * i (keys at or past key_end repeat key_end - 1).  The
   //      block ids a block needs are fetched one iteration before its K/V
   //      loads, so no table access sits in front of a K/V load. ----
   const int32_t* trow = a.tables + (int64_t)(CASCADE ? rb.q0 : rb.s) * a.W;
@@ -271,15 +278,14 @@ void prefill_kernel(const PrefillArgs a) {
   auto load_block = [&](int kb) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < P::LOADS; ++i) {
-      const int key = kb * kBlockKeys + krow + P::KPL * i;
-      const bool ok = key < key_end;
-      const int kc = ok ? key : key_end - 1;
+      // a key at or past key_end reads key key_end - 1 instead: a written
+      // row, so finite, and past every row's position, so the causal mask
+      // gives it probability 0 (no block below unmasked_blocks reaches it)
+      const int kc = min(kb * kBlockKeys + krow + P::KPL * i, key_end - 1);
       const int blk = clamp_block(ids[i], a.NB);
-      const int64_t off = (((int64_t)blk * a.BS + (kc & (a.BS - 1))) * a.Hkv + h) * D + chunk * 8;
-      const f16x8 kv = ld16(a.k_pool + off);
-      const f16x8 vv = ld16(a.v_pool + off);
-      kst[i] = ok ? kv : f16x8{};
-      vst[i] = ok ? vv : f16x8{};
+      const int64_t off = (int64_t)(blk * a.BS + (kc & (a.BS - 1))) * (a.Hkv * D) + h * D + chunk * 8;
+      kst[i] = ld16(a.k_pool + off);
+      vst[i] = ld16(a.v_pool + off);
     }
   };
   auto store_block = [&](int stage) __attribute__((always_inline)) {
@@ -301,6 +307,8 @@ void prefill_kernel(const PrefillArgs a) {
   }
   __syncthreads();
 
+  // Loading two blocks ahead (a second register set) was measured slower: the
+  // extra registers cost a wave per SIMD of occupancy.
   for (int kb = kb_lo; kb < kb_hi; ++kb) {
     const bool more = kb + 1 < kb_hi;
     if (more) {
@@ -346,7 +354,7 @@ void prefill_kernel(const PrefillArgs a) {
       mx = fmaxf(mx, shfl_xor_f(mx, 32));
       if (__ballot(mx > m_run[rt] + kRescaleSlack)) {  // wave-uniform
         const float m_new = fmaxf(m_run[rt], mx);
-        const float alpha = m_new == kNegInf ? 1.f : exp2f(m_run[rt] - m_new);
+        const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run[rt] - m_new);
         l_run[rt] *= alpha;
 #pragma unroll
         for (int x = 0; x < P::NX; ++x) o[rt][x] *= alpha;
@@ -359,7 +367,7 @@ void prefill_kernel(const PrefillArgs a) {
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float e = exp2f(sv[kt][i] - m_use);
+          const float e = exp2_fast(sv[kt][i] - m_use);
           lsum += e;
           p[4 * kt + i] = (f16)e;
         }
@@ -435,12 +443,12 @@ void prefill_kernel(const PrefillArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials are complete
   __syncthreads();
   if (tid == 0)
-    last = __hip_atomic_fetch_add(a.tickets + blockIdx.x * a.Hkv + h, 1, __ATOMIC_RELAXED,
+    last = __hip_atomic_fetch_add(a.tickets + item * a.Hkv + h, 1, __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT) == a.KS - 1;
   __syncthreads();
   if (!last) return;
   if (tid == 0)
-    __hip_atomic_store(a.tickets + blockIdx.x * a.Hkv + h, 0, __ATOMIC_RELAXED,
+    __hip_atomic_store(a.tickets + item * a.Hkv + h, 0, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   // merge: thread -> (row of the block, 4 consecutive dims).  All KS LSEs and
   // partial outputs of a row are loaded at once (indices past KS repeat the
@@ -497,8 +505,8 @@ inline int log2_exact(int x) {
 template <int D, int RT, bool CASCADE = false>
 void launch_prefill(const PrefillArgs& a, int blocks, hipStream_t stream) {
   using P = PCfg<D, RT>;
-  hipLaunchKernelGGL((prefill_kernel<D, RT, CASCADE>), dim3(blocks, a.Hkv, a.KS), dim3(kThreads),
-                     2 * P::STAGE, stream, a);
+  hipLaunchKernelGGL((prefill_kernel<D, RT, CASCADE>), dim3(blocks * a.Hkv * a.KS),
+                     dim3(kThreads), 2 * P::STAGE, stream, a);
 }
 
 constexpr int kMaxTickets = 65536;
@@ -520,7 +528,18 @@ inline Plan plan(int num_seqs, int total_q, int num_q_heads, int kv_heads) {
   p.blocks = (int)(((int64_t)total_q * G + per - 1) / per) + num_seqs;
   const int64_t wgs = (int64_t)((rows + per - 1) / per) * 1;
   int ks = (int)((1024 + wgs - 1) / (wgs > 0 ? wgs : 1));
-  p.ks = ks < 1 ? 1 : (ks > kMaxSplits ? kMaxSplits : ks);
+  ks = ks < 1 ? 1 : (ks > kMaxSplits ? kMaxSplits : ks);
+  // round KS up so that the (KV head, split) pairs divide 8 or fill a multiple
+  // of 8 (the XCD-affine grid order of prefill_kernel), when that stays within
+  // kMaxSplits
+  for (int k = ks; k <= kMaxSplits; ++k) {
+    const int pairs = kv_heads * k;
+    if (8 % pairs == 0 || pairs % 8 == 0) {
+      ks = k;
+      break;
+    }
+  }
+  p.ks = ks;
   // the split partials are addressed with 32-bit offsets (at most ~128K rows
   // split at all, ~256 MB)
   if (p.ks > 1 && (int64_t)p.ks * rows * 128 * (int64_t)sizeof(float) >= ((int64_t)1 << 31))
@@ -553,6 +572,8 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   FE_CHECK_ARG(num_q_heads % kv_heads == 0);
   const int bs_log2 = log2_exact(block_size);
   if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
+  // pool rows (block * block_size + offset) are 32-bit in the kernel
+  if ((int64_t)num_blocks * block_size >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
   if (num_seqs == 0 || total_q == 0) return FE_OK;
   FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && q_offsets && context_lens);
   FE_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(k_pool) && aligned16(v_pool));
@@ -614,6 +635,7 @@ size_t cascade_prefix_scratch_bytes(int num_groups, int batch, int hq, int hkv, 
 int cascade_prefix_launch(const CascadePrefix& c, hipStream_t stream) {
   const Plan p = plan(c.num_groups, c.batch, c.hq, c.hkv);
   if ((int64_t)p.blocks * c.hkv > kMaxTickets) return FE_ERR_UNSUPPORTED;
+  if ((int64_t)c.num_blocks * c.bs >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
   PrefillArgs a;
   a.q = (const f16*)c.q;
   a.out = nullptr;
