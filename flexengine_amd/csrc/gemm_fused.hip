@@ -48,7 +48,7 @@ constexpr int kMaxSsPerLane = 64;  // RMSNorm prologue: up to 256 tile sums per 
 #define FE_WEIGHT_POLICY 0
 #endif
 
-enum Epi { kEpiF16 = 0, kEpiResid = 1, kEpiSilu = 2, kEpiRope = 3 };
+enum Epi { kEpiF16 = 0, kEpiResid = 1, kEpiSilu = 2, kEpiRope = 3, kEpiResidNorm = 4 };
 
 struct FusedArgs {
   const f16* W;        // [N][K]
@@ -73,9 +73,16 @@ struct FusedArgs {
   int tiles, ks_count, kslice_wg;
   f32x4* part;    // [tiles][ks_count][MT][64] lane-layout partial tiles
   int* tickets;   // [tiles], zero between calls
+  // RESID + RMSNorm (kEpiResidNorm): the tile that finishes last normalises
+  // every row of r into tail_out
+  const f16* tail_w;  // [N]
+  float tail_eps;
+  f16* tail_out;      // [M][N]
+  int* grid_ticket;   // zero between calls
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kSc1 = 16;  // buffer-instruction cache policy: sc1 (device-coherent)
 
 __device__ __forceinline__ float round16(float x) { return (float)(f16)x; }
@@ -112,6 +119,71 @@ struct Stage {
   f16x8 x[MT][4];
   f16x8 nw[NORM ? 4 : 1];  // norm weight of the step's keys (RMSNorm prologue)
 };
+
+// RMSNorm of the finished residual stream r = out [M][N], run by the waves of
+// the workgroup that completed the launch's last tile (wave w: rows
+// kTailRows * w .. and every waves * kTailRows after): inv = rsqrt(sum of the
+// row's tile sums of r^2 / N + eps), h = fp16(w * fp16(r * inv)), the rounding
+// of fe_rmsnorm and transformers' Qwen2RMSNorm.  r and the tile sums were
+// written by other workgroups with device-coherent stores before their
+// tickets, so they are read device-coherently here.  N <= 64 * 8 * kTailChunks
+// and N / 16 <= 64 * kTailSs (the host checks).
+constexpr int kTailChunks = 4;  // 16-byte chunks of a row per lane
+constexpr int kTailSs = 2;      // tile sums of a row per lane
+constexpr int kTailRows = 2;    // rows of a wave whose loads are in flight together
+
+__device__ __forceinline__ void norm_tail(const FusedArgs& a, int w, int waves, int lane) {
+  const int N = a.N, M = a.M;
+  const uint32_t r_bytes = (uint32_t)M * N * 2;
+  const __amdgpu_buffer_rsrc_t rr = rsrc(a.out, r_bytes);
+  const __amdgpu_buffer_rsrc_t rs = rsrc(a.out_ss, (uint32_t)a.tiles * M * 4);
+  f16x8 wv[kTailChunks];
+#pragma unroll
+  for (int c = 0; c < kTailChunks; ++c) {
+    const int e0 = (c * kWave + lane) * 8;
+    wv[c] = e0 < N ? ld16(a.tail_w + e0) : f16x8{};
+  }
+  for (int m0 = w * kTailRows; m0 < M; m0 += waves * kTailRows) {
+    f16x8 rv[kTailRows][kTailChunks];
+    float sp[kTailRows][kTailSs];
+#pragma unroll
+    for (int r = 0; r < kTailRows; ++r) {
+      const int m = m0 + r;  // rows past M read as zeros (offsets past the range)
+#pragma unroll
+      for (int c = 0; c < kTailChunks; ++c) {
+        const int e0 = (c * kWave + lane) * 8;
+        const uint32_t off = m < M && e0 < N ? (uint32_t)(m * N + e0) * 2 : r_bytes;
+        rv[r][c] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, kSc1));
+      }
+#pragma unroll
+      for (int j = 0; j < kTailSs; ++j) {
+        const int t = j * kWave + lane;
+        const uint32_t off = m < M && t < a.tiles ? (uint32_t)(t * M + m) * 4 : (uint32_t)a.tiles * M * 4;
+        sp[r][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, kSc1));
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kTailRows; ++r) {
+      const int m = m0 + r;
+      float ssum = 0.f;
+#pragma unroll
+      for (int j = 0; j < kTailSs; ++j) ssum += sp[r][j];
+#pragma unroll
+      for (int sh = 32; sh >= 1; sh >>= 1) ssum += __shfl_xor(ssum, sh, kWave);
+      const float inv = rsqrtf(ssum / (float)N + a.tail_eps);
+      if (m >= M) continue;
+#pragma unroll
+      for (int c = 0; c < kTailChunks; ++c) {
+        const int e0 = (c * kWave + lane) * 8;
+        if (e0 >= N) continue;
+        f16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (f16)((float)wv[c][e] * round16((float)rv[r][c][e] * inv));
+        st16(a.tail_out + (int64_t)m * N + e0, o);
+      }
+    }
+  }
+}
 
 template <int MT, int WAVES, int EPI, bool NORM>
 __global__ __launch_bounds__(WAVES * kWave) void gemm_fused_kernel(const FusedArgs a) {
@@ -224,6 +296,16 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_fused_kernel(const FusedAr
     k0 += kStepK;
   }
 
+  // KEEP: every wave stays to the end (the norm tail uses all of them); the
+  // workgroup's decisions then go through LDS so that all waves take them
+  constexpr bool KEEP = EPI == kEpiResidNorm;
+  __shared__ int wg_flag[2];
+  auto broadcast = [&](int v, int slot) __attribute__((always_inline)) {
+    if (w == 0 && lane == 0) wg_flag[slot] = v;
+    __syncthreads();
+    return wg_flag[slot];
+  };
+
   // the waves' K slices are added through LDS, in wave order
   if constexpr (WAVES > 1) {
     __shared__ f32x4 red[WAVES - 1][MT][kWave];
@@ -232,11 +314,13 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_fused_kernel(const FusedAr
       for (int mt = 0; mt < MT; ++mt) red[w - 1][mt][lane] = acc[mt];
     }
     __syncthreads();
-    if (w != 0) return;
+    if (!KEEP && w != 0) return;
+    if (w == 0) {
 #pragma unroll
-    for (int v = 0; v < WAVES - 1; ++v)
+      for (int v = 0; v < WAVES - 1; ++v)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[mt] += red[v][mt][lane];
+        for (int mt = 0; mt < MT; ++mt) acc[mt] += red[v][mt][lane];
+    }
   }
 
   // ---- split-K: the last workgroup of the tile to finish adds all partial
@@ -244,35 +328,43 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_fused_kernel(const FusedAr
   if (a.ks_count > 1) {
     const __amdgpu_buffer_rsrc_t rp = rsrc(a.part + (int64_t)tile * a.ks_count * MT * kWave,
                                            (uint32_t)a.ks_count * MT * kWave * 16);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mt]), rp,
-                                             (uint32_t)(((ks * MT + mt) * kWave + lane) * 16), 0,
-                                             kSc1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial complete device-wide
     int last = 0;
-    if (lane == 0)
-      last = __hip_atomic_fetch_add(a.tickets + tile, 1, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT) == a.ks_count - 1;
-    if (!__builtin_amdgcn_readfirstlane(last)) return;
-    if (lane == 0)
-      __hip_atomic_store(a.tickets + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < a.ks_count; ++s) {
+    if (w == 0) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        acc[mt] += __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rp, (uint32_t)(((s * MT + mt) * kWave + lane) * 16), 0, kSc1));
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mt]), rp,
+                                               (uint32_t)(((ks * MT + mt) * kWave + lane) * 16),
+                                               0, kSc1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial complete device-wide
+      if (lane == 0)
+        last = __hip_atomic_fetch_add(a.tickets + tile, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == a.ks_count - 1;
+      last = __builtin_amdgcn_readfirstlane(last);
+    }
+    if constexpr (KEEP) last = broadcast(last, 0);
+    if (!last) return;
+    if (w == 0) {
+      if (lane == 0)
+        __hip_atomic_store(a.tickets + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < a.ks_count; ++s) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[mt] += __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         rp, (uint32_t)(((s * MT + mt) * kWave + lane) * 16), 0, kSc1));
+      }
     }
   }
 
   // ---- epilogue (wave 0): lane (g, n) holds out[m = mt*16 + n][tile row 4g + i] ----
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
+    if (KEEP && w != 0) break;  // the other waves wait for the norm tail
     const int m = mt * 16 + n;
-    if constexpr (EPI == kEpiF16 || EPI == kEpiResid) {
+    if constexpr (EPI == kEpiF16 || EPI == kEpiResid || EPI == kEpiResidNorm) {
+      constexpr bool RES = EPI != kEpiF16;
       const int row0 = tile * 16 + 4 * g;
       float r[4];
       float ss = 0.f;
@@ -281,7 +373,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_fused_kernel(const FusedAr
         const int row = row0 + i;
         const bool ok = m < M && row < a.N;
         float v = acc[mt][i];
-        if (EPI == kEpiF16) {
+        if (!RES) {
           if (a.bias && row < a.N) v += (float)a.bias[row];
           r[i] = round16(v);
         } else {
@@ -289,12 +381,28 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_fused_kernel(const FusedAr
           r[i] = round16(round16(v) + res);
           ss += ok ? r[i] * r[i] : 0.f;
         }
-        if (ok) a.out[(int64_t)m * a.N + row] = (f16)r[i];
+        if (EPI != kEpiResidNorm && ok) a.out[(int64_t)m * a.N + row] = (f16)r[i];
       }
-      if (EPI == kEpiResid) {
+      if constexpr (EPI == kEpiResidNorm) {
+        // device-coherent: the workgroup that finishes last reads them (N % 16 == 0)
+        if (m < M) {
+          const f16x4 h4 = {(f16)r[0], (f16)r[1], (f16)r[2], (f16)r[3]};
+          __builtin_amdgcn_raw_buffer_store_b64(
+              __builtin_bit_cast(u32x2, h4), rsrc(a.out, (uint32_t)M * a.N * 2),
+              (uint32_t)(m * a.N + row0) * 2, 0, kSc1);
+        }
+      }
+      if constexpr (RES) {
         ss += shfl_xor_f(ss, 16);
         ss += shfl_xor_f(ss, 32);
-        if (g == 0 && m < M) a.out_ss[tile * M + m] = ss;
+        if (g == 0 && m < M) {
+          if constexpr (EPI == kEpiResidNorm)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ss),
+                                                  rsrc(a.out_ss, (uint32_t)a.tiles * M * 4),
+                                                  (uint32_t)(tile * M + m) * 4, 0, kSc1);
+          else
+            a.out_ss[tile * M + m] = ss;
+        }
       }
     } else if constexpr (EPI == kEpiSilu) {
       // lanes g = 0, 1 hold gate columns 8*tile + 4g + i, lanes g + 2 the up values
@@ -350,9 +458,28 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_fused_kernel(const FusedAr
       }
     }
   }
+
+  if constexpr (KEEP) {
+    // this tile's r and sums are complete device-wide; the workgroup of the
+    // last tile normalises all rows (every wave a share) and leaves the
+    // ticket at zero
+    int last = 0;
+    if (w == 0) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (lane == 0)
+        last = __hip_atomic_fetch_add(a.grid_ticket, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == a.tiles - 1;
+      last = __builtin_amdgcn_readfirstlane(last);
+      if (last && lane == 0)
+        __hip_atomic_store(a.grid_ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!broadcast(last, 1)) return;
+    norm_tail(a, w, WAVES, lane);
+  }
 }
 
-constexpr size_t kFusedTicketBytes = 64 * 1024;  // tickets for up to 16384 tiles
+constexpr size_t kFusedTicketBytes = 64 * 1024;  // tickets for up to 16383 tiles
+constexpr int kGridTicket = kFusedTicketBytes / sizeof(int) - 1;  // the launch-wide ticket
 
 // Workgroups per tile when the tiles alone leave the chip short of ~512
 // workgroups (split-K across workgroups, at least 512 keys each), or 1.
@@ -390,13 +517,14 @@ int launch_fused(FusedArgs a, int tiles, void* workspace, size_t workspace_bytes
                  hipStream_t stream) {
   a.tiles = tiles;
   a.ks_count = ks_for(tiles, a.K);
-  if (a.ks_count > 1) {
+  if (a.ks_count > 1 || EPI == kEpiResidNorm) {
     const size_t need = fe_gemm_fused_workspace_size(a.M, a.N, a.K);
     if (workspace == nullptr || workspace_bytes < need ||
         (reinterpret_cast<uintptr_t>(workspace) & 255))
       return FE_ERR_WORKSPACE;
     a.tickets = (int*)workspace;
     a.part = (f32x4*)((char*)workspace + kFusedTicketBytes);
+    a.grid_ticket = a.tickets + kGridTicket;
   }
   int kslice_wg = (a.K + a.ks_count - 1) / a.ks_count;
   a.kslice_wg = (kslice_wg + 31) / 32 * 32;
@@ -472,6 +600,32 @@ extern "C" int fe_gemm_resid(const void* x, int M, int K, const void* W, int N,
   a.out_ss = out_ss;
   return launch_fused<kEpiResid, false>(a, (N + 15) / 16, workspace, workspace_bytes,
                                         (hipStream_t)stream);
+}
+
+extern "C" int fe_gemm_resid_rmsnorm(const void* x, int M, int K, const void* W, int N,
+                                     const void* residual, void* out, float* out_ss,
+                                     const void* norm_w, float eps, void* norm_out,
+                                     void* workspace, size_t workspace_bytes,
+                                     fe_stream_t stream) {
+  FusedArgs a;
+  const int rc = fill_common(a, x, nullptr, 0, nullptr, 0.f, M, K, W, N);
+  if (rc != FE_OK || M == 0) return rc;
+  FE_CHECK_ARG(residual && out && out_ss && norm_w && norm_out);
+  // out, out_ss and norm_out alias nothing the call reads, nor each other
+  FE_CHECK_ARG(out != residual && out != x && norm_out != out && norm_out != residual &&
+               norm_out != x);
+  if (N % 16 != 0 || N > kWave * 8 * kTailChunks || N / 16 > kWave * kTailSs)
+    return FE_ERR_UNSUPPORTED;
+  const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  FE_CHECK_ARG(al16(out) && al16(norm_w) && al16(norm_out));
+  a.residual = (const f16*)residual;
+  a.out = (f16*)out;
+  a.out_ss = out_ss;
+  a.tail_w = (const f16*)norm_w;
+  a.tail_eps = eps;
+  a.tail_out = (f16*)norm_out;
+  return launch_fused<kEpiResidNorm, false>(a, N / 16, workspace, workspace_bytes,
+                                            (hipStream_t)stream);
 }
 
 extern "C" int fe_gemm_silu(const void* x, const float* x_ss, int ss_tiles, const void* norm_w,

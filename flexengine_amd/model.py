@@ -211,26 +211,35 @@ class Qwen2Model:
         return logits * active.to(logits.dtype)[:, None]
 
     def _decode_layers_fused(self, x, h, positions, tables, ctx, cache) -> torch.Tensor:
-        """The decode layers at decode batch sizes on the fused projections: seven
+        """The decode layers at decode batch sizes on the fused projections: five
         launches per layer -- q/k/v + bias + RoPE, the paged decode with the page
-        write, o + residual, RMSNorm, gate/up + SiLU, down + residual, RMSNorm --
-        where the unfused chain needs nine.  The residual stream alternates between
-        fresh tensors (r1 after attention, r2 after the MLP).  The norms run as their
-        own one-workgroup kernel on the fp16 residual: at these sizes that measured
-        faster than normalising the operand inside the next projection, where every
-        lane transforms its 16 MFMA columns."""
+        write, o + residual + RMSNorm, gate/up + SiLU, down + residual + the next
+        RMSNorm -- where the unfused chain needs nine.  The residual stream alternates
+        between fresh tensors (r1 after attention, r2 after the MLP).  Each norm runs
+        in the residual projection that produces its input (the workgroup finishing
+        the last tile normalises the rows); normalising the operand inside the next
+        projection instead measured slower, every lane transforming its 16 MFMA
+        columns.  Hidden sizes the fused norm does not take use a separate
+        fe_rmsnorm launch."""
         eps = self.cfg.rms_norm_eps
         res = x
         rows = x.shape[0]
+        fused_norm = ops.resid_rmsnorm_supported(self.cfg.hidden_size)
         for layer, lw in enumerate(self.layer_weights):
             q, k, v = ops.gemm_rope(h, lw.w_qkv, lw.b_qkv, positions, self.inv_freq,
                                     self.nq, self.nkv, self.dim)
             attn = ops.paged_decode(q, cache.k[layer], cache.v[layer], tables, ctx, scale=self.scale,
                                     k_new=k, v_new=v)
-            r1, _ = ops.gemm_resid(attn.reshape(rows, self.nq * self.dim), lw.w_o, res)
-            h2, _ = ops.rmsnorm(r1, lw.post_norm, eps)
-            act = ops.gemm_silu(h2, lw.w_gate_up)
-            r2, _ = ops.gemm_resid(act, lw.w_down, r1)
-            h, _ = ops.rmsnorm(r2, self._next_norm(layer), eps)
+            o_in = attn.reshape(rows, self.nq * self.dim)
+            if fused_norm:
+                r1, h2 = ops.gemm_resid_rmsnorm(o_in, lw.w_o, res, lw.post_norm, eps)
+                act = ops.gemm_silu(h2, lw.w_gate_up)
+                r2, h = ops.gemm_resid_rmsnorm(act, lw.w_down, r1, self._next_norm(layer), eps)
+            else:
+                r1, _ = ops.gemm_resid(o_in, lw.w_o, res)
+                h2, _ = ops.rmsnorm(r1, lw.post_norm, eps)
+                act = ops.gemm_silu(h2, lw.w_gate_up)
+                r2, _ = ops.gemm_resid(act, lw.w_down, r1)
+                h, _ = ops.rmsnorm(r2, self._next_norm(layer), eps)
             res = r2
         return ops.gemm_f16(h, self.lm_head)

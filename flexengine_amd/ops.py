@@ -464,6 +464,32 @@ def gemm_resid(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
     return out, ss
 
 
+def gemm_resid_rmsnorm(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
+                       norm_weight: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(r, h): r = fp16(fp16(x @ weight^T) + residual) [M, N] and h = RMSNorm(r) with
+    norm_weight, in one launch (fe_gemm_resid_rmsnorm; N % 16 == 0, N <= 2048)."""
+    r_in, _, _, _, _ = _operand(x, weight)
+    dev = _require_gpu(r_in, weight, residual, norm_weight)
+    m, n = r_in.shape[0], weight.shape[0]
+    if residual.shape != (m, n) or residual.dtype != FP16 or not residual.is_contiguous():
+        raise ValueError("residual must be contiguous float16 [M, N]")
+    if norm_weight.shape != (n,) or norm_weight.dtype != FP16 or not norm_weight.is_contiguous():
+        raise ValueError("norm_weight must be contiguous float16 [N]")
+    out = torch.empty((m, n), dtype=FP16, device=dev)
+    h = torch.empty((m, n), dtype=FP16, device=dev)
+    ss = torch.empty(((n + 15) // 16, m), dtype=torch.float32, device=dev)
+    ws = _fused_ws(dev, m, n, r_in.shape[1])
+    _lib.call("fe_gemm_resid_rmsnorm", r_in.data_ptr(), m, r_in.shape[1], weight.data_ptr(), n,
+              residual.data_ptr(), out.data_ptr(), ss.data_ptr(), norm_weight.data_ptr(),
+              float(eps), h.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+    return out, h
+
+
+def resid_rmsnorm_supported(n: int) -> bool:
+    """Whether fe_gemm_resid_rmsnorm takes an output width of n."""
+    return n % 16 == 0 and n <= 2048
+
+
 def gemm_silu(x, weight: torch.Tensor) -> torch.Tensor:
     """fp16(silu(g) * u) [M, I] of the products with weight = [gate; up] [2I, K]."""
     r, ss, tiles, nw, eps = _operand(x, weight)

@@ -116,6 +116,20 @@ int fe_gemm_resid(const void* x, int M, int K, const void* W, int N, const void*
                   void* out, float* out_ss, void* workspace, size_t workspace_bytes,
                   fe_stream_t stream);
 
+/* fe_gemm_resid followed by the RMSNorm of its result, in one launch: writes
+ * r to out [M, N] and out_ss as fe_gemm_resid does, and norm_out [M, N] =
+ * fp16(norm_w * fp16(r * rsqrt(mean(r^2) + eps))) (transformers'
+ * Qwen2RMSNorm, as fe_rmsnorm computes it; the mean from the tile sums).  The
+ * workgroup that finishes the last output tile normalises every row, so the
+ * residual add and the post-attention / next input norm of qwen2.py:129-134
+ * cost one launch.  N a multiple of 16, at most 2048; out, norm_w and
+ * norm_out 16-byte aligned; workspace as for the other fused projections
+ * (always required: it holds the launch-wide ticket). */
+int fe_gemm_resid_rmsnorm(const void* x, int M, int K, const void* W, int N,
+                          const void* residual, void* out, float* out_ss, const void* norm_w,
+                          float eps, void* norm_out, void* workspace, size_t workspace_bytes,
+                          fe_stream_t stream);
+
 /* W = [gate; up] ([2I, K]); out [M, I] = fp16(fp16(silu(g)) * u) with
  * g, u = fp16 of the gate / up products: the gate/up projection and act_fn
  * product of HF Qwen2MLP (qwen2.py:130,184). */

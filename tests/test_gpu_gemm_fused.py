@@ -142,3 +142,50 @@ def test_fused_gemms_reject_unsupported_shapes():
         ops.gemm_f16(randn(2, 40), randn(16, 40))
     with pytest.raises(ValueError):
         ops.gemm_resid(randn(2, 64), randn(16, 64), randn(3, 16))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1536, 1536), (8, 1536, 8960), (17, 896, 4864),
+                                   (32, 2048, 512), (3, 16, 64)])
+def test_resid_rmsnorm_equals_resid_then_rmsnorm(m, n, k):
+    """One launch == fe_gemm_resid then fe_rmsnorm: r bit-identical, the norm within
+    two fp16 ulps (the mean of r^2 is summed from the tile sums, in another order than
+    the one-wave norm, and a one-ulp change of fp16(r * inv) can move the product with
+    the weight by two) and almost all of it bit-identical; twice in a row (the
+    launch-wide ticket resets itself)."""
+    x, w, res = randn(m, k, seed=21), randn(n, k, seed=22, scale=0.05), randn(m, n, seed=23)
+    nw = randn(n, seed=24)
+    r_ref, _ = ops.gemm_resid(x, w, res)
+    h_ref, _ = ops.rmsnorm(r_ref, nw, 1e-6)
+    for _ in range(2):
+        r, h = ops.gemm_resid_rmsnorm(x, w, res, nw, 1e-6)
+        assert torch.equal(r, r_ref)
+        err = (h.float() - h_ref.float()).abs()
+        assert (err <= 2 ** -9 * h_ref.float().abs() + 1e-7).all(), err.max().item()
+        assert (h == h_ref).float().mean() > 0.99
+    # and against the float64 emulation of the reference's rounding
+    want, _ = torch_rmsnorm(r_ref, nw, 1e-6)
+    assert ((h.float() - want.float()).abs() <= 2 ** -9 * want.float().abs() + 1e-7).all()
+
+
+def test_resid_rmsnorm_alternating_shapes_share_the_workspace():
+    a = (randn(4, 8960, seed=25), randn(1536, 8960, seed=26, scale=0.02), randn(4, 1536, seed=27),
+         randn(1536, seed=28))
+    b = (randn(1, 512, seed=29), randn(896, 512, seed=30, scale=0.05), randn(1, 896, seed=31),
+         randn(896, seed=32))
+    first = {}
+    for rep in range(3):
+        for name, (x, w, res, nw) in (("a", a), ("b", b)):
+            r, h = ops.gemm_resid_rmsnorm(x, w, res, nw, 1e-6)
+            h_ref, _ = ops.rmsnorm(r, nw, 1e-6)
+            assert (h == h_ref).float().mean() > 0.99
+            if name in first:
+                assert torch.equal(first[name], h)
+            else:
+                first[name] = h
+
+
+def test_resid_rmsnorm_rejects_unsupported_widths():
+    from flexengine_amd._lib import FlexEngineAMDError
+    for n in (24, 2064):
+        with pytest.raises(FlexEngineAMDError):
+            ops.gemm_resid_rmsnorm(randn(2, 64), randn(n, 64), randn(2, n), randn(n), 1e-6)
