@@ -335,23 +335,27 @@ void prefill_kernel(const PrefillArgs a) {
 
     // online softmax per row tile; P^T of the 32 keys as one f16x8 B operand
     f16x8 pb[RT];
-    const bool need_mask = kb >= unmasked_blocks;
+    // scores stay unscaled up to the exponent: the row max is taken on them and
+    // scaled once (scale > 0 keeps the order), and exp2(s * scale - m) is one
+    // fma per score; the causal mask only runs on blocks that need it
+    const bool need_mask = kb >= unmasked_blocks;  // wave-uniform
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       float sv[2][4];
-      float mx = kNegInf;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kb * kBlockKeys + 16 * kt + 4 * g + i;
-          float v = st[rt][kt][i] * a.scale_log2;
-          if (need_mask && key > pos[rt]) v = kNegInf;
-          sv[kt][i] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = fmaxf(mx, shfl_xor_f(mx, 16));
-      mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        for (int i = 0; i < 4; ++i) sv[kt][i] = st[rt][kt][i];
+      if (need_mask) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (kb * kBlockKeys + 16 * kt + 4 * g + i > pos[rt]) sv[kt][i] = kNegInf;
+      }
+      float mx = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
+                       fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
+      mx = max_across_rows(mx) * a.scale_log2;
       if (__ballot(mx > m_run[rt] + kRescaleSlack)) {  // wave-uniform
         const float m_new = fmaxf(m_run[rt], mx);
         const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run[rt] - m_new);
@@ -360,14 +364,14 @@ void prefill_kernel(const PrefillArgs a) {
         for (int x = 0; x < P::NX; ++x) o[rt][x] *= alpha;
         m_run[rt] = m_new;
       }
-      const float m_use = m_run[rt] == kNegInf ? 0.f : m_run[rt];
+      const float neg_m = m_run[rt] == kNegInf ? 0.f : -m_run[rt];
       float lsum = 0.f;
       f16x8 p;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float e = exp2_fast(sv[kt][i] - m_use);
+          const float e = exp2_fast(__builtin_fmaf(sv[kt][i], a.scale_log2, neg_m));
           lsum += e;
           p[4 * kt + i] = (f16)e;
         }
@@ -574,6 +578,7 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
   // pool rows (block * block_size + offset) are 32-bit in the kernel
   if ((int64_t)num_blocks * block_size >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
+  FE_CHECK_ARG(scale > 0.f);  // the kernel takes the row max on unscaled scores
   if (num_seqs == 0 || total_q == 0) return FE_OK;
   FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && q_offsets && context_lens);
   FE_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(k_pool) && aligned16(v_pool));
@@ -636,6 +641,7 @@ int cascade_prefix_launch(const CascadePrefix& c, hipStream_t stream) {
   const Plan p = plan(c.num_groups, c.batch, c.hq, c.hkv);
   if ((int64_t)p.blocks * c.hkv > kMaxTickets) return FE_ERR_UNSUPPORTED;
   if ((int64_t)c.num_blocks * c.bs >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
+  if (!(c.scale > 0.f)) return FE_ERR_INVALID_ARGUMENT;  // row max on unscaled scores
   PrefillArgs a;
   a.q = (const f16*)c.q;
   a.out = nullptr;
