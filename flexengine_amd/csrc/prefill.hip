@@ -44,7 +44,11 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kBlockKeys = 32;  // one 16x16x32 PV step per block
+// Keys staged per block (a multiple of 32).  64 measured slower: its LDS stages
+// leave two workgroups per CU instead of four (C4: ~70 vs ~59 us).
+constexpr int kBlockKeys = 32;
+constexpr int kKT = kBlockKeys / 16;    // 16-key S tiles per block
+constexpr int kPS = kBlockKeys / 32;    // 32-key PV steps per block
 constexpr int kMaxSplits = 8;   // key splits per row block (plan() clamps to it)
 // Two 16-row tiles per wave (RT = 2) once the rows fill this many 128-row blocks;
 // below it the extra blocks of RT = 1 fill the CUs better (measured: 1377 new tokens
@@ -318,10 +322,10 @@ void prefill_kernel(const PrefillArgs a) {
     const unsigned char* kbase = smem + ((kb - kb_lo) & 1) * P::STAGE;
     const unsigned char* vbase = kbase + P::KBYTES;
 
-    // S^T tiles: 2 key tiles x RT row tiles
-    f32x4 st[RT][2];
+    // S^T tiles: kKT key tiles x RT row tiles
+    f32x4 st[RT][kKT];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < kKT; ++kt) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) st[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -333,28 +337,30 @@ void prefill_kernel(const PrefillArgs a) {
       }
     }
 
-    // online softmax per row tile; P^T of the 32 keys as one f16x8 B operand
-    f16x8 pb[RT];
+    // online softmax per row tile; P^T of each 32 keys as one f16x8 B operand
+    f16x8 pb[RT][kPS];
     // scores stay unscaled up to the exponent: the row max is taken on them and
     // scaled once (scale > 0 keeps the order), and exp2(s * scale - m) is one
     // fma per score; the causal mask only runs on blocks that need it
     const bool need_mask = kb >= unmasked_blocks;  // wave-uniform
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      float sv[2][4];
+      float sv[kKT][4];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < kKT; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[kt][i] = st[rt][kt][i];
       if (need_mask) {
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < kKT; ++kt)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             if (kb * kBlockKeys + 16 * kt + 4 * g + i > pos[rt]) sv[kt][i] = kNegInf;
       }
-      float mx = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
-                       fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
+      float mx = kNegInf;
+#pragma unroll
+      for (int kt = 0; kt < kKT; ++kt)
+        mx = fmaxf(mx, fmaxf(fmaxf(sv[kt][0], sv[kt][1]), fmaxf(sv[kt][2], sv[kt][3])));
       mx = max_across_rows(mx) * a.scale_log2;
       if (__ballot(mx > m_run[rt] + kRescaleSlack)) {  // wave-uniform
         const float m_new = fmaxf(m_run[rt], mx);
@@ -366,31 +372,37 @@ void prefill_kernel(const PrefillArgs a) {
       }
       const float neg_m = m_run[rt] == kNegInf ? 0.f : -m_run[rt];
       float lsum = 0.f;
-      f16x8 p;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int ps = 0; ps < kPS; ++ps) {
+        f16x8 p;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = exp2_fast(__builtin_fmaf(sv[kt][i], a.scale_log2, neg_m));
-          lsum += e;
-          p[4 * kt + i] = (f16)e;
-        }
-      pb[rt] = p;
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float e = exp2_fast(__builtin_fmaf(sv[2 * ps + kt][i], a.scale_log2, neg_m));
+            lsum += e;
+            p[4 * kt + i] = (f16)e;
+          }
+        pb[rt][ps] = p;
+      }
       l_run[rt] += lsum;
     }
 
-    // O^T += V^T . P^T: one 32-key step per 16-dim tile
-    const unsigned char* vb = vbase + (4 * g + (n >> 2)) * P::VP + (n & 3) * 8;
+    // O^T += V^T . P^T: one 32-key step per 16-dim tile and PV step
 #pragma unroll
-    for (int x = 0; x < P::NX; ++x) {
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(vb + 32 * x));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(vb + 16 * P::VP + 32 * x));
-      const f16x4 l4 = __builtin_bit_cast(f16x4, lo), h4 = __builtin_bit_cast(f16x4, hi);
-      const f16x8 va = {l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+    for (int ps = 0; ps < kPS; ++ps) {
+      const unsigned char* vb = vbase + (32 * ps + 4 * g + (n >> 2)) * P::VP + (n & 3) * 8;
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) o[rt][x] = mfma32(va, pb[rt], o[rt][x]);
+      for (int x = 0; x < P::NX; ++x) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(vb + 32 * x));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(vb + 16 * P::VP + 32 * x));
+        const f16x4 l4 = __builtin_bit_cast(f16x4, lo), h4 = __builtin_bit_cast(f16x4, hi);
+        const f16x8 va = {l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) o[rt][x] = mfma32(va, pb[rt][ps], o[rt][x]);
+      }
     }
 
     if (more) store_block((kb + 1 - kb_lo) & 1);
