@@ -26,19 +26,6 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }
 
-// Maximum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the same position in the
-// wave's four 16-lane rows), with gfx950's row-swap instructions: each swap
-// leaves the two members of a row pair in the two results, so the max of
-// those is the pair's max in every lane.  VALU only (no LDS round trip).
-__device__ __forceinline__ float max_across_rows(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x),
-                                                  __builtin_bit_cast(unsigned, x), false, false);
-  x = fmaxf(__builtin_bit_cast(float, a[0]), __builtin_bit_cast(float, a[1]));
-  const auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
-                                                  __builtin_bit_cast(unsigned, x), false, false);
-  return fmaxf(__builtin_bit_cast(float, b[0]), __builtin_bit_cast(float, b[1]));
-}
-
 __device__ __forceinline__ int readlane_i(int v, int lane) {
   return __builtin_amdgcn_readlane(v, lane);
 }

@@ -361,7 +361,9 @@ void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
       for (int kt = 0; kt < kKT; ++kt)
         mx = fmaxf(mx, fmaxf(fmaxf(sv[kt][0], sv[kt][1]), fmaxf(sv[kt][2], sv[kt][3])));
-      mx = max_across_rows(mx) * a.scale_log2;
+      mx = fmaxf(mx, shfl_xor_f(mx, 16));
+      mx = fmaxf(mx, shfl_xor_f(mx, 32));
+      mx *= a.scale_log2;
       if (__ballot(mx > m_run[rt] + kRescaleSlack)) {  // wave-uniform
         const float m_new = fmaxf(m_run[rt], mx);
         const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run[rt] - m_new);

@@ -308,6 +308,18 @@ def test_split_merge_repeated_calls_are_stable():
             first[target] = got
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(12, 2, 128), (6, 1, 128), (14, 2, 64)])
+def test_decode_large_scores(hq, hkv, d):
+    """q scaled by 16: scores spread over hundreds, so every running max (per tile,
+    per wave, per piece, across the split merge) must be exact or exp2 overflows."""
+    w = workloads.make_decode_workload("large", 9 + hq, 6, hq, hkv, d, [700, 5, 2000, 33, 4096, 129])
+    w.q = (w.q.float() * 16).half()
+    got, _ = run_decode(w, fuse=False)
+    assert np.isfinite(got.numpy()).all()
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what=f"large scores {hq}/{hkv}/{d}")
+
+
 # --------------------------------------------------------------------------------------
 # shared-prefix (cascade) decode: same results as the plain decode on the same tables
 # --------------------------------------------------------------------------------------

@@ -64,6 +64,20 @@ def test_prefill_shapes(hq, hkv, d, bs):
     assert_attention_close(got, exp)
 
 
+@pytest.mark.parametrize("hq,hkv,d,q_scale", [(6, 1, 128, 16.0), (12, 2, 128, 8.0), (14, 2, 64, 16.0)])
+def test_prefill_large_scores(hq, hkv, d, q_scale):
+    """q scaled up so scores spread over hundreds: the running max must be the true
+    max over every key of a block (all four 16-lane rows of the score tile); a max
+    taken over part of them lets exp2 and the fp16 probabilities overflow."""
+    q, offs, ctx, tables, kp, vp = _case(77 + hq, [40, 130, 1], [300, 20, 64], hq, hkv, d)
+    q = (q.float() * q_scale).half()
+    got = _run(q, offs, ctx, tables, kp, vp)
+    assert np.isfinite(got).all()
+    exp = R.prefill_reference(q.numpy(), offs.numpy(), ctx.numpy(), kp.numpy(), vp.numpy(),
+                              tables.numpy(), 16)
+    assert_attention_close(got, exp, what=f"large scores x{q_scale}")
+
+
 def test_c4_prefill_chunks_full():
     w = workloads.c4_workload()
     got = _run(w.q, w.q_offsets, w.context_lens, w.block_tables, w.k_pool, w.v_pool)
