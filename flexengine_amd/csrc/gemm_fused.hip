@@ -16,7 +16,7 @@
 //
 // Work: one workgroup per 16-row tile of the output; its waves cut K into
 // contiguous slices and add their products through LDS.  When the tiles alone
-// leave the chip short of ~512 workgroups (q/k/v, o: 128 tiles), ks_for()
+// leave the chip short of ~192 workgroups (q/k/v 128 tiles, o and down 96), ks_for()
 // gives each tile several workgroups over disjoint K ranges: each writes its
 // fp32 partial tile with device-coherent stores and takes a per-tile ticket,
 // and the last one adds the partials in split order and runs the epilogue, so
@@ -481,10 +481,15 @@ __global__ __launch_bounds__(WAVES * kWave) void gemm_fused_kernel(const FusedAr
 constexpr size_t kFusedTicketBytes = 64 * 1024;  // tickets for up to 16383 tiles
 constexpr int kGridTicket = kFusedTicketBytes / sizeof(int) - 1;  // the launch-wide ticket
 
-// Workgroups per tile when the tiles alone leave the chip short of ~512
-// workgroups (split-K across workgroups, at least 512 keys each), or 1.
+// Workgroups per tile when the tiles alone leave the chip short of ~192
+// workgroups (split-K across workgroups, at least 512 keys each), or 1.  Every
+// split adds a partial-tile round trip and a ticket before the epilogue; on
+// the Qwen2.5-1.5B decode step (q/k/v 128 tiles, o and down 96) a target of
+// 192 workgroups measured best: 512 -> 192 raised B = 1 from ~510 to ~544
+// tok/s, and no split at all (one workgroup per tile) fell to ~489.
+constexpr int kSplitTargetWgs = 192;
 int ks_for(int tiles, int K) {
-  int ks = (512 + tiles - 1) / tiles;
+  int ks = (kSplitTargetWgs + tiles - 1) / tiles;
   const int max_ks = K / 512 > 0 ? K / 512 : 1;
   ks = ks < max_ks ? ks : max_ks;
   return ks > 1 ? ks : 1;
