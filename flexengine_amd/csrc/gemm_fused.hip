@@ -510,9 +510,13 @@ extern "C" size_t fe_gemm_fused_workspace_size(int M, int N, int K) {
 namespace {
 
 // Waves per workgroup: enough to put ~2048 waves in flight when there are few
-// tiles, and at least 32 keys per wave.
+// tiles, and at least 32 keys per wave.  With many tiles (gate/up: 1120, the
+// LM head: 9496) one wave per workgroup streaming all of K measured fastest
+// (B = 1: 4 waves 544, 2 waves 554, 1 wave 568 tok/s): a wave's pipeline ramp
+// and drain are paid once per longer stream, and no LDS reduction is needed.
+constexpr int kManyTilesWaves = 1;
 int waves_for(int tiles, int K) {
-  int waves = tiles <= 160 ? 16 : (tiles <= 512 ? 8 : 4);
+  int waves = tiles <= 160 ? 16 : (tiles <= 512 ? 8 : kManyTilesWaves);
   while (waves > 1 && (int64_t)(waves - 1) * 32 >= K) waves /= 2;
   return waves;
 }
@@ -533,6 +537,7 @@ int launch_fused(FusedArgs a, int tiles, void* workspace, size_t workspace_bytes
   }
   int kslice_wg = (a.K + a.ks_count - 1) / a.ks_count;
   a.kslice_wg = (kslice_wg + 31) / 32 * 32;
+  // split workgroups: 4 waves (1, 2, 8 and 16 measured slower)
   int waves = a.ks_count > 1 ? 4 : waves_for(tiles, a.K);
   if (a.M > 16 && waves > 8) waves = 8;  // two row tiles: the register budget of 8 waves
   int kslice = (a.kslice_wg + waves - 1) / waves;
@@ -544,6 +549,8 @@ int launch_fused(FusedArgs a, int tiles, void* workspace, size_t workspace_bytes
   if (a.M <= 16) {
     if (waves == 16) FE_FUSED(1, 16);
     else if (waves == 8) FE_FUSED(1, 8);
+    else if (waves == 2) FE_FUSED(1, 2);
+    else if (waves == 1) FE_FUSED(1, 1);
     else FE_FUSED(1, 4);
   } else {
     if (waves == 8) FE_FUSED(2, 8);
