@@ -31,6 +31,8 @@ SIGNATURES: dict[str, tuple] = {
     "fe_version": (_i, []),
     "fe_error_string": (ctypes.c_char_p, [_i]),
     "fe_write_kv": (_i, [_p, _p, _i64, _p, _p, _i, _p, _p, _i, _i, _i, _i, _p]),
+    "fe_write_kv_ragged": (_i, [_p, _p, _i64, _p, _p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _i, _p]),
+    "fe_gather_tables": (_i, [_p, _i, _p, _i, _p, _i, _i, _i, _p, _i, _p]),
     "fe_write_kv_decode": (_i, [_p, _p, _i64, _p, _p, _i, _p, _i, _p, _i, _i, _i, _i, _p]),
     "fe_gather_kv": (_i, [_p, _p, _i, _p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p]),
     "fe_paged_decode_workspace_size": (_sz, [_i, _i, _i, _i, _i]),

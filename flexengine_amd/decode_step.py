@@ -32,25 +32,25 @@ class GraphDecodeStep:
         self.scratch_blocks = list(cache.tables[SCRATCH_ID])
 
     def graph_inputs(self, chunks, batch_size: int) -> dict[str, torch.Tensor]:
-        """Padded staging rows (runtime.py:201-213): row r of a padded slot points at
-        scratch block r; active rows carry their token, position and table."""
+        """Padded staging rows (runtime.py:201-213): active rows carry their token,
+        position and block table, padded rows and table tails a scratch block.  The
+        tables are gathered on the device from the cache's mirror rows
+        (fe_gather_tables): a step copies one row index per request, not its table.
+        (Rows without a request are never written here -- their context length is 0 --
+        so they need no scratch slot of their own, unlike the reference's.)"""
         if len(chunks) > batch_size:
             raise ValueError("more chunks than batch rows")
-        tables = torch.empty((batch_size, self.max_blocks), dtype=torch.long)
-        for row in range(batch_size):
-            tables[row].fill_(self.scratch_blocks[row % len(self.scratch_blocks)])
         ids = torch.zeros(batch_size, dtype=torch.long)
         positions = torch.zeros(batch_size, dtype=torch.long)
         for row, chunk in enumerate(chunks):
-            table = self.cache.tables[chunk.request_id]
-            if len(table) > self.max_blocks:
+            if len(self.cache.tables[chunk.request_id]) > self.max_blocks:
                 raise ValueError("request longer than max_model_len")
             ids[row] = chunk.input_ids[0]
             positions[row] = chunk.start
-            tables[row, :len(table)] = torch.tensor(table, dtype=torch.long)
+        requests = [c.request_id for c in chunks] + [None] * (batch_size - len(chunks))
+        tables = self.cache.device_tables(requests, self.max_blocks, pad_block=self.scratch_blocks[0])
         dev = self.cache.device
-        return {"input_ids": ids.to(dev), "positions": positions.to(dev),
-                "block_tables": tables.to(dev)}
+        return {"input_ids": ids.to(dev), "positions": positions.to(dev), "block_tables": tables}
 
     def _decode(self, input_ids, positions, block_tables, active_mask):
         return self.model.decode_static(input_ids, positions, block_tables, active_mask, self.cache)

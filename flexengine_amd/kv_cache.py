@@ -52,6 +52,13 @@ class PagedKVCache:
         self.tables: dict[str, list[int]] = {}
         self.refs = [0] * layout.num_blocks
         self.retained_refs = [0] * layout.num_blocks
+        # device mirror of `tables` (GPU caches): one int32 row per request,
+        # written when the request's blocks change, so a step's tables are
+        # gathered on the device (device_tables) instead of filled on the host
+        self._mirror: torch.Tensor | None = None
+        self._mirror_len: torch.Tensor | None = None
+        self._rows: dict[str, int] = {}
+        self._free_rows: list[int] = []
 
     # ---- bookkeeping (allocator.py:38-106) ------------------------------------------
 
@@ -80,12 +87,15 @@ class PagedKVCache:
         needed = self.missing_blocks(request_id, target_tokens)
         if needed > len(self.free):
             raise CacheExhausted(f"Need {needed} blocks; only {len(self.free)} free")
+        fresh = request_id not in self.tables
         table = self.tables.setdefault(request_id, [])
         for _ in range(needed):
             block = self.free.popleft()
             assert self.refs[block] == 0
             self.refs[block] = 1
             table.append(block)
+        if needed or fresh:
+            self.sync_device_table(request_id)
 
     def retain_block(self, block: int) -> None:
         """Adds a non-request owner (e.g. a prefix-cache index)."""
@@ -112,6 +122,7 @@ class PagedKVCache:
         for block in block_ids:
             self.refs[block] += 1
         self.tables[request_id] = block_ids
+        self.sync_device_table(request_id)
 
     def _release_ref(self, block: int) -> None:
         if self.refs[block] <= 0:
@@ -123,6 +134,10 @@ class PagedKVCache:
     def free_request(self, request_id: str) -> None:
         for block in self.tables.pop(request_id, []):
             self._release_ref(block)
+        row = self._rows.pop(request_id, None)
+        if row is not None:
+            self._mirror_len[row:row + 1].fill_(0)
+            self._free_rows.append(row)
 
     # ---- slot mapping and device tables --------------------------------------------
 
@@ -150,6 +165,60 @@ class PagedKVCache:
             fill = pad_block if pad_block is not None else (row[-1] if row else 0)
             out[i, len(row):] = fill
         return out.to(self.device, non_blocking=True)
+
+    def sync_device_table(self, request_id: str) -> None:
+        """Writes the request's table into its row of the device mirror (called by
+        reserve / attach_prefix; call it after editing `tables` directly).  A no-op for
+        a cache that does not live on a GPU."""
+        if self.device.type != "cuda":
+            return
+        table = self.tables[request_id]
+        row = self._rows.get(request_id)
+        if row is None:
+            row = self._free_rows.pop() if self._free_rows else len(self._rows)
+            self._rows[request_id] = row
+        self._grow_mirror(row + 1, len(table))
+        if table:
+            self._mirror[row, :len(table)] = torch.tensor(table, dtype=torch.int32).to(
+                self.device, non_blocking=True)
+        self._mirror_len[row:row + 1].fill_(len(table))
+
+    def _grow_mirror(self, rows: int, width: int) -> None:
+        cur_rows, cur_width = (0, 0) if self._mirror is None else tuple(self._mirror.shape)
+        if rows <= cur_rows and width <= cur_width:
+            return
+        new_rows = max(rows, 2 * cur_rows, 16)
+        new_width = max(width, 2 * cur_width, 64)
+        mirror = torch.zeros((new_rows, new_width), dtype=torch.int32, device=self.device)
+        lens = torch.zeros((new_rows,), dtype=torch.int32, device=self.device)
+        if self._mirror is not None:
+            mirror[:cur_rows, :cur_width] = self._mirror
+            lens[:cur_rows] = self._mirror_len
+        self._mirror, self._mirror_len = mirror, lens
+
+    def device_tables(self, request_ids: Sequence[str | None], width: int | None = None,
+                      pad_block: int | None = None) -> torch.Tensor:
+        """block_table() built on the device: int32 [len(request_ids), width] gathered
+        from the mirror rows (fe_gather_tables), so a step copies one row index per
+        request instead of its whole table.  None entries are rows of pad_block."""
+        from . import ops
+        if self.device.type != "cuda":
+            raise RuntimeError("device_tables needs a GPU cache")
+        rows = []
+        for r in request_ids:
+            if r is None:
+                rows.append(-1)
+                continue
+            if len(self.tables[r]) > (width if width is not None else len(self.tables[r])):
+                raise ValueError("table wider than the requested width")
+            rows.append(self._rows[r])
+        if width is None:
+            width = max((len(self.tables[r]) for r in request_ids if r is not None), default=1)
+        if self._mirror is None:
+            self._grow_mirror(1, 1)
+        idx = torch.tensor(rows, dtype=torch.int32).to(self.device, non_blocking=True)
+        return ops.gather_tables(self._mirror, self._mirror_len, idx, width,
+                                 -1 if pad_block is None else pad_block)
 
     # ---- data movement (HIP kernels) --------------------------------------------------
 

@@ -156,17 +156,20 @@ class Qwen2Model:
         ids = torch.tensor([t for c in chunks for t in c.input_ids], dtype=torch.long).to(dev)
         pos_list = [p for c in chunks for p in range(c.start, c.start + len(c.input_ids))]
         positions = torch.tensor(pos_list, dtype=torch.long).to(dev)
-        # slot map of every new token, built once for all layers (allocator.py:107-114)
-        blocks, offsets = [], []
+        # the write's checks of allocator.py:107-125 on the host bookkeeping (slots
+        # reserved, no shared block written); the slot map itself is computed on
+        # the device from the block tables (fe_write_kv_ragged), which are
+        # gathered from the cache's device mirror (fe_gather_tables)
+        bs = cache.layout.block_size
         for c in chunks:
-            b, o = cache._locators(c.request_id, c.start, len(c.input_ids))
-            if any(cache.refs[blk] > 1 for blk in set(b)):
+            end = c.start + len(c.input_ids)
+            if c.start < 0 or end > cache.available_slots(c.request_id):
+                raise IndexError("KV slots not reserved")
+            table = cache.tables[c.request_id]
+            if any(cache.refs[table[p]] > 1 for p in range(c.start // bs, (end - 1) // bs + 1)):
                 raise RuntimeError("cannot write a shared immutable KV block")
-            blocks += b
-            offsets += o
-        slots = torch.tensor([blocks, offsets], dtype=torch.int32).to(dev)
         width = max(len(cache.tables[c.request_id]) for c in chunks)
-        tables = cache.block_table([c.request_id for c in chunks], width)
+        tables = cache.device_tables([c.request_id for c in chunks], width)
         q_offsets = torch.tensor([0] + [sum(lengths[:j + 1]) for j in range(len(lengths))],
                                  dtype=torch.int32).to(dev)
         ctx = torch.tensor([c.start + n for c, n in zip(chunks, lengths)], dtype=torch.int32).to(dev)
@@ -175,7 +178,7 @@ class Qwen2Model:
         h, _ = ops.rmsnorm(x, self.layer_weights[0].input_norm, self.cfg.rms_norm_eps)
         for layer, lw in enumerate(self.layer_weights):
             q, k, v = self._qkv(h, lw, positions)
-            ops.write_kv(k, v, cache.k[layer], cache.v[layer], slots[0], slots[1])
+            ops.write_kv_ragged(k, v, cache.k[layer], cache.v[layer], tables, q_offsets, ctx)
             attn = ops.prefill_paged(q, cache.k[layer], cache.v[layer], tables, q_offsets, ctx,
                                      max_q, scale=self.scale)
             h = self._after_attention(x, attn, lw, self._next_norm(layer))

@@ -78,6 +78,47 @@ def write_kv(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_p
               slot_offset.data_ptr(), t, hkv, d, bs, _stream(dev))
 
 
+def write_kv_ragged(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor,
+                    v_pool: torch.Tensor, block_tables: torch.Tensor, q_offsets: torch.Tensor,
+                    context_lens: torch.Tensor) -> None:
+    """Writes the new rows of ragged chunks with the slot map computed on the device:
+    rows q_offsets[s]..q_offsets[s+1]-1 are the last positions of sequence s's
+    context_lens[s] tokens (the arrays prefill_paged takes; fe_write_kv_ragged)."""
+    dev = _require_gpu(k_new, v_new, k_pool, v_pool, block_tables, q_offsets, context_lens)
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
+    if k_new.shape != v_new.shape or k_new.ndim != 3 or tuple(k_new.shape[1:]) != (hkv, d):
+        raise ValueError("K/V shapes must be [tokens, kv_heads, head_dim]")
+    if k_new.dtype != FP16 or v_new.dtype != FP16:
+        raise ValueError("wrong KV dtype")
+    if k_new.stride() != v_new.stride() or k_new.stride(2) != 1 or k_new.stride(1) != d:
+        raise ValueError("new K/V rows must have contiguous heads and equal strides")
+    block_tables = _int32(block_tables, "block_tables")
+    q_offsets, context_lens = _int32(q_offsets, "q_offsets"), _int32(context_lens, "context_lens")
+    s = context_lens.shape[0]
+    if block_tables.ndim != 2 or block_tables.shape[0] != s or q_offsets.shape != (s + 1,):
+        raise ValueError("block_tables must be [S, W], q_offsets [S+1], context_lens [S]")
+    _lib.call("fe_write_kv_ragged", k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0),
+              k_pool.data_ptr(), v_pool.data_ptr(), nb, block_tables.data_ptr(),
+              block_tables.shape[1], q_offsets.data_ptr(), context_lens.data_ptr(), s,
+              k_new.shape[0], hkv, d, bs, _stream(dev))
+
+
+def gather_tables(mirror: torch.Tensor, row_len: torch.Tensor, rows: torch.Tensor, width: int,
+                  pad_block: int = -1) -> torch.Tensor:
+    """int32 [len(rows), width] block tables from the device mirror rows (fe_gather_tables);
+    entries past a row's length are pad_block, or its last block when pad_block < 0."""
+    dev = _require_gpu(mirror, row_len, rows)
+    mirror, row_len, rows = _int32(mirror, "mirror"), _int32(row_len, "row_len"), _int32(rows, "rows")
+    if mirror.ndim != 2 or row_len.shape != (mirror.shape[0],) or rows.ndim != 1:
+        raise ValueError("mirror must be [R, M], row_len [R], rows [B]")
+    width = max(int(width), 1)
+    out = torch.empty((rows.shape[0], width), dtype=torch.int32, device=dev)
+    _lib.call("fe_gather_tables", mirror.data_ptr(), mirror.shape[1], row_len.data_ptr(),
+              mirror.shape[0], rows.data_ptr(), rows.shape[0], width, int(pad_block),
+              out.data_ptr(), width, _stream(dev))
+    return out
+
+
 def write_kv_decode(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor,
                     v_pool: torch.Tensor, block_tables: torch.Tensor,
                     context_lens: torch.Tensor) -> None:

@@ -82,6 +82,44 @@ int fe_write_kv_decode(const void* k_new, const void* v_new, int64_t new_batch_s
                        fe_stream_t stream);
 
 /*
+ * Ragged-chunk KV page write with device-side slot mapping: sequence s owns
+ * new rows q_offsets[s] .. q_offsets[s+1]-1 of k_new / v_new ([total_tokens,
+ * kv_heads, head_dim], rows new_token_stride elements apart), which are the
+ * last n_s = q_offsets[s+1] - q_offsets[s] positions of its context of
+ * context_lens[s] tokens; row i goes to position p = context_lens[s] - n_s +
+ * (i - q_offsets[s]), block block_tables[s, p / block_size], offset
+ * p % block_size (the same arrays fe_prefill_paged takes).  Rows whose page
+ * or block id is out of range are skipped.  Bit-exact copy.
+ * Replaces the per-request cache.write of the ragged forward
+ * (src/flexengine/inference/models/qwen2.py:117-126) and its slot map
+ * PagedKVCache._locators / write (src/flexengine/engine/kv_cache/allocator.py:
+ * 107-127): no host-built slot list, no device-to-host synchronisation.
+ */
+int fe_write_kv_ragged(const void* k_new, const void* v_new, int64_t new_token_stride,
+                       void* k_pool, void* v_pool, int num_blocks,
+                       const int32_t* block_tables, int table_stride,
+                       const int32_t* q_offsets, const int32_t* context_lens,
+                       int num_seqs, int total_tokens, int kv_heads, int head_dim,
+                       int block_size, fe_stream_t stream);
+
+/*
+ * Block tables of a batch built on the device from a device-resident mirror
+ * of the allocator's tables: mirror is int32 [mirror_rows, mirror_stride]
+ * with row r holding row_len[r] valid block ids; for b < batch and j < width,
+ *   out[b, j] = mirror[rows[b], j]            if j < row_len[rows[b]],
+ *             = pad_block                      otherwise (pad_block >= 0),
+ *             = the row's last block (0 if empty)  otherwise (pad_block < 0);
+ * rows[b] < 0 gives a row of padding.  out rows are out_stride apart.
+ * Replaces the per-step host fill of the padded block tables
+ * (src/flexengine/engine/runtime.py:205-213, _graph_inputs) and
+ * PagedKVCache.block_table: a step copies `batch` row indices instead of
+ * batch * width table entries.
+ */
+int fe_gather_tables(const int32_t* mirror, int mirror_stride, const int32_t* row_len,
+                     int mirror_rows, const int32_t* rows, int batch, int width,
+                     int pad_block, int32_t* out, int out_stride, fe_stream_t stream);
+
+/*
  * Block-table gather ("materialize"): for every sequence b and position
  * t < context_lens[b],
  *   k_out[out_offsets[b] + t] = k_pool[block_tables[b, t/bs], t%bs]   (and v)

@@ -146,3 +146,90 @@ def test_paged_cache_write_materialize_roundtrip():
     c.attach_prefix("p", [0])
     with pytest.raises(RuntimeError, match="shared immutable"):
         c.write(0, "a", 0, a[:1], a[:1])
+
+
+# --------------------------------------------------------------------------------------
+# device-side slot mapping of the ragged write and device-built block tables
+# --------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bs,h,d", [(16, 2, 128), (1, 2, 64), (4, 1, 64), (32, 4, 128)])
+def test_write_kv_ragged_matches_the_per_request_write(bs, h, d):
+    """Chunks of 1..70 new tokens after 0..100 cached ones (crossing block edges),
+    through fe_write_kv_ragged, byte-for-byte equal to the oracle's per-request
+    write (allocator.py:107-127) into a pool with stale contents elsewhere."""
+    g = torch.Generator().manual_seed(bs + h + d)
+    news, cached = [1, 17, 70, 5, 33], [0, 100, 3, 16 * 3, 7]
+    nb = sum(-(-(c + n) // bs) for c, n in zip(cached, news)) + 5
+    perm = torch.randperm(nb, generator=g).tolist()
+    tables, at = [], 0
+    for c, n in zip(cached, news):
+        p = -(-(c + n) // bs)
+        tables.append(perm[at:at + p])
+        at += p
+    width = max(len(t) for t in tables)
+    tab = torch.tensor([t + [t[-1]] * (width - len(t)) for t in tables], dtype=torch.int32)
+    k_pool = torch.randn(nb, bs, h, d, generator=g).half()
+    v_pool = torch.randn(nb, bs, h, d, generator=g).half()
+    keys = torch.randn(sum(news), h, d, generator=g).half()
+    vals = torch.randn(sum(news), h, d, generator=g).half()
+    offs = np.concatenate([[0], np.cumsum(news)]).astype(np.int32)
+    ctx = torch.tensor([c + n for c, n in zip(cached, news)], dtype=torch.int32)
+    ek, ev = k_pool.numpy().copy(), v_pool.numpy().copy()
+    for s, (c, n) in enumerate(zip(cached, news)):
+        R.write_kv(ek, ev, tables[s], c, keys[offs[s]:offs[s + 1]].numpy(),
+                   vals[offs[s]:offs[s + 1]].numpy(), bs)
+    kd, vd = k_pool.to(DEV), v_pool.to(DEV)
+    ops.write_kv_ragged(keys.to(DEV), vals.to(DEV), kd, vd, tab.to(DEV),
+                        torch.tensor(offs).to(DEV), ctx.to(DEV))
+    assert kd.cpu().numpy().tobytes() == ek.tobytes()
+    assert vd.cpu().numpy().tobytes() == ev.tobytes()
+
+
+def test_device_tables_follow_the_allocator():
+    """The device mirror tracks reserve (growth past the mirror's first width),
+    attach_prefix, free_request and the reuse of freed rows; device_tables equals
+    the host-built block_table for every padding choice, and None rows are pads."""
+    c = PagedKVCache(CacheLayout(1, 400, 4, 1, 8), device=DEV)
+    c.reserve("a", 9)
+    c.reserve("b", 1)
+    c.reserve("c", 0)
+    c.attach_prefix("p", c.tables["a"][:2])
+    c.reserve("a", 4 * 90)                      # 90 blocks: wider than the initial mirror
+    c.free_request("b")
+    c.reserve("d", 20)                          # reuses b's mirror row
+    c.reserve("p", 14)
+    ids = ["a", "c", "p", "d"]
+    width = max(len(c.tables[r]) for r in ids)
+    for pad in (None, 7):
+        want = c.block_table(ids, width, pad_block=pad)
+        got = c.device_tables(ids, width, pad_block=pad)
+        assert torch.equal(got, want), pad
+    got = c.device_tables(["d", None, "p"], 100, pad_block=3)
+    assert got[1].tolist() == [3] * 100
+    assert got[0, :5].tolist() == c.tables["d"] and got[0, 5:].tolist() == [3] * 95
+    c.tables["d"] = list(reversed(c.tables["d"]))   # a direct edit needs a sync
+    c.sync_device_table("d")
+    assert c.device_tables(["d"])[0].tolist() == c.tables["d"]
+    with pytest.raises(ValueError):
+        c.device_tables(["a"], 10)
+
+
+def test_graph_inputs_pad_rows_with_a_scratch_block():
+    """runtime.py:201-213: active rows carry token, position and table; padded rows
+    and the table tails hold a scratch block."""
+    from flexengine_amd.decode_step import SCRATCH_ID, GraphDecodeStep
+    from flexengine_amd.model import Chunk
+    cache = PagedKVCache(CacheLayout(1, 40, 4, 2, 8), device=DEV)
+    cache.reserve("a", 6)
+    step = GraphDecodeStep(model=None, cache=cache, max_model_len=16)
+    assert len(cache.tables[SCRATCH_ID]) == 8 * 4 // 4
+    inp = step.graph_inputs([Chunk("a", [42], 5)], 4)
+    assert inp["input_ids"].tolist() == [42, 0, 0, 0]
+    assert inp["positions"].tolist() == [5, 0, 0, 0]
+    assert inp["block_tables"].dtype == torch.int32
+    scratch = step.scratch_blocks[0]
+    assert inp["block_tables"][0].tolist() == cache.tables["a"] + [scratch] * 2
+    for row in range(1, 4):
+        assert inp["block_tables"][row].tolist() == [scratch] * 4
+    with pytest.raises(ValueError):
+        step.graph_inputs([Chunk("a", [1], 0)] * 5, 4)

@@ -172,22 +172,10 @@ def test_model_requires_gpu():
         Qwen2Model(Qwen2Config(num_hidden_layers=1, vocab_size=16), device="cpu")
 
 
-def test_graph_inputs_pad_rows_with_scratch_blocks():
-    """runtime.py:201-213: padded rows point at scratch blocks; active rows carry
-    token, position and table."""
-    from flexengine_amd.decode_step import SCRATCH_ID, GraphDecodeStep
-    from flexengine_amd.model import Chunk
+def test_device_tables_need_a_gpu_cache():
+    """The step path builds its block tables on the device (fe_gather_tables); a
+    cache that does not live on a GPU refuses instead of filling them on the host."""
     cache = PagedKVCache(CacheLayout(1, 40, 4, 2, 8), device="cpu")
     cache.reserve("a", 6)
-    step = GraphDecodeStep(model=None, cache=cache, max_model_len=16)
-    assert len(cache.tables[SCRATCH_ID]) == 8 * 4 // 4
-    inp = step.graph_inputs([Chunk("a", [42], 5)], 4)
-    assert inp["input_ids"].tolist() == [42, 0, 0, 0]
-    assert inp["positions"].tolist() == [5, 0, 0, 0]
-    table = cache.tables["a"]
-    assert inp["block_tables"][0, :2].tolist() == table
-    assert inp["block_tables"][0, 2:].tolist() == [step.scratch_blocks[0]] * 2
-    for row in range(1, 4):
-        assert inp["block_tables"][row].tolist() == [step.scratch_blocks[row]] * 4
-    with pytest.raises(ValueError):
-        step.graph_inputs([Chunk("a", [1], 0)] * 5, 4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        cache.device_tables(["a"], 4)
