@@ -503,7 +503,7 @@ int ks_for(int tiles, int K) {
 extern "C" size_t fe_gemm_fused_workspace_size(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return kFusedTicketBytes;
   const int tiles = (N + 15) / 16;
-  const int mt = M <= 16 ? 1 : 2;
+  const int mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   return kFusedTicketBytes + (size_t)tiles * ks_for(tiles, K) * mt * kWave * 16;
 }
 
@@ -540,6 +540,7 @@ int launch_fused(FusedArgs a, int tiles, void* workspace, size_t workspace_bytes
   // split workgroups: 4 waves (1, 2, 8 and 16 measured slower)
   int waves = a.ks_count > 1 ? 4 : waves_for(tiles, a.K);
   if (a.M > 16 && waves > 8) waves = 8;  // two row tiles: the register budget of 8 waves
+  if (a.M > 32 && waves > 4) waves = 4;  // four row tiles: at most 4 waves
   int kslice = (a.kslice_wg + waves - 1) / waves;
   a.kslice = (kslice + 31) / 32 * 32;
   const dim3 grid((unsigned)((int64_t)tiles * a.ks_count));
@@ -552,9 +553,15 @@ int launch_fused(FusedArgs a, int tiles, void* workspace, size_t workspace_bytes
     else if (waves == 2) FE_FUSED(1, 2);
     else if (waves == 1) FE_FUSED(1, 1);
     else FE_FUSED(1, 4);
-  } else {
+  } else if (a.M <= 32) {
     if (waves == 8) FE_FUSED(2, 8);
+    else if (waves == 2) FE_FUSED(2, 2);
+    else if (waves == 1) FE_FUSED(2, 1);
     else FE_FUSED(2, 4);
+  } else {
+    if (waves == 1) FE_FUSED(4, 1);
+    else if (waves == 2) FE_FUSED(4, 2);
+    else FE_FUSED(4, 4);
   }
 #undef FE_FUSED
   return FE_LAUNCH_STATUS();
@@ -564,7 +571,7 @@ int launch_fused(FusedArgs a, int tiles, void* workspace, size_t workspace_bytes
 int fill_common(FusedArgs& a, const void* x, const float* x_ss, int ss_tiles, const void* norm_w,
                 float eps, int M, int K, const void* W, int N) {
   FE_CHECK_ARG(M >= 0 && K > 0 && N > 0);
-  if (M > 32 || K % 32 != 0) return FE_ERR_UNSUPPORTED;
+  if (M > 64 || K % 32 != 0) return FE_ERR_UNSUPPORTED;
   // 32-bit buffer offsets into W and x
   FE_CHECK_ARG((int64_t)N * K * 2 < ((int64_t)1 << 31) && (int64_t)M * K * 2 < ((int64_t)1 << 31));
   FE_CHECK_ARG(x && W);

@@ -38,6 +38,7 @@ import torch
 from flexengine_amd import attention, ops
 
 
+
 @dataclass
 class Qwen2Config:
     vocab_size: int = 151936

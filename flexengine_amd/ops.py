@@ -474,7 +474,7 @@ def _fused_ws(dev: torch.device, m: int, n: int, k: int) -> torch.Tensor:
 
 
 def gemm_f16(x, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
-    """fp16(x @ weight^T + bias) for M <= 32 rows; x is fp16 [M, K] or Normed."""
+    """fp16(x @ weight^T + bias) for M <= 64 rows; x is fp16 [M, K] or Normed."""
     r, ss, tiles, nw, eps = _operand(x, weight)
     dev = _require_gpu(r, weight, bias)
     out = torch.empty((r.shape[0], weight.shape[0]), dtype=FP16, device=dev)

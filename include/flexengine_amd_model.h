@@ -83,7 +83,7 @@ int fe_gemm_skinny(const void* x, int M, int K, const void* W, int N, float* par
 
 /*
  * Decode-step projections with their element-wise neighbours fused
- * (M <= 32 rows, K a multiple of 32; the workgroups of a 16-row output tile
+ * (M <= 64 rows, K a multiple of 32; the workgroups of a 16-row output tile
  * reduce K among themselves -- split-K partial tiles meet in `workspace` and the
  * last workgroup adds them in split order -- so results are final fp16 values,
  * deterministic from call to call).  workspace: at least

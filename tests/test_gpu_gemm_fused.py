@@ -44,7 +44,7 @@ def tile_ss(r):
 
 
 SHAPES = [(1, 1536, 1536), (8, 2048, 1536), (16, 1000, 96), (17, 300, 1536), (32, 4000, 8960),
-          (3, 1536, 8960)]
+          (3, 1536, 8960), (33, 1536, 1536), (48, 2048, 8960), (64, 4000, 1536), (64, 1536, 8960)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
@@ -69,7 +69,7 @@ def test_gemm_resid_adds_residual_and_tile_sums(m, n, k):
 
 
 @pytest.mark.parametrize("m,inter,k", [(1, 8960, 1536), (8, 4864, 896), (17, 100, 1536),
-                                       (32, 8960, 1536)])
+                                       (32, 8960, 1536), (64, 8960, 1536), (40, 100, 512)])
 def test_gemm_silu_matches_unfused_chain(m, inter, k):
     x, w = randn(m, k, seed=7), randn(2 * inter, k, seed=8, scale=0.05)
     g, u = prod16(x, w[:inter]), prod16(x, w[inter:])
@@ -80,7 +80,8 @@ def test_gemm_silu_matches_unfused_chain(m, inter, k):
 
 
 @pytest.mark.parametrize("m,hq,hkv,d,k", [(1, 12, 2, 128, 1536), (8, 14, 2, 64, 896),
-                                          (17, 4, 4, 128, 512), (32, 12, 2, 128, 1536)])
+                                          (17, 4, 4, 128, 512), (32, 12, 2, 128, 1536),
+                                          (64, 12, 2, 128, 1536)])
 def test_gemm_rope_matches_unfused_chain(m, hq, hkv, d, k):
     n = (hq + 2 * hkv) * d
     x, w, b = randn(m, k, seed=9), randn(n, k, seed=10, scale=0.05), randn(n, seed=11)
@@ -137,7 +138,7 @@ def test_resid_feeds_norm_prologue_like_the_unfused_layer():
 def test_fused_gemms_reject_unsupported_shapes():
     from flexengine_amd._lib import FlexEngineAMDError
     with pytest.raises(FlexEngineAMDError):
-        ops.gemm_f16(randn(33, 64), randn(16, 64))
+        ops.gemm_f16(randn(65, 64), randn(16, 64))
     with pytest.raises(FlexEngineAMDError):
         ops.gemm_f16(randn(2, 40), randn(16, 40))
     with pytest.raises(ValueError):
@@ -145,7 +146,7 @@ def test_fused_gemms_reject_unsupported_shapes():
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 1536, 1536), (8, 1536, 8960), (17, 896, 4864),
-                                   (32, 2048, 512), (3, 16, 64)])
+                                   (32, 2048, 512), (3, 16, 64), (64, 1536, 8960), (50, 896, 1536)])
 def test_resid_rmsnorm_equals_resid_then_rmsnorm(m, n, k):
     """One launch == fe_gemm_resid then fe_rmsnorm: r bit-identical, the norm within
     two fp16 ulps (the mean of r^2 is summed from the tile sums, in another order than
