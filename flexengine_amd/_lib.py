@@ -52,8 +52,10 @@ SIGNATURES: dict[str, tuple] = {
     "fe_gemm_skinny_splits": (_i, [_i, _i]),
     "fe_gemm_skinny": (_i, [_p, _i, _i, _p, _i, _p, _i, _p]),
     "fe_gemm_fused_workspace_size": (_sz, [_i, _i, _i]),
+    "fe_gemm_rows64_workspace_size": (_sz, [_i, _i, _i]),
     "fe_gemm_f16": (_i, [_p, _p, _i, _p, _f, _i, _i, _p, _i, _p, _p, _p, _sz, _p]),
     "fe_gemm_resid": (_i, [_p, _i, _i, _p, _i, _p, _p, _p, _p, _sz, _p]),
+    "fe_gemm_rows64": (_i, [_p, _i, _i, _p, _i, _p, _p, _p, _sz, _p]),
     "fe_gemm_resid_rmsnorm": (_i, [_p, _i, _i, _p, _i, _p, _p, _p, _p, _f, _p, _p, _sz, _p]),
     "fe_gemm_silu": (_i, [_p, _p, _i, _p, _f, _i, _i, _p, _i, _p, _p, _sz, _p]),
     "fe_gemm_rope": (_i, [_p, _p, _i, _p, _f, _i, _i, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p,

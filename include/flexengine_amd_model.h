@@ -147,6 +147,20 @@ int fe_gemm_rope(const void* x, const float* x_ss, int ss_tiles, const void* nor
                  void* q_out, void* k_out, void* v_out, void* workspace,
                  size_t workspace_bytes, fe_stream_t stream);
 
+/*
+ * out [M, N] = fp16(x [M, K] @ W^T + bias) for 33..64 rows (any M <= 64; K a
+ * multiple of 32; bias [N] may be NULL): the four waves of a workgroup take four
+ * 16-row weight tiles over the same keys and share each 128-key chunk of x
+ * through LDS.  workspace: at least fe_gemm_rows64_workspace_size(M, N, K)
+ * bytes, 256-byte aligned, zero-filled before its first use (split-K tickets
+ * that every call leaves at zero, then partial tiles).  The batch-64 decode
+ * step's projections and LM head (qwen2.py:152-154,183-186), replacing the
+ * library GEMM there.
+ */
+size_t fe_gemm_rows64_workspace_size(int M, int N, int K);
+int fe_gemm_rows64(const void* x, int M, int K, const void* W, int N, const void* bias,
+                   void* out, void* workspace, size_t workspace_bytes, fe_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

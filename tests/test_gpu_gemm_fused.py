@@ -190,3 +190,31 @@ def test_resid_rmsnorm_rejects_unsupported_widths():
     for n in (24, 2064):
         with pytest.raises(FlexEngineAMDError):
             ops.gemm_resid_rmsnorm(randn(2, 64), randn(n, 64), randn(2, n), randn(n), 1e-6)
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 1536, 1536), (64, 2048, 1536), (48, 17920, 1536),
+                                   (33, 1536, 8960), (64, 100, 96), (1, 40, 4000),
+                                   (17, 1000, 224), (64, 151, 8960)])
+def test_gemm_rows64_matches_rounded_product(m, n, k):
+    """fe_gemm_rows64 (x staged in LDS, shared by four weight tiles): within one fp16
+    rounding of the fp32 product (+ bias), split-K or not, tile counts that are not a
+    multiple of four, steps shorter than 128 keys; repeated calls bit-identical."""
+    x, w, b = randn(m, k, seed=41), randn(n, k, seed=42, scale=0.05), randn(n, seed=43)
+    got = ops.gemm_rows64(x, w, b)
+    assert_close16(got, prod16(x, w, b))
+    assert torch.equal(ops.gemm_rows64(x, w, b), got)
+    assert_close16(ops.gemm_rows64(x, w), prod16(x, w))
+
+
+def test_gemm_rows64_alternating_shapes_share_the_workspace():
+    a = (randn(64, 8960, seed=44), randn(1536, 8960, seed=45, scale=0.02))
+    b = (randn(40, 1536, seed=46), randn(2048, 1536, seed=47, scale=0.05))
+    first = {}
+    for rep in range(3):
+        for name, (x, w) in (("a", a), ("b", b)):
+            got = ops.gemm_rows64(x, w)
+            assert_close16(got, prod16(x, w))
+            if name in first:
+                assert torch.equal(first[name], got)
+            else:
+                first[name] = got
