@@ -49,7 +49,11 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kBlockKeys = 32;
 constexpr int kKT = kBlockKeys / 16;    // 16-key S tiles per block
 constexpr int kPS = kBlockKeys / 32;    // 32-key PV steps per block
-constexpr int kMaxSplits = 8;   // key splits per row block (plan() clamps to it)
+// Key splits per row block (plan() clamps to it).  The merge loads all kMaxSplits
+// slots at once, so the bound is also its load count: 4 measured best (C4 prefill
+// 55 us; 8: 61 us, 8 with loads only for the live splits: 57.5 us, 2: 63 us; the
+// C3 shared-prefix decode 81 us at 4 and 8, 91 us at 2).
+constexpr int kMaxSplits = 4;
 // Two 16-row tiles per wave (RT = 2) once the rows fill this many 128-row blocks;
 // below it the extra blocks of RT = 1 fill the CUs better (measured: 1377 new tokens
 // x 12 heads run slower with RT = 2).
