@@ -173,12 +173,26 @@ __global__ __launch_bounds__(kThreadsR) void gemm_rows64_kernel(const RowsArgs a
       __hip_atomic_store(a.tickets + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < a.ks_count; ++s) {
+    // MB splits' partials in flight at once (a load-add loop would wait out one
+    // round trip per split), added in split order
+    constexpr int MB = 16 / MT;
+    for (int s0 = 0; s0 < a.ks_count; s0 += MB) {
+      f32x4 pv[MB][MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        acc[mt] += __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rp, (uint32_t)(((s * MT + mt) * kWave + lane) * 16), 0, kSc1));
+      for (int u = 0; u < MB; ++u)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          pv[u][mt] = s0 + u < a.ks_count
+                          ? __builtin_bit_cast(
+                                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rp, (uint32_t)((((s0 + u) * MT + mt) * kWave + lane) * 16),
+                                           0, kSc1))
+                          : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < MB; ++u)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          if (s0 + u < a.ks_count) acc[mt] += pv[u][mt];
     }
   }
 

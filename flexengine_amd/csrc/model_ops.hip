@@ -37,6 +37,7 @@ struct Src {
     if (splits == 0) return (float)static_cast<const f16*>(p)[(int64_t)row * stride + col];
     const float* f = static_cast<const float*>(p);
     float acc = 0.f;
+#pragma unroll 4  // four partial loads in flight per round trip; added in split order
     for (int k = 0; k < splits; ++k) acc += f[((int64_t)k * rows + row) * cols + col];
     if (bias) acc += (float)bias[col];
     return round16(acc);
