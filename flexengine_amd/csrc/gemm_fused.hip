@@ -590,6 +590,8 @@ int fill_common(FusedArgs& a, const void* x, const float* x_ss, int ss_tiles, co
   // 32-bit buffer offsets into W and x
   FE_CHECK_ARG((int64_t)N * K * 2 < ((int64_t)1 << 31) && (int64_t)M * K * 2 < ((int64_t)1 << 31));
   FE_CHECK_ARG(x && W);
+  // x and W are read with 16-byte loads
+  FE_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W)) & 15) == 0);
   FE_CHECK_ARG(x_ss == nullptr || (ss_tiles > 0 && ss_tiles <= 4 * kMaxSsPerLane && norm_w != nullptr));
   a = FusedArgs{};
   a.W = (const f16*)W;

@@ -241,6 +241,8 @@ extern "C" int fe_gemm_rows64(const void* x, int M, int K, const void* W, int N,
   if (M == 0) return FE_OK;
   FE_CHECK_ARG(x && W && out);
   FE_CHECK_ARG(out != x);
+  // x and W are read with 16-byte loads
+  FE_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W)) & 15) == 0);
   const int tiles = (N + 15) / 16;
   if (tiles > (int)(kTicketBytesR / sizeof(int))) return FE_ERR_UNSUPPORTED;
   RowsArgs a;

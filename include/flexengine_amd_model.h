@@ -83,7 +83,8 @@ int fe_gemm_skinny(const void* x, int M, int K, const void* W, int N, float* par
 
 /*
  * Decode-step projections with their element-wise neighbours fused
- * (M <= 64 rows, K a multiple of 32; the workgroups of a 16-row output tile
+ * (M <= 64 rows, K a multiple of 32, x and W 16-byte aligned; the workgroups
+ * of a 16-row output tile
  * reduce K among themselves -- split-K partial tiles meet in `workspace` and the
  * last workgroup adds them in split order -- so results are final fp16 values,
  * deterministic from call to call).  workspace: at least
@@ -149,13 +150,15 @@ int fe_gemm_rope(const void* x, const float* x_ss, int ss_tiles, const void* nor
 
 /*
  * out [M, N] = fp16(x [M, K] @ W^T + bias) for 33..64 rows (any M <= 64; K a
- * multiple of 32; bias [N] may be NULL): the four waves of a workgroup take four
+ * multiple of 32; x and W 16-byte aligned; bias [N] may be NULL): the four
+ * waves of a workgroup take four
  * 16-row weight tiles over the same keys and share each 128-key chunk of x
  * through LDS.  workspace: at least fe_gemm_rows64_workspace_size(M, N, K)
  * bytes, 256-byte aligned, zero-filled before its first use (split-K tickets
- * that every call leaves at zero, then partial tiles).  The batch-64 decode
- * step's projections and LM head (qwen2.py:152-154,183-186), replacing the
- * library GEMM there.
+ * that every call leaves at zero, then partial tiles).  Replaces the library
+ * GEMM for the batch-64 decode step's deep projection (K >= 4 N: the MLP down
+ * projection, qwen2.py:183-184), where it measured faster; wide projections
+ * stay on the library GEMM.
  */
 size_t fe_gemm_rows64_workspace_size(int M, int N, int K);
 int fe_gemm_rows64(const void* x, int M, int K, const void* W, int N, const void* bias,

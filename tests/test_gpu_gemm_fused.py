@@ -218,3 +218,17 @@ def test_gemm_rows64_alternating_shapes_share_the_workspace():
                 assert torch.equal(first[name], got)
             else:
                 first[name] = got
+
+
+def test_projections_reject_misaligned_operands():
+    """x and W are read with 16-byte loads: a pointer off that alignment is an argument
+    error returned before any launch (here x starts one fp16 element into its buffer)."""
+    from flexengine_amd._lib import FlexEngineAMDError
+    flat = randn(2 * 256 + 8, seed=48)
+    x = flat[1:1 + 2 * 256].view(2, 256)
+    assert x.is_contiguous() and x.data_ptr() % 16 != 0
+    w = randn(64, 256, seed=49, scale=0.05)
+    for fn in (ops.gemm_rows64, ops.gemm_f16):
+        with pytest.raises(FlexEngineAMDError):
+            fn(x, w)
+    assert_close16(ops.gemm_rows64(x.clone(), w), prod16(x, w))
