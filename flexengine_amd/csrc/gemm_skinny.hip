@@ -158,6 +158,8 @@ extern "C" int fe_gemm_skinny(const void* x, int M, int K, const void* W, int N,
   FE_CHECK_ARG((int64_t)16 * K * 2 < ((int64_t)1 << 31) && (int64_t)M * K * 2 < ((int64_t)1 << 31));
   if (M == 0) return FE_OK;
   FE_CHECK_ARG(x && W && partials);
+  // x and W are read with 16-byte loads
+  FE_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W)) & 15) == 0);
   // 4 * splits slices of kslice keys (a multiple of 32); trailing slices may be
   // empty (their waves add zeros)
   const int slices = splits * kGemmWaves;

@@ -70,7 +70,8 @@ int fe_silu_mul(const void* gate_up, int64_t row_stride, int splits, void* out, 
 int fe_gemm_skinny_splits(int N, int K);
 
 /*
- * Skinny GEMM for decode-sized batches (M <= 32, K a multiple of 32):
+ * Skinny GEMM for decode-sized batches (M <= 32, K a multiple of 32, x and W
+ * 16-byte aligned):
  *   partials[s][m][o] = sum over k in slice s of x[m][k] * W[o][k]
  * x: fp16 [M, K]; W: fp16 [N, K] (PyTorch Linear weight layout); partials:
  * fp32 [splits][M][N] with splits = fe_gemm_skinny_splits(N, K).  Consumers

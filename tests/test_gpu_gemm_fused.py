@@ -228,7 +228,7 @@ def test_projections_reject_misaligned_operands():
     x = flat[1:1 + 2 * 256].view(2, 256)
     assert x.is_contiguous() and x.data_ptr() % 16 != 0
     w = randn(64, 256, seed=49, scale=0.05)
-    for fn in (ops.gemm_rows64, ops.gemm_f16):
+    for fn in (ops.gemm_rows64, ops.gemm_f16, ops.gemm_skinny):
         with pytest.raises(FlexEngineAMDError):
             fn(x, w)
     assert_close16(ops.gemm_rows64(x.clone(), w), prod16(x, w))
