@@ -42,9 +42,11 @@ class GraphDecodeStep:
             raise ValueError("more chunks than batch rows")
         ids = torch.zeros(batch_size, dtype=torch.long)
         positions = torch.zeros(batch_size, dtype=torch.long)
+        bs = self.cache.layout.block_size
         for row, chunk in enumerate(chunks):
-            if len(self.cache.tables[chunk.request_id]) > self.max_blocks:
-                raise ValueError("request longer than max_model_len")
+            if self.cache.available_slots(chunk.request_id) > self.max_blocks * bs:
+                raise ValueError(f"request {chunk.request_id!r} holds more blocks than "
+                                 f"max_model_len allows ({self.max_blocks})")
             ids[row] = chunk.input_ids[0]
             positions[row] = chunk.start
         requests = [c.request_id for c in chunks] + [None] * (batch_size - len(chunks))

@@ -8,6 +8,7 @@ the workspace / output buffers or lets them come from the graph pool.
 """
 from __future__ import annotations
 
+import contextlib
 import math
 
 import torch
@@ -164,6 +165,25 @@ def gather_kv(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Te
 # ---------------------------------------------------------------------------------------
 
 _WORKSPACES: dict[tuple, torch.Tensor] = {}
+# open hold_workspaces() scopes, innermost last
+_HOLDERS: list[list[torch.Tensor]] = []
+
+
+@contextlib.contextmanager
+def hold_workspaces():
+    """Collects every workspace decode_workspace() hands out inside the block.
+
+    A per-device workspace is replaced by a larger one when a call needs more
+    bytes, and the old buffer returns to the caching allocator once nothing
+    references it.  Work recorded into a HIP graph keeps the old address, so a
+    caller that captures kernels keeps the collected list for as long as the
+    graph may be replayed."""
+    held: list[torch.Tensor] = []
+    _HOLDERS.append(held)
+    try:
+        yield held
+    finally:
+        _HOLDERS.remove(held)
 
 
 def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_context: int,
@@ -179,7 +199,8 @@ def decode_workspace(device: torch.device, nbytes: int, kind: str = "decode") ->
 
     Calls on one stream are ordered, so sharing is safe there; callers running
     these kernels on several streams at once must pass their own zero-filled
-    workspace.
+    workspace.  A larger request replaces the buffer; see hold_workspaces() for
+    callers that record the kernels into a graph.
     """
     key = (device.type, device.index, kind)
     ws = _WORKSPACES.get(key)
@@ -188,6 +209,9 @@ def decode_workspace(device: torch.device, nbytes: int, kind: str = "decode") ->
         # (every call leaves them at zero again)
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
+    for held in _HOLDERS:
+        if not any(t is ws for t in held):
+            held.append(ws)
     return ws
 
 

@@ -85,3 +85,15 @@ def decode_batch_materialized(q: torch.Tensor, k_pool: torch.Tensor, v_pool: tor
         pos = torch.tensor([length - 1])
         out[b:b + 1] = materialized_route(q[b:b + 1], k_pool, v_pool, tables[b], length, pos)
     return out
+
+
+def decode_batch_blockwise(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                           tables: list[list[int]], context_lens: list[int]) -> torch.Tensor:
+    """The same per-request loop on the blockwise route (paged.py:50-70)."""
+    out = torch.zeros_like(q)
+    for b, length in enumerate(context_lens):
+        if length <= 0:
+            continue
+        pos = torch.tensor([length - 1])
+        out[b:b + 1] = blockwise_route(q[b:b + 1], k_pool, v_pool, tables[b], length, pos)
+    return out

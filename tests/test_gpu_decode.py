@@ -381,6 +381,17 @@ def test_shared_prefix_without_groups_is_the_plain_decode():
     assert torch.equal(got, plain)
 
 
+def test_c3_full_plain_and_cascade_against_oracle():
+    """Full C3 (8 groups x 32 rows sharing 2048 tokens, private tails U{16..2048}):
+    the plain decode and the shared-prefix decode each against the float64 oracle."""
+    w = workloads.c3_workload()
+    exp, _, _ = oracle_decode(w)
+    plain, _ = run_decode(w)
+    assert_attention_close(plain.numpy(), exp, what="full C3 plain decode")
+    cascade, _ = run_shared_prefix(w)
+    assert_attention_close(cascade.numpy(), exp, what="full C3 cascade decode")
+
+
 def test_shared_prefix_full_c3_against_plain_decode_and_repeatable():
     """Full C3 (8 groups x 32 sharing 2048 tokens): the cascade agrees with the
     plain decode to the contract tolerance and is bit-identical across calls."""

@@ -207,9 +207,9 @@ def test_device_tables_follow_the_allocator():
     got = c.device_tables(["d", None, "p"], 100, pad_block=3)
     assert got[1].tolist() == [3] * 100
     assert got[0, :5].tolist() == c.tables["d"] and got[0, 5:].tolist() == [3] * 95
-    c.tables["d"] = list(reversed(c.tables["d"]))   # a direct edit needs a sync
-    c.sync_device_table("d")
+    c.tables["d"] = list(reversed(c.tables["d"]))   # a reorder re-copies the row itself
     assert c.device_tables(["d"])[0].tolist() == c.tables["d"]
+    c.assert_invariants()                           # device tables == host tables
     with pytest.raises(ValueError):
         c.device_tables(["a"], 10)
 

@@ -10,6 +10,8 @@ configuration instead of HF weights.
 """
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 
@@ -171,3 +173,171 @@ def test_full_size_qwen25_15b_shapes_decode_and_prefill():
     assert out is not None and torch.isfinite(out[0]).all()
     out = step([Chunk("a", [int(out[0].argmax())], 20), Chunk("b", [int(out[1].argmax())], 4)])
     assert out is not None and step.manager.stats()["replays"] == 2
+
+
+# --------------------------------------------------------------------------------------
+# C5 at its stated configuration: Qwen2.5-1.5B shapes, contexts U{512..4096}
+# --------------------------------------------------------------------------------------
+
+C5_ROWS = 64
+C5_STEPS = 12
+
+
+@pytest.fixture(scope="module")
+def c5():
+    """Random-init Qwen2.5-1.5B (seed 5) and a paged cache holding 64 requests with
+    L ~ U{512..4096} tokens of N(0, 1) K/V in every layer (bench_model's set-up)."""
+    model = Qwen2Model(Qwen2Config(), DEV, seed=5)
+    gen = torch.Generator().manual_seed(505)
+    lengths = torch.randint(512, 4097, (C5_ROWS,), generator=gen).tolist()
+    tokens = torch.randint(0, model.cfg.vocab_size, (C5_ROWS,), generator=gen).tolist()
+    bs = 16
+    blocks = sum((n + C5_STEPS + bs) // bs + 1 for n in lengths) + 64
+    cache = PagedKVCache(CacheLayout(model.layers, blocks, bs, model.nkv, model.dim), device=DEV)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(5)
+    for layer in range(model.layers):
+        cache.k[layer].normal_(generator=g)
+        cache.v[layer].normal_(generator=g)
+    for b, n in enumerate(lengths):
+        cache.reserve(f"r{b}", n + C5_STEPS + 1)
+    step = GraphDecodeStep(model, cache, max_model_len=4096 + C5_STEPS + 32)
+    state = {"pos": list(lengths), "tok": tokens}
+    yield model, cache, step, state
+    del step, cache, model
+    torch.cuda.empty_cache()
+
+
+def _eager(model, cache, step, chunks):
+    inputs = step.graph_inputs(chunks, len(chunks))
+    return model.decode_static(**inputs, active_mask=torch.ones(len(chunks), device=DEV),
+                               cache=cache)
+
+
+def _agree(graph_rows, eager_rows, what):
+    """Logits within the model tolerance; greedy tokens equal wherever the eager
+    top-2 margin exceeds the tolerance (a near-tie may flip either way)."""
+    g = torch.stack(list(graph_rows)).double().cpu()
+    e = eager_rows.double().cpu()
+    scale = e.abs().max().item()
+    err = (g - e).abs()
+    print(f"{what}: max err {err.max().item():.3e} mean {err.mean().item():.3e} "
+          f"(max |logit| {scale:.3f})", flush=True)
+    assert err.max().item() <= MAX_REL * scale, what
+    assert err.mean().item() <= MEAN_REL * scale, what
+    top2 = e.topk(2, dim=-1).values
+    clear = (top2[:, 0] - top2[:, 1]) > 2 * MAX_REL * scale
+    assert torch.equal(g.argmax(-1)[clear], e.argmax(-1)[clear]), what
+
+
+def test_c5_buckets_captured_together_replay_interleaved_like_eager(c5):
+    """tests/gpu/test_engine_cuda_graph.py:45-57 at the C5 configuration: buckets 1, 2,
+    4 and 8 captured lazily in one GraphDecodeStep (the engine's order), replayed in
+    interleaved order for active counts 1, 2, 3, 4, 5, 8, each step matching eager
+    decode_static on the same cache state; 9 rows fall back.  Later replays of a
+    bucket captured before a larger one exercise the graph-owned workspaces."""
+    model, cache, step, st = c5
+    for n in (8, 1, 4, 2, 3, 5, 1, 8, 2, 4):
+        chunks = [Chunk(f"r{b}", [st["tok"][b]], st["pos"][b]) for b in range(n)]
+        eager = _eager(model, cache, step, chunks)
+        out = step(chunks)
+        assert out is not None, f"{n} rows fell back"
+        _agree(out, eager, f"C5 {n} active rows (bucket {step.manager.bucket_for(n)})")
+        for b in range(n):
+            st["tok"][b] = int(out[b].argmax())
+            st["pos"][b] += 1
+    stats = step.manager.stats()
+    assert stats["captures"] == 4 and stats["fallbacks"] == 0 and stats["replays"] == 10
+    assert stats["padded_slots"] == 1 + 3         # 3 rows in bucket 4, 5 rows in bucket 8
+    assert step([Chunk(f"r{b}", [st["tok"][b]], st["pos"][b]) for b in range(9)]) is None
+    assert step.manager.stats()["fallbacks"] == 1
+
+
+# Full-depth tolerance against the float32 reference: the 2-layer bounds above,
+# scaled by sqrt(28 / 2) for the independent fp16 roundings of 14x as many layers
+# (each layer rounds at about ten points), i.e. max 2e-2 and mean 4e-3 of
+# max |logit|.  A wrong row, position, head map or KV slot moves logits by tens
+# of percent.
+DEEP_MAX_REL, DEEP_MEAN_REL = 2e-2, 4e-3
+
+
+@torch.inference_mode()
+def _fp32_decode_reference(model, cache, chunks):
+    """Plain PyTorch float32 decode step of the same model on the same cache: fp32
+    weights, RMSNorm, RoPE (qwen2.py:73-77), attention over the cached K/V of
+    positions < p (read back from the pool) plus the step's own K/V at p, and the
+    tied LM head.  Logits [B, vocab] float32."""
+    cfg = model.cfg
+    eps, d, hq, hkv = cfg.rms_norm_eps, model.dim, model.nq, model.nkv
+    grp = hq // hkv
+    dev = model.device
+    bs = cache.layout.block_size
+    pos = torch.tensor([c.start for c in chunks], device=dev)
+    x = model.embed.index_select(0, torch.tensor([c.input_ids[0] for c in chunks],
+                                                 device=dev)).float()
+    ang = pos[:, None].float() * model.inv_freq[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], -1)[:, None, :]
+    sin = torch.cat([ang.sin(), ang.sin()], -1)[:, None, :]
+
+    def rms(t, w):
+        return t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+
+    def rope(t):
+        rot = torch.cat([-t[..., d // 2:], t[..., :d // 2]], -1)
+        return t * cos + rot * sin
+
+    tables = [torch.tensor(cache.tables[c.request_id], device=dev) for c in chunks]
+    for layer, lw in enumerate(model.layer_weights):
+        h = rms(x, lw.input_norm)
+        qkv = h @ lw.w_qkv.float().t() + lw.b_qkv.float()
+        q = rope(qkv[:, :hq * d].reshape(-1, hq, d))
+        k = rope(qkv[:, hq * d:(hq + hkv) * d].reshape(-1, hkv, d))
+        v = qkv[:, (hq + hkv) * d:].reshape(-1, hkv, d)
+        attn = torch.empty_like(q)
+        for b, c in enumerate(chunks):
+            p = c.start
+            kc = cache.k[layer][tables[b]].reshape(-1, hkv, d)[:p].float()
+            vc = cache.v[layer][tables[b]].reshape(-1, hkv, d)[:p].float()
+            kc = torch.cat([kc, k[b:b + 1]], 0).repeat_interleave(grp, dim=1)   # [p+1, Hq, D]
+            vc = torch.cat([vc, v[b:b + 1]], 0).repeat_interleave(grp, dim=1)
+            w = torch.softmax((kc * q[b][None]).sum(-1) / math.sqrt(d), dim=0)  # [p+1, Hq]
+            attn[b] = (w[..., None] * vc).sum(0)
+        x = x + attn.reshape(-1, hq * d) @ lw.w_o.float().t()
+        gu = rms(x, lw.post_norm) @ lw.w_gate_up.float().t()
+        g, u = gu.chunk(2, dim=-1)
+        x = x + (torch.nn.functional.silu(g) * u) @ lw.w_down.float().t()
+    return rms(x, model.final_norm) @ model.lm_head.float().t()
+
+
+def _near(got_rows, ref, what):
+    g = torch.stack(list(got_rows)).double().cpu() if not torch.is_tensor(got_rows) \
+        else got_rows.double().cpu()
+    e = ref.double().cpu()
+    scale = e.abs().max().item()
+    err = (g - e).abs()
+    print(f"{what}: max err {err.max().item():.3e} mean {err.mean().item():.3e} "
+          f"(max |logit| {scale:.3f})", flush=True)
+    assert err.max().item() <= DEEP_MAX_REL * scale, what
+    assert err.mean().item() <= DEEP_MEAN_REL * scale, what
+    top2 = e.topk(2, dim=-1).values
+    clear = (top2[:, 0] - top2[:, 1]) > 2 * DEEP_MAX_REL * scale
+    assert torch.equal(g.argmax(-1)[clear], e.argmax(-1)[clear]), what
+
+
+def test_c5_eager_b64_and_bucket8_replays_against_fp32(c5):
+    """Batch invariance at 64 rows: one eager decode_static step over all 64 rows
+    (library GEMMs + unfused layer kernels) and eight bucket-8 graph replays of the
+    same rows (fused projections), on the same cache state, each against a plain
+    PyTorch float32 decode step of the same model."""
+    model, cache, step, st = c5
+    chunks = [Chunk(f"r{b}", [st["tok"][b]], st["pos"][b]) for b in range(C5_ROWS)]
+    eager = _eager(model, cache, step, chunks)
+    rows = []
+    for i in range(0, C5_ROWS, 8):
+        out = step(chunks[i:i + 8])
+        assert out is not None
+        rows.extend(out)
+    ref = _fp32_decode_reference(model, cache, chunks)
+    _near(eager, ref, "C5 eager B=64 vs fp32")
+    _near(rows, ref, "C5 8 x bucket 8 vs fp32")
+    _near(rows, eager.float(), "C5 8 x bucket 8 vs eager B=64")

@@ -86,6 +86,36 @@ def test_c4_prefill_chunks_full():
     assert_attention_close(got, exp, what="C4 prefill")
 
 
+def test_c4_decode_rows_full():
+    """C4's 48 decode rows (L ~ U{256..4096}) in the same pool as the prefill chunks,
+    through the decode kernel, against the float64 oracle."""
+    w = workloads.c4_workload().decode
+    d = w.to(DEV)
+    got = ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens)
+    torch.cuda.synchronize()
+    exp = R.decode_reference(w.q.numpy(), w.k_pool.numpy(), w.v_pool.numpy(),
+                             w.block_tables.numpy(), w.context_lens.numpy(), 16)
+    assert_attention_close(got.cpu().numpy(), exp, what="C4 decode rows")
+
+
+def test_c4_whole_step_prefill_and_decode_share_the_pool():
+    """The whole C4 step as the benchmark runs it: the prefill launch over the four
+    chunks, then the decode launch over the 48 rows, back to back on one stream."""
+    w = workloads.c4_workload()
+    d = w.to(DEV)
+    pre = ops.prefill_paged(d.q, d.k_pool, d.v_pool, d.block_tables, d.q_offsets,
+                            d.context_lens, int(max(w.meta["n_new"])))
+    dd = d.decode
+    dec = ops.paged_decode(dd.q, d.k_pool, d.v_pool, dd.block_tables, dd.context_lens)
+    torch.cuda.synchronize()
+    exp_pre = R.prefill_reference(w.q.numpy(), w.q_offsets.numpy(), w.context_lens.numpy(),
+                                  w.k_pool.numpy(), w.v_pool.numpy(), w.block_tables.numpy(), 16)
+    exp_dec = R.decode_reference(w.decode.q.numpy(), w.k_pool.numpy(), w.v_pool.numpy(),
+                                 w.decode.block_tables.numpy(), w.decode.context_lens.numpy(), 16)
+    assert_attention_close(pre.cpu().numpy(), exp_pre, what="C4 step: prefill")
+    assert_attention_close(dec.cpu().numpy(), exp_dec, what="C4 step: decode rows")
+
+
 def test_per_request_interface_multi_token_chunk():
     """attention_for_request with Q > 1 takes the prefill kernel (the reference routes it to
     the materialized SDPA, test_triton_paged_attention.py:29-41); compare with the oracle."""

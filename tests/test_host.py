@@ -179,3 +179,170 @@ def test_device_tables_need_a_gpu_cache():
     cache.reserve("a", 6)
     with pytest.raises(RuntimeError, match="GPU"):
         cache.device_tables(["a"], 4)
+
+
+# --------------------------------------------------------------------------------------
+# cache internals of this package's own design
+# --------------------------------------------------------------------------------------
+
+def test_free_ring_reuses_blocks_in_release_order():
+    c = make_cache(6, 4)
+    c.reserve("a", 8)          # blocks 0, 1
+    c.reserve("b", 8)          # blocks 2, 3
+    c.free_request("b")        # ring: 4, 5, 2, 3
+    c.free_request("a")        # ring: 4, 5, 2, 3, 0, 1
+    assert list(c.free) == [4, 5, 2, 3, 0, 1]
+    c.reserve("c", 12)
+    assert c.tables["c"] == [4, 5, 2]
+    assert 3 in c.free and 4 not in c.free and 99 not in c.free
+    c.assert_invariants()
+
+
+def test_refs_are_read_only_and_count_pins():
+    c = make_cache()
+    c.reserve("a", 8)
+    b = c.tables["a"][1]
+    c.retain_block(b)
+    c.retain_block(b)
+    assert c.refs[b] == 3
+    with pytest.raises(ValueError):
+        c.refs[b] = 0
+    with pytest.raises(ValueError):
+        c.release_block(c.tables["a"][0])          # no pin on that block
+    with pytest.raises(ValueError):
+        c.retain_block(9)                          # free block
+    with pytest.raises(ValueError):
+        c.retain_block(-1)
+    c.free_request("a")
+    assert c.refs[b] == 2 and b not in c.free and c.free_blocks == 9
+    c.release_block(b)
+    c.release_block(b)
+    assert b in c.free and c.free_blocks == 10
+    c.assert_invariants()
+
+
+def test_table_reorder_only_accepts_a_permutation_of_the_own_blocks():
+    c = make_cache(12, 4)
+    c.reserve("a", 12)
+    c.reserve("b", 4)
+    c.tables["a"] = list(reversed(c.tables["a"]))
+    assert c.tables["a"] == [2, 1, 0]
+    with pytest.raises(ValueError):
+        c.tables["a"] = [2, 1, 3]          # 3 belongs to b
+    with pytest.raises(ValueError):
+        c.tables["a"] = [2, 1]
+    assert c.tables["a"] == [2, 1, 0]
+    c.assert_invariants()
+
+
+def test_shared_block_write_is_refused_before_any_device_work():
+    """tests/unit/test_prefix_cache.py:85: a request never writes a block it shares."""
+    c = make_cache(12, 4)
+    c.reserve("src", 8)
+    c.attach_prefix("child", c.tables["src"])
+    c.reserve("child", 9)
+    with pytest.raises(RuntimeError, match="shared immutable"):
+        c.write(0, "child", 0, torch.zeros(1, 2, 8, dtype=torch.float16),
+                torch.zeros(1, 2, 8, dtype=torch.float16))
+    with pytest.raises(ValueError):
+        c.attach_prefix("x", [0, 0])
+    with pytest.raises(ValueError):
+        c.attach_prefix("y", [11])                  # never allocated
+    with pytest.raises(ValueError):
+        c.attach_prefix("child", [0])               # already has a table
+    c.assert_invariants()
+
+
+def test_page_table_matrix_grows_and_rows_are_reused():
+    c = make_cache(400, 1)
+    for i in range(40):                              # more rows than the first matrix
+        c.reserve(f"r{i}", 3)
+    c.reserve("r0", 100)                             # wider than the first matrix
+    assert len(c.tables["r0"]) == 100 and c.tables["r1"] == [3, 4, 5]
+    c.free_request("r5")
+    c.reserve("new", 2)
+    assert len(c.tables) == 40 and "r5" not in c.tables and "new" in c.tables
+    assert c.available_slots("r5") == 0 and c.missing_blocks("new", 5) == 3
+    t = c.block_table(["new", "r1"], width=4, pad_block=7)
+    assert t.tolist() == [c.tables["new"] + [7, 7], [3, 4, 5, 7]]
+    c.assert_invariants()
+
+
+# --------------------------------------------------------------------------------------
+# graph records own the workspaces their kernels recorded
+# --------------------------------------------------------------------------------------
+
+class _EagerRecorder(DecodeGraphManager):
+    """Stands in for hipGraph capture on the CPU: the 'graph' re-runs decode on the
+    staging tensors into the captured output, as a replayed graph would."""
+
+    def eligible(self, active_count):
+        return self.bucket_for(active_count) is not None
+
+    def _record(self, decode, staging, mask):
+        decode(**staging, active_mask=mask)                # warm-up
+        out = decode(**staging, active_mask=mask)
+
+        class _Rerun:
+            def replay(self):
+                out.copy_(decode(**staging, active_mask=mask))
+        return _Rerun(), out, 0
+
+
+def test_graph_records_keep_their_workspaces_when_the_library_replaces_them():
+    from flexengine_amd import ops
+    cpu = torch.device("cpu")
+    recorded = {}
+
+    def decode(input_ids, active_mask):
+        rows = input_ids.shape[0]
+        ws = ops.decode_workspace(cpu, rows << 20, kind="test-graph")
+        ws[0] = rows
+        recorded.setdefault(rows, ws.data_ptr())
+        return (input_ids.float() + ws[0].float()) * active_mask
+
+    m = _EagerRecorder(device="cpu")
+    m.capture(1, decode, {"input_ids": torch.ones(1, 1)})
+    # an eager batch of 16 rows replaces the per-device workspace with a larger one
+    decode(torch.ones(16, 1), torch.ones(16, 1))
+    m.capture(8, decode, {"input_ids": torch.ones(8, 1)})
+    held1 = [t.data_ptr() for t in m.workspaces(1)]
+    held8 = [t.data_ptr() for t in m.workspaces(8)]
+    assert recorded[1] in held1                  # bucket 1's buffer is still owned
+    assert recorded[1] != recorded[16] and recorded[16] in held8
+    import gc
+    gc.collect()
+    assert [t.data_ptr() for t in m.workspaces(1)] == held1
+    out = m.replay(1, {"input_ids": torch.tensor([[5.0]])})
+    assert out.tolist() == [[6.0]]
+    out = m.replay(5, {"input_ids": torch.arange(1.0, 6.0).reshape(5, 1)})
+    assert out.tolist() == [[9.0], [10.0], [11.0], [12.0], [13.0]]   # + bucket rows (8)
+    st = m.stats()
+    assert st["captures"] == 2 and st["replays"] == 2 and st["padded_slots"] == 3
+
+
+def test_replay_pads_with_zeros_and_a_zero_mask():
+    m = _EagerRecorder(device="cpu")
+
+    def decode(input_ids, positions, active_mask):
+        return (input_ids.float() + positions.float()) * active_mask
+
+    m.capture(4, decode, {"input_ids": torch.ones(4, 1, dtype=torch.long),
+                          "positions": torch.ones(4, 1, dtype=torch.long)})
+    addrs = m.staging_addresses(4)
+    got = m.replay(3, {"input_ids": torch.tensor([[3], [7], [11]]),
+                       "positions": torch.tensor([[2], [4], [6]])})
+    assert got.tolist() == [[5.0], [11.0], [17.0]]
+    assert m.staging_addresses(4) == addrs
+    assert m._graphs[4].staging["input_ids"][3].item() == 0
+    assert m._graphs[4].mask.reshape(-1).tolist() == [1.0, 1.0, 1.0, 0.0]
+    with pytest.raises(ValueError):
+        m.replay(3, {"input_ids": torch.zeros(3, 1, dtype=torch.long)})
+    with pytest.raises(ValueError):
+        m.replay(2, {"input_ids": torch.zeros(3, 1, dtype=torch.long),
+                     "positions": torch.zeros(3, 1, dtype=torch.long)})
+    with pytest.raises(ValueError):
+        m.replay(1, {"input_ids": torch.zeros(1, 1, dtype=torch.long),
+                     "positions": torch.zeros(1, 1, dtype=torch.long)})   # bucket 1 not captured
+    with pytest.raises(ValueError):
+        m.capture(3, decode, {"input_ids": torch.ones(3, 1)})             # not a bucket
