@@ -19,6 +19,9 @@ FE_OK = 0
 FE_ERR_INVALID_ARGUMENT = -1
 FE_ERR_UNSUPPORTED = -2
 FE_ERR_WORKSPACE = -3
+FE_ERR_SCRATCH_LIMIT = -4
+# FE_PAGED_DECODE_NOALLOC_SCRATCH_BYTES of include/flexengine_amd.h
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -38,6 +41,8 @@ SIGNATURES: dict[str, tuple] = {
     "fe_paged_decode_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
     "fe_paged_decode": (_i, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i, _p, _i, _p, _p, _sz,
                              _i, _i, _i, _i, _i, _f, _i, _p]),
+    "fe_paged_decode_noalloc": (_i, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i, _p, _i, _p,
+                                     _i, _i, _i, _i, _i, _f, _i, _p]),
     "fe_paged_decode_shared_prefix_workspace_size": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "fe_paged_decode_shared_prefix": (_i, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i, _p, _i, _p,
                                            _p, _p, _i, _p, _sz, _i, _i, _i, _i, _i, _f, _i, _p]),

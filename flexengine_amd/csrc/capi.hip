@@ -16,6 +16,9 @@ extern "C" const char* fe_error_string(int code) {
              "block_size a power of two)";
     case FE_ERR_WORKSPACE:
       return "workspace missing, misaligned or smaller than fe_paged_decode_workspace_size()";
+    case FE_ERR_SCRATCH_LIMIT:
+      return "the call needs more scratch than the 16 MiB fe_paged_decode_noalloc holds per "
+             "GPU; call fe_paged_decode with a workspace instead";
     default:
       break;
   }

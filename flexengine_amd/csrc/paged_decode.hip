@@ -28,6 +28,8 @@
 // columns), so every K/V byte is read from HBM once per step; the reference's
 // Triton kernel reads it G times, once per query head
 // (src/flexengine/inference/kernels/paged_attention.py:99-139).
+#include <mutex>
+
 #include "attn_core.h"
 
 using namespace fe;
@@ -1330,6 +1332,93 @@ extern "C" int fe_paged_decode_shared_prefix(
                      num_blocks, block_tables, table_stride, context_lens, workspace,
                      workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
                      target_splits, &c, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode (fe_paged_decode_noalloc)
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// fe_paged_decode_noalloc's split-K tickets and partials: one copy of this
+// array per GPU, zero-initialised when the code object is loaded and held
+// until the process ends.  Host code never uses the name itself (on the host
+// it is a stand-in, not a device address): the device address comes from
+// hipGetSymbolAddress, once per device.
+static __device__ __align__(256) char scratch[FE_PAGED_DECODE_NOALLOC_SCRATCH_BYTES];
+
+__global__ void clear_words_kernel(int* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+struct ScratchTable {
+  std::mutex mu;
+  void* ptr[64] = {};
+};
+ScratchTable& scratch_table() {
+  static ScratchTable t;
+  return t;
+}
+
+// Device address of the current device's scratch.  The first call on a device
+// looks it up and clears the ticket region with a fill kernel on `stream` (a
+// kernel rather than hipMemsetAsync, so a first call under graph capture
+// records a kernel node); every later call finds the tickets at zero because
+// each decode leaves them so.
+int scratch_for_current_device(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= 64) return FE_ERR_UNSUPPORTED;
+  ScratchTable& t = scratch_table();
+  std::lock_guard<std::mutex> lock(t.mu);
+  if (t.ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr || !aligned16(p)) return (int)hipErrorInvalidSymbol;
+    hipLaunchKernelGGL(clear_words_kernel, dim3(64), dim3(256), 0, stream, (int*)p,
+                       (int)(kTicketBytes / sizeof(int)));
+    const int rc = FE_LAUNCH_STATUS();
+    if (rc != FE_OK) return rc;
+    t.ptr[dev] = p;
+  }
+  *out = t.ptr[dev];
+  return FE_OK;
+}
+
+}  // namespace
+
+extern "C" int fe_paged_decode_noalloc(const void* q, int64_t q_batch_stride, void* out,
+                                       const void* k_new, const void* v_new,
+                                       int64_t new_batch_stride, void* k_pool, void* v_pool,
+                                       int num_blocks, const int32_t* block_tables,
+                                       int table_stride, const int32_t* context_lens, int batch,
+                                       int num_q_heads, int kv_heads, int head_dim,
+                                       int block_size, float scale, int target_splits,
+                                       fe_stream_t stream) {
+  // the scratch the call would need, checked before anything is launched
+  // (decode_impl validates the remaining arguments the same way as for
+  // fe_paged_decode)
+  if (batch > 0 && num_q_heads > 0 && kv_heads > 0 && head_dim > 0 && table_stride > 0 &&
+      block_size > 0 && target_splits >= 0 &&
+      (int64_t)table_stride * block_size <= 262144) {
+    const int max_len = table_stride * block_size;
+    const int target = effective_target(batch, kv_heads, max_len, target_splits);
+    if (fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, max_len, target) >
+        (size_t)FE_PAGED_DECODE_NOALLOC_SCRATCH_BYTES)
+      return FE_ERR_SCRATCH_LIMIT;
+  }
+  void* ws = nullptr;
+  if (batch > 0) {
+    const int rc = scratch_for_current_device((hipStream_t)stream, &ws);
+    if (rc != FE_OK) return rc;
+  }
+  return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
+                     num_blocks, block_tables, table_stride, context_lens, ws,
+                     (size_t)FE_PAGED_DECODE_NOALLOC_SCRATCH_BYTES, batch, num_q_heads,
+                     kv_heads, head_dim, block_size, scale, target_splits, nullptr,
+                     (hipStream_t)stream);
 }
 
 extern "C" int fe_lse_merge(const float* part_out, const float* part_lse, int num_splits,

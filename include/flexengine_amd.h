@@ -42,6 +42,10 @@ typedef struct ihipStream_t* fe_stream_t;
 #define FE_ERR_INVALID_ARGUMENT (-1)  /* null pointer, bad size, misalignment */
 #define FE_ERR_UNSUPPORTED (-2)       /* head_dim / group size / block size not built */
 #define FE_ERR_WORKSPACE (-3)         /* workspace missing or smaller than required */
+#define FE_ERR_SCRATCH_LIMIT (-4)     /* more scratch than fe_paged_decode_noalloc holds */
+
+/* Bytes of the static per-GPU scratch array of fe_paged_decode_noalloc. */
+#define FE_PAGED_DECODE_NOALLOC_SCRATCH_BYTES (16u << 20)
 
 /* Library version (major*10000 + minor*100 + patch). */
 int fe_version(void);
@@ -178,6 +182,33 @@ int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
                     int batch, int num_q_heads, int kv_heads, int head_dim,
                     int block_size, float scale, int target_splits,
                     fe_stream_t stream);
+
+/*
+ * fe_paged_decode without a workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  No counterpart in the reference.
+ * Same arguments (minus workspace / workspace_bytes), kernels and results as
+ * fe_paged_decode; the split-K tickets and partials live in a static device
+ * array of FE_PAGED_DECODE_NOALLOC_SCRATCH_BYTES (16 MiB) that each GPU the
+ * library runs on holds until the process ends.  The call allocates nothing
+ * (no hipMalloc / hipFree); the first call on a device looks up that
+ * device's array and clears its split counters with a kernel on `stream`.
+ * A call needing more scratch than the array holds -- what
+ * fe_paged_decode_workspace_size reports for the same arguments -- returns
+ * FE_ERR_SCRATCH_LIMIT before launching anything (C2-sized batches need
+ * about 4 MiB).  Every call on one GPU shares that GPU's array and leaves the
+ * last call's partials in it: calls that overlap in time on one GPU (several
+ * streams, or host threads without ordering) race and must not be issued.
+ * The current device must be the device of `stream` and of the pointers.
+ */
+int fe_paged_decode_noalloc(const void* q, int64_t q_batch_stride, void* out,
+                            const void* k_new, const void* v_new, int64_t new_batch_stride,
+                            void* k_pool, void* v_pool, int num_blocks,
+                            const int32_t* block_tables, int table_stride,
+                            const int32_t* context_lens,
+                            int batch, int num_q_heads, int kv_heads, int head_dim,
+                            int block_size, float scale, int target_splits,
+                            fe_stream_t stream);
 
 /*
  * Bytes of device workspace fe_paged_decode_shared_prefix needs; zero-filled
