@@ -81,11 +81,14 @@ struct PrefillArgs {
   const int32_t* tables;
   const int32_t* q_off;
   const int32_t* ctx;
-  float* part_o;     // [KS][total_q * Hq][D] normalised partial outputs (KS > 1)
+  float* part_o;     // [KS][total_q * Hq][D] normalised partial outputs (KS > 1); the
+                     // stream-K kernel's partials [2 * nwg_max * 128][D]
   float* part_lse;   // [KS][total_q * Hq] base-2 LSE of each partial
+  struct MergeDesc* merge;  // stream-K kernel: [nwg_max] split units to merge
   int* tickets;      // [row blocks * Hkv], zero between calls
   int64_t q_stride;  // elements from one query row (token or sequence) to the next
   int W, S, total_q, Hq, Hkv, G, BS, bs_log2, NB, KS;
+  int nwg_max;       // stream-K kernel: workgroups of the launch
   float scale_log2;
   // shared-prefix (cascade) mode: "sequence" s is a group of decode rows
   // q_off[s] .. q_off[s+1]-1 sharing the first prefix_len[s] keys of row
@@ -516,6 +519,762 @@ void prefill_kernel(const PrefillArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// prefill_dma_kernel: 32 rows per wave, 64-key blocks staged by buffer->LDS DMA
+// ---------------------------------------------------------------------------
+//
+// Used for block sizes that are multiples of 16 (every 16-key run of a block
+// lies in one page).  Differences from prefill_kernel:
+//
+// * Each wave owns 32 rows (two 16-row MFMA tiles), a workgroup 128 rows, so
+//   every K/V fragment read from LDS feeds two MFMAs: 32 flops per LDS byte
+//   (one tile per wave, as in prefill_kernel, is 16 flops per byte, which caps
+//   the MFMA pipes at about half of their peak on LDS bandwidth alone).
+// * Keys come in blocks of 64.  Wave w stages keys 16w .. 16w+15 of a block --
+//   one run of one page -- with buffer_load_dwordx4 ... lds: one scalar buffer
+//   descriptor per run (its range ends at the last key the row block reads, so
+//   later keys arrive as zeros; the causal mask covers them), loop-invariant
+//   lane offsets, and no registers or address arithmetic per staged byte.  The
+//   next block's DMA runs while the current block is computed.
+// * LDS rows are not padded (a DMA instruction fills 1 KiB contiguously); bank
+//   conflicts are avoided by XOR-swizzling the 16-byte chunks of each row (see
+//   swz_k / swz_v): the QK^T operand read puts consecutive lanes on consecutive
+//   key rows of one chunk, a transposing V read puts each 16-lane group on 4
+//   consecutive rows x 32 bytes.
+// * Row sums come from the PV MFMA: a tile of ones as the V^T operand gives
+//   sum_k P[row][k] in every element, from the same fp16 probabilities the
+//   output uses, and takes the place of a VALU add per score.
+
+constexpr int kDmaKeys = 64;                       // keys per staged block
+constexpr int kDmaRows = 128;                      // rows per workgroup
+// RT 16-row MFMA tiles per wave, 8 / RT waves per workgroup: RT = 2 feeds two
+// MFMAs from every K/V fragment read from LDS (VGPRs allow 2 waves per SIMD),
+// RT = 1 one (4 waves per SIMD)
+template <int RT>
+struct DWaves {
+  static constexpr int NW = kDmaRows / (16 * RT);
+  static constexpr int THREADS = NW * kWave;
+};
+
+template <int D>
+struct DCfg {
+  static constexpr int NC = D / 32;          // 32-dim k-chunks of QK^T
+  static constexpr int NX = D / 16;          // 16-dim output tiles
+  static constexpr int ROWB = D * 2;         // LDS bytes per staged key row
+  static constexpr int MAT = kDmaKeys * ROWB;
+  static constexpr int STAGE = 2 * MAT;      // K rows, then V rows
+  static constexpr int CPR = D / 8;          // 16-byte chunks per row
+  static constexpr int RPI = kWave / CPR;    // rows per DMA instruction
+  static constexpr int NI = 16 / RPI;        // DMA instructions per 16-key run and matrix
+};
+
+// Chunk swizzles of staged key row r.  gfx950's LDS serves 256 bytes per clock
+// (64 banks of 4 bytes): 16 lanes of a 16-byte read, 32 lanes of an 8-byte read.
+// K (16 consecutive rows, one chunk each): D = 128 rows are 256 bytes, so
+// chunk c goes to slot c ^ (r & 15); D = 64 rows are 128 bytes, row parity
+// already picks the half of the 256 bytes, so slot c ^ ((r >> 1) & 7).
+// V (transposing reads: 8 consecutive rows x 32 bytes per 32 lanes): 32-byte
+// pairs of chunks move together, slot c ^ ((r & 7) << 1) for D = 128 and
+// c ^ (((r >> 1) & 3) << 1) for D = 64.  The D = 128 forms are also
+// conflict-free with 32 banks (8 and 16 lanes per clock).
+template <int D>
+__device__ __forceinline__ int swz_k(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+template <int D>
+__device__ __forceinline__ int swz_v(int r) { return D == 128 ? ((r & 7) << 1) : (((r >> 1) & 3) << 1); }
+
+// Row maxima of scores (finite or -inf, never NaN): v_max3_f32 straight from the
+// MFMA results (fmaxf would first canonicalise every operand, one v_max_f32
+// x, x, x each, under the IEEE mode), and the cross-lane steps with gfx950's
+// permlane swaps (VALU, no LDS round trip).  Each swap returns both halves and
+// both are used: permlane32_swap(x, x) gives lane l the values of lanes l % 32
+// and l % 32 + 32, permlane16_swap(x, x) those of the two 16-lane rows l / 16
+// pairs with.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float vmax2(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max_over_lane_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = vmax2(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return vmax2(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+// max of the 16 values sv[4][4]
+__device__ __forceinline__ float max16(const float (&v)[4][4]) {
+  const float a = vmax3(v[0][0], v[0][1], v[0][2]);
+  const float b = vmax3(v[0][3], v[1][0], v[1][1]);
+  const float c = vmax3(v[1][2], v[1][3], v[2][0]);
+  const float d = vmax3(v[2][1], v[2][2], v[2][3]);
+  const float e = vmax3(v[3][0], v[3][1], v[3][2]);
+  return vmax2(vmax3(a, b, c), vmax3(d, e, v[3][3]));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(4))) const int32_t const_i32;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t run_rsrc(const f16* base, uint32_t bytes) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)addr);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32));
+  void* p = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, (int)__builtin_amdgcn_readfirstlane(bytes),
+                                           0x00020000);
+}
+
+// DMA of one wave's 16-key run of block kb (first key t0) into the K and V
+// stages: one buffer descriptor per matrix whose range ends at the run's last
+// key before key_end (later rows arrive as zeros).
+template <int D>
+__device__ __forceinline__ void dma_run(const PrefillArgs& a, int h, int w, int t0, int key_end,
+                                        int id, const uint32_t (&voff_k)[DCfg<D>::NI],
+                                        const uint32_t (&voff_v)[DCfg<D>::NI],
+                                        unsigned char* kst, unsigned char* vst) {
+  using P = DCfg<D>;
+  const int rs = a.Hkv * D * 2;
+  int nv = key_end - t0;
+  nv = nv < 0 ? 0 : (nv > 16 ? 16 : nv);
+  const uint32_t nrec = nv > 0 ? (uint32_t)((nv - 1) * rs + D * 2) : 0u;
+  const int64_t row0 = (int64_t)id * a.BS + (t0 & (a.BS - 1));
+  const int64_t off = row0 * a.Hkv * D + h * D;
+  const __amdgpu_buffer_rsrc_t rk = run_rsrc(a.k_pool + off, nrec);
+  const __amdgpu_buffer_rsrc_t rv = run_rsrc(a.v_pool + off, nrec);
+  unsigned char* kl = kst + 16 * w * P::ROWB;
+  unsigned char* vl = vst + 16 * w * P::ROWB;
+#pragma unroll
+  for (int i = 0; i < P::NI; ++i) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(kl + i * P::RPI * P::ROWB), 16,
+                                             voff_k[i], 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(vl + i * P::RPI * P::ROWB), 16,
+                                             voff_v[i], 0, 0, 0);
+  }
+}
+
+// ---- stream-K work split -------------------------------------------------
+//
+// Units are (sequence, KV head, 128-row block) in that order; unit u has nb_u
+// key blocks of 64 (through its last row's position).  The grid is a fixed
+// number of workgroups (two per CU); logical workgroup g takes blocks
+// [g*T/NWG, (g+1)*T/NWG) of the concatenated key blocks of all units (T in
+// total), so every workgroup gets the same number of blocks whatever the mix
+// of context lengths.  A unit covered by one workgroup is written directly; a
+// unit split between workgroups gets a normalised fp32 partial and base-2 LSE
+// from each contributor (slot 2g, or 2g + 1 for the last unit of a range that
+// started in an earlier one), and a second launch merges them.  The launch
+// boundary orders the partials' stores before the merge's loads, so no
+// counter, fence or cache-bypassing access is involved.
+//
+// Key blocks per row block, in closed form: a row block whose last row is y
+// (row = position * G + head) reads keys up to c + y / G, so it has
+// floor((G * (c + 64) + y) / (64 * G)) blocks of 64 (c cached tokens), and
+// the row blocks 0 .. R-2 of a sequence (all but the last, whose y is cut at
+// the sequence's last row) have floor_sum(R - 1, 64G, 128, G * (c + 64) + 127)
+// blocks together.
+
+// sum_{i < n} floor((a * i + b) / m) (the Euclidean-like reduction).  The
+// divisions are 32-bit: fe_prefill_paged accepts sizes with a * n + b < 2^29
+// on the first call, and y = a * n + b does not grow from one step to the
+// next (a < m after the first reduction, b < m).
+__device__ __forceinline__ int64_t floor_sum(uint32_t n, uint32_t m, uint32_t a, uint32_t b) {
+  int64_t ans = 0;
+  while (true) {
+    if (a >= m) {
+      ans += (int64_t)((uint64_t)n * (n - 1) / 2) * (a / m);
+      a %= m;
+    }
+    if (b >= m) {
+      ans += (int64_t)n * (b / m);
+      b %= m;
+    }
+    const uint32_t y = a * n + b;
+    if (y < m) break;
+    n = y / m;
+    b = y % m;
+    const uint32_t t = m;
+    m = a;
+    a = t;
+  }
+  return ans;
+}
+
+// A sequence as the work split sees it.
+struct SeqWork {
+  int q0;      // first query row in q / out
+  int n;       // new tokens (positions)
+  int cached;  // keys before the first new token
+  int R;       // 128-row blocks
+  int tb;      // key blocks of all row blocks of one KV head
+};
+
+__device__ __forceinline__ SeqWork seq_work(const PrefillArgs& a, int s) {
+  SeqWork w;
+  w.q0 = min(max(a.q_off[s], 0), a.total_q);
+  w.n = min(a.q_off[s + 1], a.total_q) - w.q0;
+  w.n = w.n > 0 ? w.n : 0;
+  const int ctx = min(clamp_len(a.ctx[s]), a.W * a.BS);  // what the table addresses
+  w.cached = ctx >= w.n ? ctx - w.n : 0;
+  w.R = (w.n * a.G + kDmaRows - 1) / kDmaRows;
+  w.tb = 0;
+  if (w.R > 0) {
+    const uint32_t G = (uint32_t)a.G, m = (uint32_t)kDmaKeys * G;
+    const uint32_t b = G * (uint32_t)(w.cached + kDmaKeys) + kDmaRows - 1;
+    w.tb = (int)(floor_sum((uint32_t)(w.R - 1), m, kDmaRows, b) +
+                 (G * (uint32_t)(w.cached + kDmaKeys) + (uint32_t)(w.n * a.G) - 1) / m);
+  }
+  return w;
+}
+
+// key blocks of row block rb of a sequence
+__device__ __forceinline__ int rb_blocks(const PrefillArgs& a, const SeqWork& w, int rb) {
+  const int y = min(kDmaRows * (rb + 1), w.n * a.G) - 1;
+  return (a.G * (w.cached + kDmaKeys) + y) / (kDmaKeys * a.G);
+}
+
+// Where block x of the concatenation lies: sequence s, head h, row block rb
+// and block kb of that unit.  Every wave computes it (wave-parallel over
+// sequences and row blocks, results uniform).
+struct StreamPos {
+  int s, h, rb, kb;
+  SeqWork w;
+};
+// The ranges of the nwg workgroups: [start(g), start(g + 1)) with start(g) =
+// floor(g * T / nwg), in 32-bit arithmetic (fe_prefill_paged keeps T < 2^31
+// and nwg < 2^13, so g * q < T and g * r < nwg^2).
+struct Ranges {
+  int T, nwg, q, r;  // T = q * nwg + r
+  __device__ __forceinline__ int start(int g) const { return g * q + (g * r) / nwg; }
+  // the workgroup whose range holds block x (0 <= x < T): a float estimate
+  // within one of the answer, then exact steps
+  __device__ __forceinline__ int owner(int x) const {
+    int g = (int)((float)x * (float)nwg / (float)T);
+    g = min(max(g, 0), nwg - 1);
+    while (g + 1 < nwg && start(g + 1) <= x) ++g;
+    while (g > 0 && start(g) > x) --g;
+    return g;
+  }
+};
+
+// The split every workgroup of the two launches derives from the sizes: the
+// ranges (T key blocks in all, nwg workgroups, a multiple of 8 from 8 on) and
+// this lane's sequence of the first 64 (kept for stream_locate).
+struct StreamPlan {
+  Ranges rg;
+  SeqWork w0;
+};
+
+// Contributors of one split unit at most kMaxContrib: ranges of at least
+// ceil(nb_max / (kMaxContrib - 2)) blocks, so a unit of nb_max blocks meets at
+// most kMaxContrib - 1 of them.
+constexpr int kMaxContrib = 32;
+
+__device__ __forceinline__ StreamPlan stream_plan(const PrefillArgs& a) {
+  const int lane = lane_id();
+  StreamPlan p;
+  int T = 0;
+  p.w0 = SeqWork{};
+  int nb_max = 0;
+  for (int base = 0; base < a.S; base += kWave) {
+    int blocks = 0, most = 0;
+    if (base + lane < a.S) {
+      const SeqWork w = seq_work(a, base + lane);
+      if (base == 0) p.w0 = w;
+      blocks = w.tb * a.Hkv;
+      if (w.R > 0) most = rb_blocks(a, w, w.R - 1);  // the last row block reads the most keys
+    }
+    T += wave_sum_i(blocks);
+    nb_max = max(nb_max, wave_max_i(most));
+  }
+  const int min_range = max((nb_max + kMaxContrib - 3) / (kMaxContrib - 2), 1);
+  int nwg = max(1, min(a.nwg_max, T / min_range));
+  nwg = nwg >= 8 ? nwg & ~7 : nwg;
+  p.rg = Ranges{T, nwg, T / nwg, T % nwg};
+  return p;
+}
+
+// Logical workgroup of workgroup g < nwg: the dispatcher deals workgroups to
+// the 8 XCDs in turn (g % 8), so logical ranges (g % 8) * nwg / 8 + g / 8 put
+// consecutive key blocks -- the same sequence and KV head, mostly -- on one
+// XCD and its L2.
+__device__ __forceinline__ int logical_wg(int g, int nwg) {
+  return nwg >= 8 ? (g & 7) * (nwg >> 3) + (g >> 3) : g;
+}
+
+__device__ __forceinline__ bool stream_locate(const PrefillArgs& a, const SeqWork& w0, int x,
+                                              StreamPos& p) {
+  const int lane = lane_id();
+  int bcarry = 0;
+  for (int base = 0; base < a.S; base += kWave) {
+    const int s = base + lane;
+    SeqWork w{};
+    if (base == 0) w = w0;
+    else if (s < a.S) w = seq_work(a, s);
+    const int blocks = w.tb * a.Hkv;
+    const int incl = wave_scan_incl_i(blocks);
+    const int lo = bcarry + incl - blocks;
+    const unsigned long long hit = __ballot(s < a.S && blocks > 0 && x >= lo && x < lo + blocks);
+    if (hit) {
+      const int src = __builtin_ctzll(hit);
+      p.s = base + src;
+      p.w.q0 = readlane_i(w.q0, src);
+      p.w.n = readlane_i(w.n, src);
+      p.w.cached = readlane_i(w.cached, src);
+      p.w.R = readlane_i(w.R, src);
+      p.w.tb = readlane_i(w.tb, src);
+      const int o = x - (bcarry + readlane_i(incl - blocks, src));
+      p.h = o / p.w.tb;
+      const int o2 = o - p.h * p.w.tb;
+      // row block: scan of the row blocks' key blocks, 64 row blocks at a time
+      // (one division per lane and chunk)
+      int rcarry = 0;
+      for (int rb0 = 0; rb0 < p.w.R; rb0 += kWave) {
+        const int rb = rb0 + lane;
+        const int nbl = rb < p.w.R ? rb_blocks(a, p.w, rb) : 0;
+        const int rincl = wave_scan_incl_i(nbl);
+        const int rlo = rcarry + rincl - nbl;
+        const unsigned long long rhit = __ballot(nbl > 0 && o2 >= rlo && o2 < rlo + nbl);
+        if (rhit) {
+          const int rsrc = __builtin_ctzll(rhit);
+          p.rb = rb0 + rsrc;
+          p.kb = o2 - readlane_i(rlo, rsrc);
+          return true;
+        }
+        rcarry += readlane_i(rincl, kWave - 1);
+      }
+      return false;
+    }
+    bcarry += readlane_i(incl, kWave - 1);
+  }
+  return false;
+}
+
+
+// What the merge launch needs of a split unit, written by the unit's first
+// contributor g (the unit starts in g's range and runs past its end; a range
+// starts at most one such unit, its last) into entry blockIdx.x of
+// PrefillArgs::merge; cnt = 0 where workgroup blockIdx.x has none.  The
+// contributors are g .. g + cnt - 1; the unit is the first unit of every
+// range after g's, so their slots are 2 (g + k), and g's slot is `slot0`.
+struct MergeDesc {
+  int cnt, slot0, q0, h;  // contributors, g's partial slot, first query row, KV head
+  int r0, r_end, pad0, pad1;  // the unit's rows [r0, r_end) (row = position * G + head)
+};
+
+// Merge launch, after the stream-K launch on the same stream (whose partials
+// and descriptors it therefore reads with plain loads).  The split units are
+// the descriptors with cnt >= 2, in descriptor order; task j is quarter j % 4
+// (32 rows) of split unit j / 4, and workgroup b takes tasks b, b + grid, ...
+// so the merge spreads over the whole grid however few units are split.  Per
+// task the rows' weights go to LDS, then items (row, 4 dims) go to consecutive
+// threads, which sum the contributors' partials MAXK at a time with all their
+// loads in flight.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeRows = 32;                       // rows per task
+constexpr int kMergeParts = kDmaRows / kMergeRows;   // tasks per split unit
+constexpr int kMergeGrid = 2;  // merge workgroups per stream-K workgroup: one task each in
+                               // the usual case (at most one split unit per range)
+constexpr int kMergeDescPerThread = 4;  // descriptors a thread counts (nwg_max <= 1024)
+
+template <int D>
+__global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(const PrefillArgs a) {
+  constexpr int TPR = D / 4;                                // items per row
+  constexpr int PER = kMergeRows * TPR / kMergeThreads;     // items per thread
+  constexpr int MAXK = 4;
+  constexpr int NWAVE = kMergeThreads / kWave;
+  constexpr int DPT = kMergeDescPerThread;
+  __shared__ float wts[kMergeRows][kMaxContrib];
+  __shared__ int wave_total[NWAVE];
+  __shared__ int task_desc;
+  // ---- the split units: thread t holds descriptors t, t + 256, ... (loads in flight together) ----
+  const int ndesc = a.nwg_max;
+  bool split[DPT];
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int i = threadIdx.x + j * kMergeThreads;
+    split[j] = i < ndesc && a.merge[i].cnt >= 2;
+  }
+  // split units are numbered in the order (j, t): descriptor t + 256 j
+  const int w = threadIdx.x / kWave;
+  int excl[DPT], total = 0;
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int incl = wave_scan_incl_i(split[j] ? 1 : 0);
+    if (lane_id() == kWave - 1) wave_total[w] = incl;
+    __syncthreads();
+    int before = 0, sum = 0;
+#pragma unroll
+    for (int k = 0; k < NWAVE; ++k) {
+      before += k < w ? wave_total[k] : 0;
+      sum += wave_total[k];
+    }
+    excl[j] = total + before + incl - (split[j] ? 1 : 0);
+    total += sum;
+    __syncthreads();
+  }
+  const int G = a.G;
+  for (int task = blockIdx.x; task < total * kMergeParts; task += gridDim.x) {
+    const int u = task / kMergeParts, part = task % kMergeParts;
+#pragma unroll
+    for (int j = 0; j < DPT; ++j)
+      if (split[j] && excl[j] == u) task_desc = threadIdx.x + j * kMergeThreads;
+    __syncthreads();
+    const MergeDesc md = a.merge[task_desc];
+    __syncthreads();  // task_desc is read before the next task writes it
+    const int cnt = min(md.cnt, kMaxContrib);
+    const int r0 = md.r0 + part * kMergeRows;
+    const int nrows = min(md.r_end - r0, kMergeRows);
+    if (nrows <= 0) continue;  // uniform over the workgroup
+    const int prow0 = part * kMergeRows;
+    const int g0 = md.slot0 >> 1;
+    auto slot_of = [&](int k) __attribute__((always_inline)) {
+      return k == 0 ? md.slot0 : 2 * (g0 + k);
+    };
+    // weights: every (row, contributor) LSE load in flight, then one thread per
+    // row normalises exp2(lse_k - max) in LDS
+    for (int i = threadIdx.x; i < nrows * cnt; i += kMergeThreads) {
+      const int r = i / cnt, k = i - r * cnt;
+      wts[r][k] = a.part_lse[slot_of(k) * kDmaRows + prow0 + r];
+    }
+    __syncthreads();
+    for (int r = threadIdx.x; r < nrows; r += kMergeThreads) {
+      float* wr = wts[r];
+      float M = kNegInf;
+      for (int k = 0; k < cnt; ++k) M = fmaxf(M, wr[k]);
+      float den = 0.f;
+      for (int k = 0; k < cnt; ++k) den += wr[k] != kNegInf ? exp2f(wr[k] - M) : 0.f;
+      const float inv = den > 0.f ? 1.f / den : 0.f;
+      for (int k = 0; k < cnt; ++k) wr[k] = wr[k] != kNegInf ? exp2f(wr[k] - M) * inv : 0.f;
+    }
+    __syncthreads();
+    int row[PER], d4[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int it = threadIdx.x + i * kMergeThreads;
+      row[i] = min(it / TPR, nrows - 1);  // rows past nrows are computed and not stored
+      d4[i] = (it % TPR) * 4;
+    }
+    f32x4 num[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) num[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < cnt; c0 += MAXK) {
+      f32x4 ov[PER][MAXK];
+#pragma unroll
+      for (int k = 0; k < MAXK; ++k) {
+        const float* base =
+            a.part_o + ((int64_t)slot_of(min(c0 + k, cnt - 1)) * kDmaRows + prow0) * D;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+          ov[i][k] = *reinterpret_cast<const f32x4*>(base + row[i] * D + d4[i]);
+      }
+#pragma unroll
+      for (int k = 0; k < MAXK; ++k)
+        if (c0 + k < cnt) {
+#pragma unroll
+          for (int i = 0; i < PER; ++i) num[i] += wts[row[i]][c0 + k] * ov[i][k];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if ((int)(threadIdx.x + i * kMergeThreads) / TPR >= nrows) continue;
+      const int rr = r0 + row[i];
+      const int64_t orow = (int64_t)(md.q0 + rr / G) * a.Hq + md.h * G + rr % G;
+      *reinterpret_cast<f16x4*>(a.out + orow * D + d4[i]) =
+          f16x4{(f16)num[i][0], (f16)num[i][1], (f16)num[i][2], (f16)num[i][3]};
+    }
+    __syncthreads();  // wts is free for the next task
+  }
+}
+
+template <int D, int RT>
+__global__ __launch_bounds__(DWaves<RT>::THREADS) __attribute__((amdgpu_waves_per_eu(4 / RT, 4 / RT)))
+void prefill_dma_kernel(const PrefillArgs a) {
+  using P = DCfg<D>;
+  // K and V of two stages as four LDS objects: the compiler's wait for an LDS
+  // DMA before an LDS read is then limited to reads of the object it fills
+  __shared__ __align__(16) unsigned char k0[P::MAT];
+  __shared__ __align__(16) unsigned char v0[P::MAT];
+  __shared__ __align__(16) unsigned char k1[P::MAT];
+  __shared__ __align__(16) unsigned char v1[P::MAT];
+
+  // this workgroup's merge descriptor: empty unless its last unit is split and
+  // starts in its range
+  MergeDesc md{};
+  auto put_desc = [&]() __attribute__((always_inline)) {
+    if (threadIdx.x == 0) a.merge[blockIdx.x] = md;
+  };
+  const StreamPlan pl = stream_plan(a);
+  const int nwg = pl.rg.nwg;
+  if ((int)blockIdx.x >= nwg) return put_desc();
+  const int gid = logical_wg(blockIdx.x, nwg);
+  const int x_begin = pl.rg.start(gid);
+  const int x_end = pl.rg.start(gid + 1);
+  if (x_begin >= x_end) return put_desc();
+  StreamPos sp;
+  if (!stream_locate(a, pl.w0, x_begin, sp)) return put_desc();
+
+  const int G = a.G;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = lane_id();
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int rs = a.Hkv * D * 2;  // pool bytes from one key row to the next
+  uint32_t voff_k[P::NI], voff_v[P::NI];  // loop-invariant DMA lane offsets
+#pragma unroll
+  for (int i = 0; i < P::NI; ++i) {
+    const int r = P::RPI * i + lane / P::CPR;
+    const int sl = lane % P::CPR;
+    voff_k[i] = (uint32_t)(r * rs + (sl ^ swz_k<D>(r)) * 16);
+    voff_v[i] = (uint32_t)(r * rs + (sl ^ swz_v<D>(r)) * 16);
+  }
+  const bool dma_wave = w < kDmaKeys / 16;  // the 16-key runs of a block go to waves 0..3
+  int x = x_begin;
+  while (x < x_end) {
+    // ---- the unit at x and this workgroup's blocks of it ----
+    const int h = sp.h;
+    const int total_rows = sp.w.n * G;
+    const int cached = sp.w.cached;
+    const int r0 = sp.rb * kDmaRows;
+    const int r_last = min(r0 + kDmaRows, total_rows) - 1;
+    const int key_end = cached + r_last / G + 1;  // keys the row block reads
+    const int nb = rb_blocks(a, sp.w, sp.rb);
+    const int kb_lo = sp.kb;
+    const int kb_hi = min(nb, kb_lo + (x_end - x));
+    const int unit_start = x - kb_lo;
+    const bool split = kb_lo > 0 || kb_hi < nb;  // other workgroups hold blocks of the unit
+    if (kb_hi < nb && unit_start >= x_begin) {   // this range's last unit, merged later
+      md.cnt = pl.rg.owner(unit_start + nb - 1) - gid + 1;
+      md.slot0 = 2 * gid + (x_begin < unit_start ? 1 : 0);
+      md.q0 = sp.w.q0;
+      md.h = h;
+      md.r0 = r0;
+      md.r_end = r_last + 1;
+    }
+    const int wr0 = r0 + w * 16 * RT;             // first row of this wave
+    const bool has_rows = wr0 <= r_last;          // wave-uniform
+
+    // block ids of the wave's run for blocks kb_base .. kb_base + 63 (lane j:
+    // block kb_base + j), loaded before the rows' queries so that the first
+    // block's DMA waits for the ids only
+    const int32_t* trow = a.tables + (int64_t)sp.s * a.W;
+    auto load_ids = [&](int kb_base) __attribute__((always_inline)) {
+      int page = ((kb_base + lane) * kDmaKeys + 16 * w) >> a.bs_log2;
+      page = page < a.W ? page : a.W - 1;
+      return trow[page];
+    };
+    int kb_base = kb_lo;
+    int idv = load_ids(kb_lo);
+
+    // ---- this lane's rows (B operand columns n of the RT tiles) ----
+    f16x8 qv[RT][P::NC];
+    int pos[RT];
+    bool valid[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int row = wr0 + 16 * rt + n;
+      valid[rt] = row < total_rows;
+      const int rc = valid[rt] ? row : r_last;
+      pos[rt] = cached + rc / G;
+      const f16* qrow =
+          a.q + (int64_t)(sp.w.q0 + rc / G) * a.q_stride + (h * G + rc % G) * D + 8 * g;
+#pragma unroll
+      for (int c = 0; c < P::NC; ++c) {
+        const f16x8 v = ld16(qrow + 32 * c);
+        qv[rt][c] = valid[rt] ? v : f16x8{};
+      }
+    }
+    // blocks whose last key is <= every row's position of this wave need no mask
+    const int unmasked_blocks = (cached + min(wr0, r_last) / G + 1) / kDmaKeys;
+
+    float m_run[RT];
+    f32x4 o[RT][P::NX];
+    f32x4 lsum[RT];  // ones-tile accumulators: every element is the row's sum of P
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      m_run[rt] = kNegInf;
+      lsum[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int xx = 0; xx < P::NX; ++xx) o[rt][xx] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // ---- one block: S^T = K.Q^T, online softmax, O^T += V^T.P^T ----
+    const f16x8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f,
+                        (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
+    auto compute = [&](int kb, const unsigned char* kbase,
+                       const unsigned char* vbase) __attribute__((always_inline)) {
+      // K fragments (16 keys x 32 dims, A operand): all reads issued ahead of
+      // the MFMAs that use them
+      f16x8 kf[4][P::NC];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int c = 0; c < P::NC; ++c)
+          kf[kt][c] = *reinterpret_cast<const f16x8*>(
+              kbase + (16 * kt + n) * P::ROWB + (((4 * c + g) ^ swz_k<D>(16 * kt + n)) * 16));
+      f32x4 st[RT][4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) st[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int c = 0; c < P::NC; ++c)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) st[rt][kt] = mfma32(kf[kt][c], qv[rt][c], st[rt][kt]);
+      // V fragments (transposing reads): lane (g, n) of a read addresses V[key
+      // 32ps + 4g + n/4][dims 16x + 4(n%4) .. +3] (and the same 16 keys further
+      // for the second half of the k = 32 operand; 32ps and 16 keep the row's
+      // swizzle).  The first 32 keys' fragments are read before the softmax,
+      // whose VALU work hides their latency.
+      const int vrow = 4 * g + (n >> 2);
+      const int vswz = swz_v<D>(vrow);
+      auto vfrag = [&](int ps, int x) __attribute__((always_inline)) {
+        const unsigned char* vb = vbase + (32 * ps + vrow) * P::ROWB + (n & 1) * 8;
+        const unsigned char* vh = vbase + (32 * ps + 16 + vrow) * P::ROWB + (n & 1) * 8;
+        const int slot = (2 * x + ((n & 3) >> 1)) ^ vswz;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + slot * 16));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vh + slot * 16));
+        const f16x4 l4 = __builtin_bit_cast(f16x4, lo), h4 = __builtin_bit_cast(f16x4, hi);
+        return f16x8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+      };
+      f16x8 vf[P::NX];
+#pragma unroll
+      for (int x = 0; x < P::NX; ++x) vf[x] = vfrag(0, x);
+
+      const bool need_mask = kb >= unmasked_blocks;  // wave-uniform
+      f16x8 pb[RT][2];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        float sv[4][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sv[kt][i] = st[rt][kt][i];
+        if (need_mask) {
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (kb * kDmaKeys + 16 * kt + 4 * g + i > pos[rt]) sv[kt][i] = kNegInf;
+        }
+        const float mx = max_over_lane_rows(max16(sv)) * a.scale_log2;
+        if (__ballot(mx > m_run[rt] + kRescaleSlack)) {  // wave-uniform
+          const float m_new = fmaxf(m_run[rt], mx);
+          const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run[rt] - m_new);
+          lsum[rt] *= alpha;
+#pragma unroll
+          for (int x = 0; x < P::NX; ++x) o[rt][x] *= alpha;
+          m_run[rt] = m_new;
+        }
+        const float neg_m = m_run[rt] == kNegInf ? 0.f : -m_run[rt];
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps) {
+          f16x8 p;
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              p[4 * kt + i] = (f16)exp2_fast(__builtin_fmaf(sv[2 * ps + kt][i], a.scale_log2, neg_m));
+          pb[rt][ps] = p;
+        }
+      }
+#pragma unroll
+      for (int ps = 0; ps < 2; ++ps) {
+#pragma unroll
+        for (int x = 0; x < P::NX; ++x) {
+          const f16x8 va = vf[x];
+          if (ps == 0) vf[x] = vfrag(1, x);  // the next 32 keys' fragment, in flight meanwhile
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) o[rt][x] = mfma32(va, pb[rt][ps], o[rt][x]);
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) lsum[rt] = mfma32(ones, pb[rt][ps], lsum[rt]);
+      }
+    };
+
+
+    // ---- pipeline: the DMA of block kb+1 runs while block kb is computed; the
+    //      loop is unrolled by two so each half names its stage objects ----
+    auto block_id = [&](int kb) __attribute__((always_inline)) {
+      return clamp_block(__builtin_amdgcn_readlane(idv, kb - kb_base), a.NB);
+    };
+    if (dma_wave)
+      dma_run<D>(a, h, w, kb_lo * kDmaKeys + 16 * w, key_end, block_id(kb_lo), voff_k, voff_v,
+                 k0, v0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    auto step = [&](int kb, unsigned char* kc, unsigned char* vc, unsigned char* kn,
+                    unsigned char* vn) __attribute__((always_inline)) {
+      if (kb + 1 < kb_hi && dma_wave) {
+        if (kb + 1 - kb_base == kWave) {
+          kb_base = kb + 1;
+          idv = load_ids(kb_base);
+        }
+        dma_run<D>(a, h, w, (kb + 1) * kDmaKeys + 16 * w, key_end, block_id(kb + 1), voff_k,
+                   voff_v, kn, vn);
+      }
+      if (has_rows) compute(kb, kc, vc);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    };
+    for (int kb = kb_lo; kb < kb_hi; kb += 2) {
+      step(kb, k0, v0, k1, v1);
+      if (kb + 1 < kb_hi) step(kb + 1, k1, v1, k0, v0);
+    }
+
+    // ---- the whole unit here: store.  Part of it: normalised partial and
+    //      base-2 LSE (fp32) for the merge launch ----
+    const uint32_t slot = 2u * gid + (x_begin < unit_start ? 1u : 0u);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const float l = lsum[rt][0];
+      if (!has_rows || !valid[rt]) continue;
+      const int row = wr0 + 16 * rt + n;
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      if (!split) {
+        const int64_t orow_idx = (int64_t)(sp.w.q0 + row / G) * a.Hq + h * G + row % G;
+        f16* orow = a.out + orow_idx * D + 4 * g;
+#pragma unroll
+        for (int xx = 0; xx < P::NX; ++xx)
+          *reinterpret_cast<f16x4*>(orow + 16 * xx) =
+              f16x4{(f16)(o[rt][xx][0] * inv), (f16)(o[rt][xx][1] * inv),
+                    (f16)(o[rt][xx][2] * inv), (f16)(o[rt][xx][3] * inv)};
+      } else {
+        const uint32_t prow = slot * kDmaRows + (row - r0);
+        float* prow_o = a.part_o + (size_t)prow * D + 4 * g;
+#pragma unroll
+        for (int xx = 0; xx < P::NX; ++xx)
+          *reinterpret_cast<f32x4*>(prow_o + 16 * xx) = o[rt][xx] * inv;
+        if (g == 0) a.part_lse[prow] = l > 0.f ? m_run[rt] + log2f(l) : kNegInf;
+      }
+    }
+
+    // ---- next unit: next row block, head, then sequence ----
+    x += kb_hi - kb_lo;
+    if (x >= x_end) break;
+    sp.kb = 0;
+    if (++sp.rb == sp.w.R) {
+      sp.rb = 0;
+      if (++sp.h == a.Hkv) {
+        sp.h = 0;
+        // x < x_end <= T, so a sequence with blocks follows; the bound on s only
+        // guards the reads of q_off / ctx
+        do {
+          ++sp.s;
+        } while (sp.s < a.S && (sp.w = seq_work(a, sp.s)).tb == 0);
+        if (sp.s >= a.S) break;
+      }
+    }
+    __syncthreads();  // the stages are free for the next unit
+  }
+  put_desc();
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline int log2_exact(int x) {
   if (x <= 0 || (x & (x - 1))) return -1;
@@ -529,6 +1288,39 @@ void launch_prefill(const PrefillArgs& a, int blocks, hipStream_t stream) {
   using P = PCfg<D, RT>;
   hipLaunchKernelGGL((prefill_kernel<D, RT, CASCADE>), dim3(blocks * a.Hkv * a.KS),
                      dim3(kThreads), 2 * P::STAGE, stream, a);
+}
+
+#ifndef FE_PREFILL_DMA_RT
+#define FE_PREFILL_DMA_RT 2
+#endif
+// Workgroups of the stream-K kernel per CU (LDS: 64 KiB per workgroup at D =
+// 128, so two fit).
+#ifndef FE_PREFILL_DMA_PER_CU
+#define FE_PREFILL_DMA_PER_CU 2
+#endif
+
+// Compute units of the current device (queried once per device).
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  static int cache[64] = {};
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  if (dev >= 0 && dev < 64) cache[dev] = cus;
+  return cus;
+}
+inline int stream_wgs() { return FE_PREFILL_DMA_PER_CU * device_cus(); }
+
+template <int D>
+void launch_prefill_dma(const PrefillArgs& a, hipStream_t stream) {
+  constexpr int RT = FE_PREFILL_DMA_RT;
+  hipLaunchKernelGGL((prefill_dma_kernel<D, RT>), dim3(a.nwg_max), dim3(DWaves<RT>::THREADS), 0,
+                     stream, a);
+  hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3(kMergeGrid * a.nwg_max), dim3(kMergeThreads),
+                     0, stream, a);
 }
 
 constexpr int kMaxTickets = 65536;
@@ -569,6 +1361,27 @@ inline Plan plan(int num_seqs, int total_q, int num_q_heads, int kv_heads) {
   return p;
 }
 
+// Whether the stream-K kernel takes a launch: block sizes that are multiples
+// of 16 (every 16-key run of a 64-key block lies in one page), and sizes whose
+// block counts stay within the 32-bit closed form of the work split.
+inline bool stream_ok(int block_size, int table_stride, int total_q, int G, int num_seqs,
+                      int kv_heads, int nwg) {
+  if (block_size % 16 != 0 || nwg <= 0 || nwg > kMergeDescPerThread * kMergeThreads) return false;
+  const int64_t max_ctx = (int64_t)table_stride * block_size;
+  const int64_t units = ((int64_t)total_q * G + kDmaRows - 1) / kDmaRows + num_seqs;
+  // closed-form operands within 32 bits; total key blocks within 31 bits (a
+  // row block reads at most the context plus its own new rows' positions)
+  return max_ctx * G < ((int64_t)1 << 28) && (int64_t)total_q * G < ((int64_t)1 << 28) &&
+         units * kv_heads * ((max_ctx + total_q) / kDmaKeys + 2) < ((int64_t)1 << 31);
+}
+
+// Partial slots of the stream-K kernel: two per workgroup, 128 rows each.
+inline size_t stream_ws_bytes(int head_dim) {
+  const size_t rows = (size_t)2 * stream_wgs() * kDmaRows;
+  return kTicketBytes + align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float)) +
+         align256((size_t)stream_wgs() * sizeof(MergeDesc));
+}
+
 }  // namespace
 
 extern "C" size_t fe_prefill_workspace_size(int num_seqs, int total_q, int num_q_heads,
@@ -576,10 +1389,15 @@ extern "C" size_t fe_prefill_workspace_size(int num_seqs, int total_q, int num_q
   if (num_seqs < 0 || total_q < 0 || num_q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
       num_q_heads % kv_heads)
     return 0;
+  // enough for either kernel (the size does not depend on the block size)
   const Plan p = plan(num_seqs, total_q, num_q_heads, kv_heads);
-  if (p.ks == 1) return kTicketBytes;
-  const size_t rows = (size_t)p.ks * total_q * num_q_heads;
-  return kTicketBytes + align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
+  size_t need = kTicketBytes;
+  if (p.ks > 1) {
+    const size_t rows = (size_t)p.ks * total_q * num_q_heads;
+    need += align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
+  }
+  const size_t sk = stream_ws_bytes(head_dim);
+  return need > sk ? need : sk;
 }
 
 extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, const void* v_pool,
@@ -600,8 +1418,12 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   if (num_seqs == 0 || total_q == 0) return FE_OK;
   FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && q_offsets && context_lens);
   FE_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(k_pool) && aligned16(v_pool));
+  const int nwg = stream_wgs();
+  const bool dma = stream_ok(block_size, table_stride, total_q, num_q_heads / kv_heads, num_seqs,
+                             kv_heads, nwg);
   const Plan p = plan(num_seqs, total_q, num_q_heads, kv_heads);
-  if ((int64_t)p.blocks * kv_heads > kMaxTickets) return FE_ERR_UNSUPPORTED;
+  // split-K tickets of prefill_kernel: one per (row block, KV head)
+  if (!dma && (int64_t)p.blocks * kv_heads > kMaxTickets) return FE_ERR_UNSUPPORTED;
   const size_t need = fe_prefill_workspace_size(num_seqs, total_q, num_q_heads, kv_heads, head_dim);
   if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
     return FE_ERR_WORKSPACE;
@@ -617,10 +1439,12 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   char* ws = (char*)workspace;
   a.tickets = (int*)ws;
   ws += kTicketBytes;
-  const size_t rows = (size_t)p.ks * total_q * num_q_heads;
+  const size_t rows = dma ? (size_t)2 * nwg * kDmaRows : (size_t)p.ks * total_q * num_q_heads;
   a.part_o = (float*)ws;
   ws += align256(rows * head_dim * sizeof(float));
   a.part_lse = (float*)ws;
+  ws += align256(rows * sizeof(float));
+  a.merge = dma ? (MergeDesc*)ws : nullptr;
   a.W = table_stride;
   a.S = num_seqs;
   a.total_q = total_q;
@@ -630,7 +1454,8 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   a.BS = block_size;
   a.bs_log2 = bs_log2;
   a.NB = num_blocks;
-  a.KS = p.ks;
+  a.KS = dma ? 1 : p.ks;
+  a.nwg_max = nwg;
   a.scale_log2 = scale * kLog2e;
   a.q_stride = (int64_t)num_q_heads * head_dim;
   a.prefix_len = nullptr;
@@ -638,7 +1463,9 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   a.pre_lse = nullptr;
   a.tok0 = nullptr;
   hipStream_t s = (hipStream_t)stream;
-  if (head_dim == 64) {
+  if (dma) {
+    if (head_dim == 64) launch_prefill_dma<64>(a, s); else launch_prefill_dma<128>(a, s);
+  } else if (head_dim == 64) {
     if (p.rt == 2) launch_prefill<64, 2>(a, p.blocks, s); else launch_prefill<64, 1>(a, p.blocks, s);
   } else {
     if (p.rt == 2) launch_prefill<128, 2>(a, p.blocks, s); else launch_prefill<128, 1>(a, p.blocks, s);
@@ -684,6 +1511,8 @@ int cascade_prefix_launch(const CascadePrefix& c, hipStream_t stream) {
   a.bs_log2 = log2_exact(c.bs);
   a.NB = c.num_blocks;
   a.KS = p.ks;
+  a.nwg_max = 0;
+  a.merge = nullptr;
   a.scale_log2 = c.scale * kLog2e;
   a.prefix_len = c.prefix_len;
   a.pre_o = c.pre_o;
