@@ -546,15 +546,7 @@ void prefill_kernel(const PrefillArgs a) {
 //   output uses, and takes the place of a VALU add per score.
 
 constexpr int kDmaKeys = 64;                       // keys per staged block
-constexpr int kDmaRows = 128;                      // rows per workgroup
-// RT 16-row MFMA tiles per wave, 8 / RT waves per workgroup: RT = 2 feeds two
-// MFMAs from every K/V fragment read from LDS (VGPRs allow 2 waves per SIMD),
-// RT = 1 one (4 waves per SIMD)
-template <int RT>
-struct DWaves {
-  static constexpr int NW = kDmaRows / (16 * RT);
-  static constexpr int THREADS = NW * kWave;
-};
+constexpr int kDmaRows = 128;                      // rows per unit
 
 template <int D>
 struct DCfg {
@@ -633,8 +625,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t run_rsrc(const f16* base, uint
 // key before key_end (later rows arrive as zeros).
 template <int D>
 __device__ __forceinline__ void dma_run(const PrefillArgs& a, int h, int w, int t0, int key_end,
-                                        int id, const uint32_t (&voff_k)[DCfg<D>::NI],
-                                        const uint32_t (&voff_v)[DCfg<D>::NI],
+                                        int id, const uint32_t* voff_k, const uint32_t* voff_v,
                                         unsigned char* kst, unsigned char* vst) {
   using P = DCfg<D>;
   const int rs = a.Hkv * D * 2;
@@ -876,7 +867,7 @@ struct MergeDesc {
 constexpr int kMergeThreads = 256;
 constexpr int kMergeRows = 32;                       // rows per task
 constexpr int kMergeParts = kDmaRows / kMergeRows;   // tasks per split unit
-constexpr int kMergeGrid = 2;  // merge workgroups per stream-K workgroup: one task each in
+constexpr int kMergeGrid = 4;  // merge workgroups per stream-K workgroup: one task each in
                                // the usual case (at most one split unit per range)
 constexpr int kMergeDescPerThread = 4;  // descriptors a thread counts (nwg_max <= 1024)
 
@@ -990,35 +981,31 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(const Pref
   }
 }
 
-template <int D, int RT>
-__global__ __launch_bounds__(DWaves<RT>::THREADS) __attribute__((amdgpu_waves_per_eu(4 / RT, 4 / RT)))
-void prefill_dma_kernel(const PrefillArgs a) {
+// The stream-K kernel's workgroup: two halves of kHalfWaves waves, each wave
+// 32 rows (RT = 2 tiles of 16) of the unit's 128.  Half H takes the unit's
+// blocks kb_lo + H, kb_lo + H + 2, ... with its own two LDS stages, so the
+// workgroup keeps 128 rows in flight per CU with two waves per SIMD, and the
+// halves' online-softmax states of each row meet in LDS at the unit's end.
+constexpr int kHalfWaves = kDmaRows / 32;
+constexpr int kDmaThreads = 2 * kHalfWaves * kWave;
+
+// The units of workgroup gid's range [x_begin, x_end) for the waves of half H
+// (wave r of the half); k0 .. v1 are the half's stage objects, pk1 / pv1 the
+// partner half's stage-1 objects and xml the exchange of row maxima and sums.
+// Units follow each other without a pipeline bubble: after a unit's last step
+// the next unit's block ids, queries and first block (into stage 0) are loaded
+// while the halves exchange their states (in the stage-1 objects) and store.
+template <int D, int RT, int H>
+__device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan& pl, int gid,
+                                          int x_begin, int x_end, StreamPos sp, MergeDesc& md,
+                                          int r, unsigned char* k0, unsigned char* v0,
+                                          unsigned char* k1, unsigned char* v1,
+                                          const unsigned char* pk1, const unsigned char* pv1,
+                                          float* xml) {
   using P = DCfg<D>;
-  // K and V of two stages as four LDS objects: the compiler's wait for an LDS
-  // DMA before an LDS read is then limited to reads of the object it fills
-  __shared__ __align__(16) unsigned char k0[P::MAT];
-  __shared__ __align__(16) unsigned char v0[P::MAT];
-  __shared__ __align__(16) unsigned char k1[P::MAT];
-  __shared__ __align__(16) unsigned char v1[P::MAT];
-
-  // this workgroup's merge descriptor: empty unless its last unit is split and
-  // starts in its range
-  MergeDesc md{};
-  auto put_desc = [&]() __attribute__((always_inline)) {
-    if (threadIdx.x == 0) a.merge[blockIdx.x] = md;
-  };
-  const StreamPlan pl = stream_plan(a);
-  const int nwg = pl.rg.nwg;
-  if ((int)blockIdx.x >= nwg) return put_desc();
-  const int gid = logical_wg(blockIdx.x, nwg);
-  const int x_begin = pl.rg.start(gid);
-  const int x_end = pl.rg.start(gid + 1);
-  if (x_begin >= x_end) return put_desc();
-  StreamPos sp;
-  if (!stream_locate(a, pl.w0, x_begin, sp)) return put_desc();
-
+  static_assert(RT == 2, "each half's wave exchanges one of its two row tiles");
+  static_assert(2 * P::NX * kWave * 16 <= P::MAT, "two waves' tiles per stage object");
   const int G = a.G;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = lane_id();
   const int g = lane >> 4;
   const int n = lane & 15;
@@ -1026,61 +1013,67 @@ void prefill_dma_kernel(const PrefillArgs a) {
   uint32_t voff_k[P::NI], voff_v[P::NI];  // loop-invariant DMA lane offsets
 #pragma unroll
   for (int i = 0; i < P::NI; ++i) {
-    const int r = P::RPI * i + lane / P::CPR;
+    const int rr = P::RPI * i + lane / P::CPR;
     const int sl = lane % P::CPR;
-    voff_k[i] = (uint32_t)(r * rs + (sl ^ swz_k<D>(r)) * 16);
-    voff_v[i] = (uint32_t)(r * rs + (sl ^ swz_v<D>(r)) * 16);
+    voff_k[i] = (uint32_t)(rr * rs + (sl ^ swz_k<D>(rr)) * 16);
+    voff_v[i] = (uint32_t)(rr * rs + (sl ^ swz_v<D>(rr)) * 16);
   }
-  const bool dma_wave = w < kDmaKeys / 16;  // the 16-key runs of a block go to waves 0..3
+
+  // ---- the current unit (wave-uniform, except the lanes' rows) ----
   int x = x_begin;
-  while (x < x_end) {
-    // ---- the unit at x and this workgroup's blocks of it ----
-    const int h = sp.h;
-    const int total_rows = sp.w.n * G;
-    const int cached = sp.w.cached;
-    const int r0 = sp.rb * kDmaRows;
-    const int r_last = min(r0 + kDmaRows, total_rows) - 1;
-    const int key_end = cached + r_last / G + 1;  // keys the row block reads
+  int h = 0, q0 = 0, total_rows = 0, cached = 0, r0 = 0, r_last = 0, key_end = 0;
+  int kb_lo = 0, kb_hi = 0, kb_first = 0, unit_start = 0, wr0 = 0, unmasked_blocks = 0;
+  bool split = false, has_rows = false;
+  const int32_t* trow = a.tables;
+  int kb_base = 0, idv = 0;
+  f16x8 qv[RT][P::NC];
+  int pos[RT];
+  bool valid[RT];
+  // block ids of the wave's run for blocks base .. base + 63 (lane j: block base + j)
+  auto load_ids = [&](int base) __attribute__((always_inline)) {
+    int page = ((base + lane) * kDmaKeys + 16 * r) >> a.bs_log2;
+    page = page < a.W ? page : a.W - 1;
+    return trow[page];
+  };
+  auto block_id = [&](int kb) __attribute__((always_inline)) {
+    return clamp_block(__builtin_amdgcn_readlane(idv, kb - kb_base), a.NB);
+  };
+  // takes the unit at (x, sp) and issues its block ids, the lanes' queries and
+  // the DMA of the half's first block into stage 0
+  auto open_unit = [&]() __attribute__((always_inline)) {
+    h = sp.h;
+    q0 = sp.w.q0;
+    total_rows = sp.w.n * G;
+    cached = sp.w.cached;
+    r0 = sp.rb * kDmaRows;
+    r_last = min(r0 + kDmaRows, total_rows) - 1;
+    key_end = cached + r_last / G + 1;  // keys the row block reads
     const int nb = rb_blocks(a, sp.w, sp.rb);
-    const int kb_lo = sp.kb;
-    const int kb_hi = min(nb, kb_lo + (x_end - x));
-    const int unit_start = x - kb_lo;
-    const bool split = kb_lo > 0 || kb_hi < nb;  // other workgroups hold blocks of the unit
-    if (kb_hi < nb && unit_start >= x_begin) {   // this range's last unit, merged later
+    kb_lo = sp.kb;
+    kb_hi = min(nb, kb_lo + (x_end - x));
+    unit_start = x - kb_lo;
+    split = kb_lo > 0 || kb_hi < nb;  // other workgroups hold blocks of the unit
+    if (kb_hi < nb && unit_start >= x_begin) {  // this range's last unit, merged later
       md.cnt = pl.rg.owner(unit_start + nb - 1) - gid + 1;
       md.slot0 = 2 * gid + (x_begin < unit_start ? 1 : 0);
-      md.q0 = sp.w.q0;
+      md.q0 = q0;
       md.h = h;
       md.r0 = r0;
       md.r_end = r_last + 1;
     }
-    const int wr0 = r0 + w * 16 * RT;             // first row of this wave
-    const bool has_rows = wr0 <= r_last;          // wave-uniform
-
-    // block ids of the wave's run for blocks kb_base .. kb_base + 63 (lane j:
-    // block kb_base + j), loaded before the rows' queries so that the first
-    // block's DMA waits for the ids only
-    const int32_t* trow = a.tables + (int64_t)sp.s * a.W;
-    auto load_ids = [&](int kb_base) __attribute__((always_inline)) {
-      int page = ((kb_base + lane) * kDmaKeys + 16 * w) >> a.bs_log2;
-      page = page < a.W ? page : a.W - 1;
-      return trow[page];
-    };
-    int kb_base = kb_lo;
-    int idv = load_ids(kb_lo);
-
-    // ---- this lane's rows (B operand columns n of the RT tiles) ----
-    f16x8 qv[RT][P::NC];
-    int pos[RT];
-    bool valid[RT];
+    wr0 = r0 + r * 16 * RT;  // first row of this wave
+    has_rows = wr0 <= r_last;
+    trow = a.tables + (int64_t)sp.s * a.W;
+    kb_first = kb_lo + H;  // this half's blocks: kb_first, kb_first + 2, ...
+    kb_base = kb_first;
+    idv = load_ids(kb_first);  // before the queries: the DMA below waits for the ids only
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int row = wr0 + 16 * rt + n;
       valid[rt] = row < total_rows;
       const int rc = valid[rt] ? row : r_last;
       pos[rt] = cached + rc / G;
-      const f16* qrow =
-          a.q + (int64_t)(sp.w.q0 + rc / G) * a.q_stride + (h * G + rc % G) * D + 8 * g;
+      const f16* qrow = a.q + (int64_t)(q0 + rc / G) * a.q_stride + (h * G + rc % G) * D + 8 * g;
 #pragma unroll
       for (int c = 0; c < P::NC; ++c) {
         const f16x8 v = ld16(qrow + 32 * c);
@@ -1088,8 +1081,32 @@ void prefill_dma_kernel(const PrefillArgs a) {
       }
     }
     // blocks whose last key is <= every row's position of this wave need no mask
-    const int unmasked_blocks = (cached + min(wr0, r_last) / G + 1) / kDmaKeys;
+    unmasked_blocks = (cached + min(wr0, r_last) / G + 1) / kDmaKeys;
+    if (kb_first < kb_hi)
+      dma_run<D>(a, h, r, kb_first * kDmaKeys + 16 * r, key_end, block_id(kb_first), voff_k,
+                 voff_v, k0, v0);
+  };
+  // moves sp to the unit after the current one: next row block, head, then
+  // sequence; false past the last sequence
+  auto next_unit = [&]() __attribute__((always_inline)) {
+    sp.kb = 0;
+    if (++sp.rb == sp.w.R) {
+      sp.rb = 0;
+      if (++sp.h == a.Hkv) {
+        sp.h = 0;
+        do {
+          ++sp.s;
+        } while (sp.s < a.S && (sp.w = seq_work(a, sp.s)).tb == 0);
+        if (sp.s >= a.S) return false;
+      }
+    }
+    return true;
+  };
 
+  open_unit();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  while (true) {
     float m_run[RT];
     f32x4 o[RT][P::NX];
     f32x4 lsum[RT];  // ones-tile accumulators: every element is the row's sum of P
@@ -1197,81 +1214,140 @@ void prefill_dma_kernel(const PrefillArgs a) {
       }
     };
 
-
-    // ---- pipeline: the DMA of block kb+1 runs while block kb is computed; the
-    //      loop is unrolled by two so each half names its stage objects ----
-    auto block_id = [&](int kb) __attribute__((always_inline)) {
-      return clamp_block(__builtin_amdgcn_readlane(idv, kb - kb_base), a.NB);
-    };
-    if (dma_wave)
-      dma_run<D>(a, h, w, kb_lo * kDmaKeys + 16 * w, key_end, block_id(kb_lo), voff_k, voff_v,
-                 k0, v0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    auto step = [&](int kb, unsigned char* kc, unsigned char* vc, unsigned char* kn,
+    // ---- pipeline: the DMA of the half's next block (kb + 2) runs while block
+    //      kb is computed; the loop is unrolled by two so each step names its
+    //      stage objects; both halves take the same number of steps ----
+    const int nsteps = (kb_hi - kb_lo + 1) / 2;
+    auto step = [&](int j, unsigned char* kc, unsigned char* vc, unsigned char* kn,
                     unsigned char* vn) __attribute__((always_inline)) {
-      if (kb + 1 < kb_hi && dma_wave) {
-        if (kb + 1 - kb_base == kWave) {
-          kb_base = kb + 1;
+      const int kb = kb_first + 2 * j;
+      if (kb + 2 < kb_hi) {
+        if (kb + 2 - kb_base >= kWave) {
+          kb_base = kb + 2;
           idv = load_ids(kb_base);
         }
-        dma_run<D>(a, h, w, (kb + 1) * kDmaKeys + 16 * w, key_end, block_id(kb + 1), voff_k,
+        dma_run<D>(a, h, r, (kb + 2) * kDmaKeys + 16 * r, key_end, block_id(kb + 2), voff_k,
                    voff_v, kn, vn);
       }
-      if (has_rows) compute(kb, kc, vc);
+      if (has_rows && kb < kb_hi) compute(kb, kc, vc);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     };
-    for (int kb = kb_lo; kb < kb_hi; kb += 2) {
-      step(kb, k0, v0, k1, v1);
-      if (kb + 1 < kb_hi) step(kb + 1, k1, v1, k0, v0);
+    for (int j = 0; j < nsteps; j += 2) {
+      step(j, k0, v0, k1, v1);
+      if (j + 1 < nsteps) step(j + 1, k1, v1, k0, v0);
+    }
+
+    // ---- what the store of this unit needs; then the next unit's loads ----
+    const bool st_ok = has_rows && valid[H];
+    const int st_row = wr0 + 16 * H + n;
+    const int st_q0 = q0, st_h = h, st_r0 = r0;
+    const bool st_split = split;
+    const uint32_t slot = 2u * gid + (x_begin < unit_start ? 1u : 0u);
+    const int x_next = x + (kb_hi - kb_lo);
+    const bool more = x_next < x_end && next_unit();
+    if (more) {
+      x = x_next;
+      open_unit();
+    }
+
+    // ---- the two halves' states of the unit's rows meet in LDS (stage 1 is
+    //      idle: the next unit's first block goes to stage 0): tile rt = H
+    //      stays, tile 1 - H goes to the partner wave (1 - H, r), which holds
+    //      the same rows ----
+    {
+      float* xo = reinterpret_cast<float*>((r < 2 ? k1 : v1) + (r & 1) * P::NX * kWave * 16);
+#pragma unroll
+      for (int xx = 0; xx < P::NX; ++xx)
+        *reinterpret_cast<f32x4*>(xo + (xx * kWave + lane) * 4) = o[1 - H][xx];
+      float* xm = xml + (H * kHalfWaves + r) * 2 * kWave;
+      xm[lane] = m_run[1 - H];
+      xm[kWave + lane] = lsum[1 - H][0];
+    }
+    __syncthreads();
+    {
+      const float* xp =
+          reinterpret_cast<const float*>((r < 2 ? pk1 : pv1) + (r & 1) * P::NX * kWave * 16);
+      const float* xm = xml + ((1 - H) * kHalfWaves + r) * 2 * kWave;
+      const float pm = xm[lane];
+      const float pl = xm[kWave + lane];
+      const float mm = fmaxf(m_run[H], pm);
+      const float a0 = m_run[H] == kNegInf ? 0.f : exp2_fast(m_run[H] - mm);
+      const float a1 = pm == kNegInf ? 0.f : exp2_fast(pm - mm);
+#pragma unroll
+      for (int xx = 0; xx < P::NX; ++xx)
+        o[H][xx] = a0 * o[H][xx] + a1 * *reinterpret_cast<const f32x4*>(xp + (xx * kWave + lane) * 4);
+      lsum[H][0] = a0 * lsum[H][0] + a1 * pl;
+      m_run[H] = mm;
     }
 
     // ---- the whole unit here: store.  Part of it: normalised partial and
     //      base-2 LSE (fp32) for the merge launch ----
-    const uint32_t slot = 2u * gid + (x_begin < unit_start ? 1u : 0u);
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const float l = lsum[rt][0];
-      if (!has_rows || !valid[rt]) continue;
-      const int row = wr0 + 16 * rt + n;
+    if (st_ok) {
+      const float l = lsum[H][0];
       const float inv = l > 0.f ? 1.f / l : 0.f;
-      if (!split) {
-        const int64_t orow_idx = (int64_t)(sp.w.q0 + row / G) * a.Hq + h * G + row % G;
+      if (!st_split) {
+        const int64_t orow_idx = (int64_t)(st_q0 + st_row / G) * a.Hq + st_h * G + st_row % G;
         f16* orow = a.out + orow_idx * D + 4 * g;
 #pragma unroll
         for (int xx = 0; xx < P::NX; ++xx)
           *reinterpret_cast<f16x4*>(orow + 16 * xx) =
-              f16x4{(f16)(o[rt][xx][0] * inv), (f16)(o[rt][xx][1] * inv),
-                    (f16)(o[rt][xx][2] * inv), (f16)(o[rt][xx][3] * inv)};
+              f16x4{(f16)(o[H][xx][0] * inv), (f16)(o[H][xx][1] * inv),
+                    (f16)(o[H][xx][2] * inv), (f16)(o[H][xx][3] * inv)};
       } else {
-        const uint32_t prow = slot * kDmaRows + (row - r0);
+        const uint32_t prow = slot * kDmaRows + (st_row - st_r0);
         float* prow_o = a.part_o + (size_t)prow * D + 4 * g;
 #pragma unroll
         for (int xx = 0; xx < P::NX; ++xx)
-          *reinterpret_cast<f32x4*>(prow_o + 16 * xx) = o[rt][xx] * inv;
-        if (g == 0) a.part_lse[prow] = l > 0.f ? m_run[rt] + log2f(l) : kNegInf;
+          *reinterpret_cast<f32x4*>(prow_o + 16 * xx) = o[H][xx] * inv;
+        if (g == 0) a.part_lse[prow] = l > 0.f ? m_run[H] + log2f(l) : kNegInf;
       }
     }
-
-    // ---- next unit: next row block, head, then sequence ----
-    x += kb_hi - kb_lo;
-    if (x >= x_end) break;
-    sp.kb = 0;
-    if (++sp.rb == sp.w.R) {
-      sp.rb = 0;
-      if (++sp.h == a.Hkv) {
-        sp.h = 0;
-        // x < x_end <= T, so a sequence with blocks follows; the bound on s only
-        // guards the reads of q_off / ctx
-        do {
-          ++sp.s;
-        } while (sp.s < a.S && (sp.w = seq_work(a, sp.s)).tb == 0);
-        if (sp.s >= a.S) break;
-      }
-    }
-    __syncthreads();  // the stages are free for the next unit
+    if (!more) break;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next unit's ids, queries, block
+    __syncthreads();  // ... and the exchange has been read before stage 1 is refilled
   }
+}
+
+template <int D, int RT>
+__global__ __launch_bounds__(kDmaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_dma_kernel(const PrefillArgs a) {
+  using P = DCfg<D>;
+  // K and V of two stages per half as eight LDS objects: the compiler's wait
+  // for an LDS DMA before an LDS read is then limited to reads of the object
+  // it fills
+  __shared__ __align__(16) unsigned char k00[P::MAT];
+  __shared__ __align__(16) unsigned char v00[P::MAT];
+  __shared__ __align__(16) unsigned char k01[P::MAT];
+  __shared__ __align__(16) unsigned char v01[P::MAT];
+  __shared__ __align__(16) unsigned char k10[P::MAT];
+  __shared__ __align__(16) unsigned char v10[P::MAT];
+  __shared__ __align__(16) unsigned char k11[P::MAT];
+  __shared__ __align__(16) unsigned char v11[P::MAT];
+  __shared__ float xml[2 * kHalfWaves * 2 * kWave];  // row maxima and sums exchanged at unit ends
+
+  // this workgroup's merge descriptor: empty unless its last unit is split and
+  // starts in its range
+  MergeDesc md{};
+  auto put_desc = [&]() __attribute__((always_inline)) {
+    if (threadIdx.x == 0) a.merge[blockIdx.x] = md;
+  };
+  const StreamPlan pl = stream_plan(a);
+  const int nwg = pl.rg.nwg;
+  if ((int)blockIdx.x >= nwg) return put_desc();
+  const int gid = logical_wg(blockIdx.x, nwg);
+  const int x_begin = pl.rg.start(gid);
+  const int x_end = pl.rg.start(gid + 1);
+  if (x_begin >= x_end) return put_desc();
+  StreamPos sp;
+  if (!stream_locate(a, pl.w0, x_begin, sp)) return put_desc();
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = w % kHalfWaves;
+  if (w < kHalfWaves)
+    run_units<D, RT, 0>(a, pl, gid, x_begin, x_end, sp, md, r, k00, v00, k01, v01, k11, v11, xml);
+  else
+    run_units<D, RT, 1>(a, pl, gid, x_begin, x_end, sp, md, r, k10, v10, k11, v11, k01, v01, xml);
   put_desc();
 }
 
@@ -1290,14 +1366,9 @@ void launch_prefill(const PrefillArgs& a, int blocks, hipStream_t stream) {
                      dim3(kThreads), 2 * P::STAGE, stream, a);
 }
 
-#ifndef FE_PREFILL_DMA_RT
-#define FE_PREFILL_DMA_RT 2
-#endif
-// Workgroups of the stream-K kernel per CU (LDS: 64 KiB per workgroup at D =
-// 128, so two fit).
-#ifndef FE_PREFILL_DMA_PER_CU
-#define FE_PREFILL_DMA_PER_CU 2
-#endif
+// RT 16-row MFMA tiles per wave of the stream-K kernel: two, so every K/V
+// fragment read from LDS feeds two MFMAs (VGPRs allow 2 waves per SIMD).
+constexpr int kDmaRt = 2;
 
 // Compute units of the current device (queried once per device).
 int device_cus() {
@@ -1312,13 +1383,14 @@ int device_cus() {
   if (dev >= 0 && dev < 64) cache[dev] = cus;
   return cus;
 }
-inline int stream_wgs() { return FE_PREFILL_DMA_PER_CU * device_cus(); }
+// One stream-K workgroup per CU (LDS: 128 KiB of stages at D = 128).
+inline int stream_wgs() { return device_cus(); }
 
 template <int D>
 void launch_prefill_dma(const PrefillArgs& a, hipStream_t stream) {
-  constexpr int RT = FE_PREFILL_DMA_RT;
-  hipLaunchKernelGGL((prefill_dma_kernel<D, RT>), dim3(a.nwg_max), dim3(DWaves<RT>::THREADS), 0,
-                     stream, a);
+  constexpr int RT = kDmaRt;
+  hipLaunchKernelGGL((prefill_dma_kernel<D, RT>), dim3(a.nwg_max), dim3(kDmaThreads), 0, stream,
+                     a);
   hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3(kMergeGrid * a.nwg_max), dim3(kMergeThreads),
                      0, stream, a);
 }
