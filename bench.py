@@ -5,9 +5,14 @@ plus decode tokens/s of the Qwen2.5-1.5B decoder (C5) on the same line.
 Workload: one layer of a batched decode step at Qwen2.5-1.5B
 head shapes -- 12 query heads, 2 KV heads, head_dim 128, fp16, batch 64,
 context lengths log-uniform in [128, 4096], block size 16, a 1.25x pool and
-randomly permuted block tables.  A "step" is one fe_paged_decode call: the page
-write of each sequence's new token, split-K attention over its paged K/V and
-the LSE merge, with every input resident in HBM.
+randomly permuted block tables.  A "step" is one layer's decode call
+(fe_paged_decode_planned): the page write of each sequence's new token, split-K
+attention over its paged K/V and the LSE merge, with every input resident in HBM.
+The decode plan (fe_paged_decode_plan: the split-K partition and the block rows
+of every workgroup) is computed once per model decode step and shared by its 28
+layers; the timed region runs it before step 0, 28, 56, ... (ceil(steps / 28)
+plan launches), so each step carries 1/28 of its cost.  --unplanned times
+fe_paged_decode instead (partition and tables at the start of every launch).
 
 Timing: exactly --steps steps between two synchronisations, replayed from HIP
 graphs (one graph cycling once over the rotating pools, replayed as often as it
@@ -33,6 +38,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -43,6 +49,7 @@ if str(REPO) not in sys.path:
     sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
+LAYERS = 28  # Qwen2.5-1.5B decoder layers sharing one decode plan per step
 METRIC = "paged decode attn HBM GB/s (% peak) at B=64; decode tok/s Qwen2.5-1.5B"
 # published by the reference for its fused Triton decode at the microbenchmark
 # shape on an RTX 3080 Ti Laptop (README.md:278, docs/FINAL_REPORT.md:59-61)
@@ -60,6 +67,8 @@ def parse_args(argv=None):
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--pools", type=int, default=8, help="rotating KV pool copies (MALL flush)")
     p.add_argument("--target-splits", type=int, default=0)
+    p.add_argument("--unplanned", action="store_true",
+                   help="time fe_paged_decode (no shared per-step plan)")
     p.add_argument("--cpu-seconds", type=float, default=6.0,
                    help="time budget per CPU-baseline route and config")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -254,13 +263,24 @@ def main(argv=None) -> int:
         w.batch, 12, 128, w.block_tables.shape[1] * w.block_size, args.target_splits))
     nbytes = w.algorithmic_bytes()
     steps, warm = max(1, args.steps), max(0, args.warmup)
+    planned = not args.unplanned
+    nb, bs, hkv = d.k_pool.shape[0], d.k_pool.shape[1], d.k_pool.shape[2]
+    plan = ops.paged_decode_plan(d.block_tables, d.context_lens, nb, hkv, bs,
+                                 target_splits=args.target_splits) if planned else None
 
     def step(i: int) -> None:
         kp, vp = pools[i % n_pool]
+        if planned and i % LAYERS == 0:    # one plan per model decode step of 28 layers
+            ops.paged_decode_plan(d.block_tables, d.context_lens, nb, hkv, bs,
+                                  target_splits=args.target_splits, out=plan)
         ops.paged_decode(d.q, kp, vp, d.block_tables, d.context_lens, k_new=d.k_new,
-                         v_new=d.v_new, out=out, workspace=ws, target_splits=args.target_splits)
+                         v_new=d.v_new, out=out, workspace=ws, target_splits=args.target_splits,
+                         plan=plan)
 
-    for i in range(max(warm, n_pool)):     # warm-up (also outside any capture)
+    # graphs of whole periods of both the pool rotation and the plan: the cycle
+    # graph replays steps 0 .. period-1, the rest graph steps 0 .. steps % period - 1
+    period = n_pool * LAYERS // math.gcd(n_pool, LAYERS) if planned else n_pool
+    for i in range(max(warm, period)):     # warm-up (also outside any capture)
         step(i)
     torch.cuda.synchronize()
 
@@ -273,15 +293,15 @@ def main(argv=None) -> int:
                 step(i)
         return g
 
-    cycle = record(n_pool)
-    rest = record(steps % n_pool)
+    cycle = record(min(period, steps))
+    rest = record(steps % period) if steps > period else None
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record(stream)
-    for _ in range(steps // n_pool):
+    for _ in range(max(1, steps // period)):
         cycle.replay()
     if rest is not None:
         rest.replay()
@@ -316,7 +336,7 @@ def main(argv=None) -> int:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": max(warm, n_pool),
+        "warmup": max(warm, period),
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -333,6 +353,9 @@ def main(argv=None) -> int:
             "rotating_pools": n_pool,
             "graph_replay": True,
             "target_splits": args.target_splits,
+            "decode_plan": (f"fe_paged_decode_plan once per {LAYERS} steps inside the timed "
+                            f"region ({-(-steps // LAYERS)} plan launches: one per model decode "
+                            f"step of the {LAYERS}-layer model)") if planned else "none",
         },
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {
@@ -343,7 +366,10 @@ def main(argv=None) -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "kernel": "piece_decode_kernel<128, true> (fe_paged_decode: page write + split-K "
+            "kernel": ("piece_decode_kernel<128, true, true> (fe_paged_decode_planned: page "
+                       "write + split-K attention + in-kernel LSE merge, one launch; achieved "
+                       "includes 1/28 of decode_plan_kernel per launch)") if planned else
+                      "piece_decode_kernel<128, true> (fe_paged_decode: page write + split-K "
                       "attention + in-kernel LSE merge, one launch)",
             "us_per_launch": round(per_launch_ms * 1e3, 3),
         },

@@ -41,6 +41,10 @@ SIGNATURES: dict[str, tuple] = {
     "fe_paged_decode_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
     "fe_paged_decode": (_i, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i, _p, _i, _p, _p, _sz,
                              _i, _i, _i, _i, _i, _f, _i, _p]),
+    "fe_paged_decode_plan_size": (_sz, [_i, _i, _i, _i]),
+    "fe_paged_decode_plan": (_i, [_p, _i, _p, _i, _i, _i, _i, _i, _p, _sz, _p]),
+    "fe_paged_decode_planned": (_i, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i, _p, _i, _p, _p, _sz,
+                                     _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p]),
     "fe_paged_decode_noalloc": (_i, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i, _p, _i, _p,
                                      _i, _i, _i, _i, _i, _f, _i, _p]),
     "fe_paged_decode_shared_prefix_workspace_size": (_sz, [_i, _i, _i, _i, _i, _i, _i]),

@@ -88,7 +88,21 @@ struct DecodeArgs {
   float scale_log2;  // softmax scale * log2(e)
   int nwg;           // balanced kernel: workgroups sharing the tile order (= grid size)
   int states;        // balanced kernel: parked-state slots in LDS
+  // decode plan (fe_paged_decode_plan): per workgroup item the piece header
+  // [kPlanHdr ints], then per item, wave and lane the pool row of the lane's
+  // tile; null for the unplanned decode
+  int* plan;
 };
+
+// The decode plan of one step: items = target + 2 * batch (the grid of the
+// piece kernel over kv_heads), a header per item -- the Piece fields b, id,
+// split, nsplit, L, tok0, tok_begin, tok_end; b = -1 for an item without a
+// piece, whose id field is then the row it zero-fills when inactive -- and
+// the tile list of each of its four waves (lane k: pool row of tile k).
+constexpr int kPlanHdr = 8;
+inline size_t plan_bytes(int items) {
+  return (size_t)items * (kPlanHdr + kWaves * kWave) * sizeof(int32_t);
+}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kSc1 = 16;  // buffer-instruction cache policy: sc1 (device-coherent)
@@ -202,7 +216,46 @@ __device__ __forceinline__ void setup_core(Core& core, const DecodeArgs& a, cons
   core.stage = stage;
 }
 
-template <int D, bool PAGE16>
+// Tile list of wave w of piece pc (block sizes that are multiples of 16):
+// lane k < ntiles gets the pool row (block * BS + offset) of the first key of
+// the wave's tile k, i.e. of piece tile w + 4k.
+__device__ __forceinline__ int tile_list_row(const DecodeArgs& a, const Piece& pc, int w) {
+  const int lane = lane_id();
+  const int t_first = pc.tok_begin / kTile + w;
+  const int t_end = (pc.tok_end + kTile - 1) / kTile;
+  const int ntiles = t_first < t_end ? (t_end - t_first + kWaves - 1) / kWaves : 0;
+  const int tok = (t_first + lane * kWaves) * kTile;
+  int blk = 0;
+  if (lane < ntiles) blk = clamp_block(a.tables[(int64_t)pc.b * a.W + (tok >> a.bs_log2)], a.NB);
+  return blk * a.BS + (tok & (a.BS - 1));
+}
+
+// The decode plan: workgroup `item` (256 threads) finds its piece as the piece
+// kernel would and writes the header and its four waves' tile lists.
+__global__ __launch_bounds__(kThreads) void decode_plan_kernel(const DecodeArgs a) {
+  const int item = blockIdx.x;
+  const int items = a.target + 2 * a.B;
+  Piece pc;
+  int total = 0;
+  const bool found = find_piece(a.ctx, nullptr, a.B, a.max_len, a.target, item, pc, total);
+  int* hdr = a.plan + (int64_t)item * kPlanHdr;
+  if (threadIdx.x == 0) {
+    hdr[0] = found ? pc.b : -1;
+    hdr[1] = found ? pc.id : item - total;
+    hdr[2] = found ? pc.split : 0;
+    hdr[3] = found ? pc.nsplit : 0;
+    hdr[4] = found ? pc.L : 0;
+    hdr[5] = found ? pc.tok0 : 0;
+    hdr[6] = found ? pc.tok_begin : 0;
+    hdr[7] = found ? pc.tok_end : 0;
+  }
+  if (!found) return;
+  const int w = threadIdx.x / kWave;
+  a.plan[(int64_t)items * kPlanHdr + ((int64_t)item * kWaves + w) * kWave + lane_id()] =
+      tile_list_row(a, pc, w);
+}
+
+template <int D, bool PAGE16, bool PLANNED = false>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(PAGE16 ? FE_DECODE_WAVES_PER_EU : 2, 8)))
 void piece_decode_kernel(const DecodeArgs a) {
@@ -211,11 +264,34 @@ void piece_decode_kernel(const DecodeArgs a) {
 
   const int h = blockIdx.x % a.Hkv;
   const int item = blockIdx.x / a.Hkv;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   Piece pc;
-  int total = 0;
-  if (!find_piece(a.ctx, a.tok0, a.B, a.max_len, a.target, item, pc, total)) {
+  int planned_row = 0;
+  bool found;
+  int spare_row;
+  if constexpr (PLANNED) {
+    // the header and this lane's tile row come from the plan, both loads in flight at once
+    const int* hdr = a.plan + (int64_t)item * kPlanHdr;
+    planned_row = a.plan[(int64_t)(a.target + 2 * a.B) * kPlanHdr +
+                         ((int64_t)item * kWaves + w) * kWave + lane_id()];
+    pc.b = __builtin_amdgcn_readfirstlane(hdr[0]);
+    pc.id = __builtin_amdgcn_readfirstlane(hdr[1]);
+    pc.split = __builtin_amdgcn_readfirstlane(hdr[2]);
+    pc.nsplit = __builtin_amdgcn_readfirstlane(hdr[3]);
+    pc.L = __builtin_amdgcn_readfirstlane(hdr[4]);
+    pc.tok0 = __builtin_amdgcn_readfirstlane(hdr[5]);
+    pc.tok_begin = __builtin_amdgcn_readfirstlane(hdr[6]);
+    pc.tok_end = __builtin_amdgcn_readfirstlane(hdr[7]);
+    found = pc.b >= 0;
+    spare_row = pc.id;
+  } else {
+    int total = 0;
+    found = find_piece(a.ctx, a.tok0, a.B, a.max_len, a.target, item, pc, total);
+    spare_row = item - total;
+  }
+  if (!found) {
     // spare workgroup: zero rows of inactive sequences
-    const int b = item - total;
+    const int b = spare_row;
     if (b < a.B && seq_len(a.ctx, b, a.max_len) == 0) {
       for (int e = threadIdx.x; e < a.G * D; e += kThreads)
         a.out[((int64_t)b * a.Hq + h * a.G) * D + e] = (f16)0.f;
@@ -224,7 +300,6 @@ void piece_decode_kernel(const DecodeArgs a) {
   }
   using Lds = PieceLds<D>;
 
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = lane_id();
   const int g = lane >> 4;
   const int n = lane & 15;
@@ -259,10 +334,11 @@ void piece_decode_kernel(const DecodeArgs a) {
     core.ntiles = ntiles;
     {
       const int tok = (t_first + lane * kWaves) * kTile;
-      int blk = 0;
-      if (lane < ntiles) blk = clamp_block(a.tables[(int64_t)b * a.W + (tok >> a.bs_log2)], a.NB);
       const int rem = pc.tok_end - tok;
-      core.row_vec = blk * a.BS + (tok & (a.BS - 1));
+      if constexpr (PLANNED)
+        core.row_vec = planned_row;
+      else
+        core.row_vec = tile_list_row(a, pc, w);
       core.rows_vec = lane < ntiles ? (rem < kTile ? rem : kTile) : 0;
     }
     core.new_tile = -1;
@@ -316,17 +392,18 @@ void piece_decode_kernel(const DecodeArgs a) {
   // conflict-free); wave w then combines output tiles [w*XW, (w+1)*XW) of all
   // four in the register layout of the loop: lane (g, n) holds
   // O[head n][16x + 4g + i], so the per-head scale factors are per lane.
+  constexpr int XW = C::NX / kWaves;  // output tiles per wave
+  f32x4 ox[XW];
+  float M = kNegInf, den = 0.f;
   {
 #pragma unroll
     for (int x = 0; x < C::NX; ++x) park[(w * C::NX + x) * kWave + lane] = o[x];
     park_m[w * kWave + lane] = m_run;
     park_l[w * kWave + lane] = l_tot;
     __syncthreads();
-    float M = kNegInf;
 #pragma unroll
     for (int v = 0; v < kWaves; ++v) M = fmaxf(M, park_m[v * kWave + lane]);
     float sc[kWaves];
-    float den = 0.f;
 #pragma unroll
     for (int v = 0; v < kWaves; ++v) {
       const float mv = park_m[v * kWave + lane];
@@ -334,8 +411,6 @@ void piece_decode_kernel(const DecodeArgs a) {
       den += sc[v] * park_l[v * kWave + lane];
     }
     const float inv = 1.f / den;
-    constexpr int XW = C::NX / kWaves;  // output tiles per wave
-    f32x4 ox[XW];
 #pragma unroll
     for (int xi = 0; xi < XW; ++xi) {
       const int x = w * XW + xi;
@@ -344,41 +419,43 @@ void piece_decode_kernel(const DecodeArgs a) {
       for (int v = 0; v < kWaves; ++v) acc += sc[v] * park[(v * C::NX + x) * kWave + lane];
       ox[xi] = acc * inv;
     }
-    if (n < G) {
-      const int hq = h * G + n;
-      if (!split) {
-        f16* orow = a.out + ((int64_t)b * a.Hq + hq) * D + 4 * g;
-#pragma unroll
-        for (int xi = 0; xi < XW; ++xi)
-          *reinterpret_cast<f16x4*>(orow + 16 * (w * XW + xi)) =
-              f16x4{(f16)ox[xi][0], (f16)ox[xi][1], (f16)ox[xi][2], (f16)ox[xi][3]};
-      } else {
-        // device-coherent (sc1) 16-byte stores of this piece's partial output
-        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-            a.ws_o + ((int64_t)pc.id * a.Hq + h * G) * D, 0, G * D * (int)sizeof(float),
-            0x00020000);
-        const uint32_t off = (uint32_t)((n * D + 4 * g) * sizeof(float));
-#pragma unroll
-        for (int xi = 0; xi < XW; ++xi)
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(u32x4, ox[xi]), r,
-              off + 16 * (w * XW + xi) * (uint32_t)sizeof(float), 0, kSc1);
-        if (w == 0 && g == 0) store_coherent(a.ws_lse + (int64_t)pc.id * a.Hq + hq, M + log2f(den));
-      }
-    }
   }
-  if (!split) return;
-
-  // ---- split-K: the last piece of (b, h) to finish merges all pieces ----
+  const int hq = h * G + (n < G ? n : G - 1);
+  if (!split) {
+    if (n < G) {
+      f16* orow = a.out + ((int64_t)b * a.Hq + hq) * D + 4 * g;
+#pragma unroll
+      for (int xi = 0; xi < XW; ++xi)
+        *reinterpret_cast<f16x4*>(orow + 16 * (w * XW + xi)) =
+            f16x4{(f16)ox[xi][0], (f16)ox[xi][1], (f16)ox[xi][2], (f16)ox[xi][3]};
+    }
+    return;
+  }
+  // device-coherent (sc1) 16-byte stores of this piece's partial output and LSE
+  auto store_partial = [&]() __attribute__((always_inline)) {
+    if (n >= G) return;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        a.ws_o + ((int64_t)pc.id * a.Hq + h * G) * D, 0, G * D * (int)sizeof(float), 0x00020000);
+    const uint32_t off = (uint32_t)((n * D + 4 * g) * sizeof(float));
+#pragma unroll
+    for (int xi = 0; xi < XW; ++xi)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ox[xi]), r,
+                                             off + 16 * (w * XW + xi) * (uint32_t)sizeof(float),
+                                             0, kSc1);
+    if (w == 0 && g == 0) store_coherent(a.ws_lse + (int64_t)pc.id * a.Hq + hq, M + log2f(den));
+  };
+  // ---- split-K: every piece stores its partial and waits for it before its
+  // ticket; the last piece of (b, h) to finish merges them all ----
+  int* const ticket = a.tickets + b * a.Hkv + h;
+  store_partial();
   wait_stores();  // this wave's partials are complete at the device-coherent level
   __syncthreads();
   if (threadIdx.x == 0)
-    *flag = __hip_atomic_fetch_add(a.tickets + b * a.Hkv + h, 1, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT) == pc.nsplit - 1;
+    *flag = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            pc.nsplit - 1;
   __syncthreads();
   if (!*flag) return;
-  if (threadIdx.x == 0)
-    __hip_atomic_store(a.tickets + b * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   merge_pieces<D>(a, b, h, pc.id - pc.split, pc.nsplit, pc.tok0 > 0);
 }
 
@@ -1130,7 +1207,10 @@ int launch_decode(const DecodeArgs& a, hipStream_t stream) {
     return FE_LAUNCH_STATUS();
   }
   const dim3 grid((a.target + 2 * a.B) * a.Hkv);
-  if (a.BS % kTile == 0)
+  if (a.plan != nullptr)
+    hipLaunchKernelGGL((piece_decode_kernel<D, true, true>), grid, dim3(kThreads),
+                       PieceLds<D>::bytes, stream, a);
+  else if (a.BS % kTile == 0)
     hipLaunchKernelGGL((piece_decode_kernel<D, true>), grid, dim3(kThreads), PieceLds<D>::bytes,
                        stream, a);
   else
@@ -1162,7 +1242,8 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
                 int num_blocks, const int32_t* block_tables, int table_stride,
                 const int32_t* context_lens, void* workspace, size_t workspace_bytes, int batch,
                 int num_q_heads, int kv_heads, int head_dim, int block_size, float scale,
-                int target_splits, CascadePrefix* cascade, hipStream_t stream) {
+                int target_splits, CascadePrefix* cascade, hipStream_t stream,
+                const void* plan = nullptr, size_t plan_len = 0) {
   FE_CHECK_ARG(batch >= 0 && num_q_heads > 0 && kv_heads > 0 && num_blocks > 0 &&
                table_stride > 0 && target_splits >= 0);
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
@@ -1235,6 +1316,13 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   // partials inside the same region of the workspace
   a.nwg = 0;
   a.states = 0;
+  a.plan = nullptr;
+  if (plan != nullptr) {
+    // the planned piece kernel: tile lists need block sizes that are multiples of 16
+    if (cascade || block_size % kTile != 0) return FE_ERR_UNSUPPORTED;
+    if (plan_len < plan_bytes(target + 2 * batch) || !aligned16(plan)) return FE_ERR_WORKSPACE;
+    a.plan = (int*)plan;
+  }
   if (cascade) {
     const BalancedPlan bp =
         head_dim == 64 ? plan_balanced<64>(batch, kv_heads, G, block_size, max_len, need)
@@ -1294,6 +1382,60 @@ extern "C" int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
                      num_blocks, block_tables, table_stride, context_lens, workspace,
                      workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
                      target_splits, nullptr, (hipStream_t)stream);
+}
+
+extern "C" size_t fe_paged_decode_plan_size(int batch, int kv_heads, int max_context,
+                                            int target_splits) {
+  if (batch < 0 || kv_heads <= 0 || max_context < 0 || target_splits < 0) return 0;
+  return plan_bytes(effective_target(batch, kv_heads, max_context, target_splits) + 2 * batch);
+}
+
+extern "C" int fe_paged_decode_plan(const int32_t* block_tables, int table_stride,
+                                    const int32_t* context_lens, int num_blocks, int batch,
+                                    int kv_heads, int block_size, int target_splits, void* plan,
+                                    size_t plan_len, fe_stream_t stream) {
+  FE_CHECK_ARG(batch >= 0 && kv_heads > 0 && num_blocks > 0 && table_stride > 0 &&
+               target_splits >= 0);
+  const int bs_log2 = log2_exact(block_size);
+  if (bs_log2 < 0 || block_size % kTile != 0) return FE_ERR_UNSUPPORTED;
+  if ((int64_t)table_stride * block_size > 262144) return FE_ERR_UNSUPPORTED;
+  if (batch == 0) return FE_OK;
+  FE_CHECK_ARG(block_tables && context_lens);
+  const int max_len = table_stride * block_size;
+  const int target = effective_target(batch, kv_heads, max_len, target_splits);
+  if (plan == nullptr || plan_len < plan_bytes(target + 2 * batch) || !aligned16(plan))
+    return FE_ERR_WORKSPACE;
+  DecodeArgs a{};
+  a.tables = block_tables;
+  a.ctx = context_lens;
+  a.W = table_stride;
+  a.B = batch;
+  a.Hkv = kv_heads;
+  a.BS = block_size;
+  a.bs_log2 = bs_log2;
+  a.NB = num_blocks;
+  a.target = target;
+  a.max_len = max_len;
+  a.plan = (int*)plan;
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(target + 2 * batch), dim3(kThreads), 0,
+                     (hipStream_t)stream, a);
+  return FE_LAUNCH_STATUS();
+}
+
+extern "C" int fe_paged_decode_planned(const void* q, int64_t q_batch_stride, void* out,
+                                       const void* k_new, const void* v_new,
+                                       int64_t new_batch_stride, void* k_pool, void* v_pool,
+                                       int num_blocks, const int32_t* block_tables,
+                                       int table_stride, const int32_t* context_lens,
+                                       void* workspace, size_t workspace_bytes, int batch,
+                                       int num_q_heads, int kv_heads, int head_dim,
+                                       int block_size, float scale, int target_splits,
+                                       const void* plan, size_t plan_len, fe_stream_t stream) {
+  if (plan == nullptr) return FE_ERR_INVALID_ARGUMENT;
+  return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
+                     num_blocks, block_tables, table_stride, context_lens, workspace,
+                     workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
+                     target_splits, nullptr, (hipStream_t)stream, plan, plan_len);
 }
 
 extern "C" size_t fe_paged_decode_shared_prefix_workspace_size(int batch, int num_q_heads,

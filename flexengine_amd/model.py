@@ -14,9 +14,10 @@ no network for checkpoints).
   Returns the last-token logits of each chunk.
 * decode_static(input_ids, positions, block_tables, active_mask, cache) -- the
   graph-compatible one-token step of qwen2.py:138-186 over fixed padded batch
-  tensors; per layer the page write of the new token and the attention run in
-  one fe_paged_decode launch.  Inactive rows leave the pool untouched and give
-  zero logits.
+  tensors; one fe_paged_decode_plan launch per step (the split-K partition and
+  block rows, the same for every layer), then per layer the page write of the
+  new token and the attention in one fe_paged_decode_planned launch.  Inactive
+  rows leave the pool untouched and give zero logits.
 
 RoPE follows qwen2.py:15-17,46,73-77: inv_freq = theta^(-2i/D), the half-split
 rotate_half, cos/sin cast to the activation dtype.  RMSNorm computes in fp32
@@ -201,20 +202,25 @@ class Qwen2Model:
         # (paged_attention.py:115,131,138): length = position + 1, 0 for inactive rows
         ctx = attention.context_lens_from_positions(positions, active)
         tables = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
+        tables = tables.contiguous()
+        # the decode plan (split-K partition and block rows) of this step, shared by
+        # every layer: the tables and lengths are the same for all of them
+        nb, bs, hkv = cache.k[0].shape[0], cache.k[0].shape[1], cache.k[0].shape[2]
+        plan = ops.paged_decode_plan(tables, ctx, nb, hkv, bs) if bs % 16 == 0 else None
         x = self.embed.index_select(0, input_ids)
         h, _ = ops.rmsnorm(x, self.layer_weights[0].input_norm, self.cfg.rms_norm_eps)
         if batch <= ops.SKINNY_MAX_ROWS and self.cfg.hidden_size % 32 == 0:
-            logits = self._decode_layers_fused(x, h, positions, tables, ctx, cache)
+            logits = self._decode_layers_fused(x, h, positions, tables, ctx, cache, plan)
         else:
             for layer, lw in enumerate(self.layer_weights):
                 q, k, v = self._qkv(h, lw, positions)
                 attn = ops.paged_decode(q, cache.k[layer], cache.v[layer], tables, ctx,
-                                        scale=self.scale, k_new=k, v_new=v)
+                                        scale=self.scale, k_new=k, v_new=v, plan=plan)
                 h = self._after_attention(x, attn, lw, self._next_norm(layer))
             logits = self._logits(h)
         return logits * active.to(logits.dtype)[:, None]
 
-    def _decode_layers_fused(self, x, h, positions, tables, ctx, cache) -> torch.Tensor:
+    def _decode_layers_fused(self, x, h, positions, tables, ctx, cache, plan=None) -> torch.Tensor:
         """The decode layers at decode batch sizes on the fused projections: five
         launches per layer -- q/k/v + bias + RoPE, the paged decode with the page
         write, o + residual + RMSNorm, gate/up + SiLU, down + residual + the next
@@ -233,7 +239,7 @@ class Qwen2Model:
             q, k, v = ops.gemm_rope(h, lw.w_qkv, lw.b_qkv, positions, self.inv_freq,
                                     self.nq, self.nkv, self.dim)
             attn = ops.paged_decode(q, cache.k[layer], cache.v[layer], tables, ctx, scale=self.scale,
-                                    k_new=k, v_new=v)
+                                    k_new=k, v_new=v, plan=plan)
             o_in = attn.reshape(rows, self.nq * self.dim)
             if fused_norm:
                 r1, h2 = ops.gemm_resid_rmsnorm(o_in, lw.w_o, res, lw.post_norm, eps)

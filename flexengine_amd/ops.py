@@ -9,6 +9,7 @@ the workspace / output buffers or lets them come from the graph pool.
 from __future__ import annotations
 
 import contextlib
+from dataclasses import dataclass
 import math
 
 import torch
@@ -250,28 +251,76 @@ def _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_
     return dev, nb, bs, hkv, d, batch, hq, block_tables, context_lens, new_stride, out, scale
 
 
+@dataclass(frozen=True)
+class DecodePlan:
+    """A decode step's split-K partition and block rows (fe_paged_decode_plan),
+    for the block_tables / context_lens tensors it was computed from."""
+    buffer: torch.Tensor
+    tables_ptr: int
+    lens_ptr: int
+    shape: tuple  # (batch, kv_heads, table width, block size, num_blocks, target_splits)
+
+
+def paged_decode_plan(block_tables: torch.Tensor, context_lens: torch.Tensor, num_blocks: int,
+                      kv_heads: int, block_size: int, *, target_splits: int = 0,
+                      out: DecodePlan | None = None) -> DecodePlan:
+    """Computes the plan every layer's paged_decode(..., plan=) of one decode step
+    reuses (the tables and lengths must not change between those calls).
+    `out` reuses an earlier plan's buffer for the same sizes (graph capture)."""
+    dev = _require_gpu(block_tables, context_lens)
+    block_tables = _int32(block_tables, "block_tables")
+    context_lens = _int32(context_lens, "context_lens")
+    batch, width = block_tables.shape
+    shape = (batch, int(kv_heads), width, int(block_size), int(num_blocks), int(target_splits))
+    need = int(_lib.load().fe_paged_decode_plan_size(batch, int(kv_heads), width * block_size,
+                                                      int(target_splits)))
+    if out is not None:
+        if out.shape != shape:
+            raise ValueError(f"plan buffer is for sizes {out.shape}, not {shape}")
+        buffer = out.buffer
+    else:
+        buffer = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    _lib.call("fe_paged_decode_plan", block_tables.data_ptr(), width, context_lens.data_ptr(),
+              int(num_blocks), batch, int(kv_heads), int(block_size), int(target_splits),
+              buffer.data_ptr(), buffer.numel(), _stream(dev))
+    return DecodePlan(buffer, block_tables.data_ptr(), context_lens.data_ptr(), shape)
+
+
 def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                  block_tables: torch.Tensor, context_lens: torch.Tensor, *,
                  scale: float | None = None, k_new: torch.Tensor | None = None,
                  v_new: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                 workspace: torch.Tensor | None = None, target_splits: int = 0) -> torch.Tensor:
+                 workspace: torch.Tensor | None = None, target_splits: int = 0,
+                 plan: DecodePlan | None = None) -> torch.Tensor:
     """Single-token paged decode attention over one layer's pools.
 
     q [B, Hq, D] fp16 (rows may be strided, heads contiguous); pools
     [NB, BS, Hkv, D]; block_tables int32 [B, W]; context_lens int32 [B]
     (0 = inactive row -> zeros).  With k_new/v_new ([B, Hkv, D]) the new token's
     K/V are written to the pool at position context_lens-1 in the same launch.
+    With `plan` (paged_decode_plan on these block_tables / context_lens) the
+    launch reads the partition and first block rows from it
+    (fe_paged_decode_planned); same results.
     """
     (dev, nb, bs, hkv, d, batch, hq, block_tables, context_lens, new_stride, out,
      scale) = _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_new, out)
     need = decode_workspace_bytes(batch, hq, d, block_tables.shape[1] * bs, target_splits)
     if workspace is None:
         workspace = decode_workspace(dev, need)
-    _lib.call("fe_paged_decode", q.data_ptr(), q.stride(0), out.data_ptr(), _ptr(k_new),
-              _ptr(v_new), new_stride, k_pool.data_ptr(), v_pool.data_ptr(), nb,
-              block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(),
-              workspace.data_ptr(), workspace.numel() * workspace.element_size(), batch, hq, hkv,
-              d, bs, float(scale), int(target_splits), _stream(dev))
+    args = (q.data_ptr(), q.stride(0), out.data_ptr(), _ptr(k_new), _ptr(v_new), new_stride,
+            k_pool.data_ptr(), v_pool.data_ptr(), nb, block_tables.data_ptr(),
+            block_tables.shape[1], context_lens.data_ptr(), workspace.data_ptr(),
+            workspace.numel() * workspace.element_size(), batch, hq, hkv, d, bs, float(scale),
+            int(target_splits))
+    if plan is None:
+        _lib.call("fe_paged_decode", *args, _stream(dev))
+        return out
+    shape = (batch, hkv, block_tables.shape[1], bs, nb, int(target_splits))
+    if plan.shape != shape or plan.tables_ptr != block_tables.data_ptr() or \
+            plan.lens_ptr != context_lens.data_ptr():
+        raise ValueError("the plan was computed for other block_tables / context_lens or sizes")
+    _lib.call("fe_paged_decode_planned", *args, plan.buffer.data_ptr(), plan.buffer.numel(),
+              _stream(dev))
     return out
 
 

@@ -184,6 +184,43 @@ int fe_paged_decode(const void* q, int64_t q_batch_stride, void* out,
                     fe_stream_t stream);
 
 /*
+ * Decode plan of one step, shared by every layer's fe_paged_decode_planned:
+ * the split-K partition of the sequences (from context_lens) and each
+ * workgroup's block rows (from block_tables), which fe_paged_decode otherwise
+ * derives at the start of every launch.  A model's decode step computes it
+ * once and its 28 layers reuse it, since tables and lengths do not change
+ * between layers.  No counterpart in the reference: its decode
+ * (src/flexengine/inference/kernels/paged_attention.py:99-155) has no split-K
+ * partition to plan.  Block sizes must be multiples of 16.
+ * fe_paged_decode_plan_size: bytes of the plan for these sizes (the same
+ * table capacity max_context = table_stride * block_size and target_splits
+ * as the decode calls).
+ */
+size_t fe_paged_decode_plan_size(int batch, int kv_heads, int max_context, int target_splits);
+int fe_paged_decode_plan(const int32_t* block_tables, int table_stride,
+                         const int32_t* context_lens, int num_blocks, int batch, int kv_heads,
+                         int block_size, int target_splits, void* plan, size_t plan_bytes,
+                         fe_stream_t stream);
+
+/*
+ * fe_paged_decode with the partition and first block rows read from `plan`
+ * (written by fe_paged_decode_plan on the same block_tables, table_stride,
+ * context_lens, num_blocks, batch, kv_heads, block_size and target_splits,
+ * earlier on the stream): same results, one dependent load fewer before the
+ * first K/V loads.  A plan from other sizes or tables gives wrong results;
+ * a plan_bytes below fe_paged_decode_plan_size returns FE_ERR_WORKSPACE.
+ */
+int fe_paged_decode_planned(const void* q, int64_t q_batch_stride, void* out,
+                            const void* k_new, const void* v_new, int64_t new_batch_stride,
+                            void* k_pool, void* v_pool, int num_blocks,
+                            const int32_t* block_tables, int table_stride,
+                            const int32_t* context_lens,
+                            void* workspace, size_t workspace_bytes,
+                            int batch, int num_q_heads, int kv_heads, int head_dim,
+                            int block_size, float scale, int target_splits,
+                            const void* plan, size_t plan_bytes, fe_stream_t stream);
+
+/*
  * fe_paged_decode without a workspace argument, for callers that cannot
  * allocate device memory: code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc.  No counterpart in the reference.

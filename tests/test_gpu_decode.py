@@ -513,3 +513,66 @@ def test_balanced_cascade_repeated_calls_are_identical_and_share_the_workspace()
         if first is None:
             first = got
         assert (first == got).all(), "results differ between identical calls"
+
+
+# --------------------------------------------------------------------------------------
+# decode plan (fe_paged_decode_plan / fe_paged_decode_planned): one plan per decode step,
+# reused by every layer; results must be bit-identical to the unplanned launch
+# --------------------------------------------------------------------------------------
+
+def _planned_cases():
+    c2 = workloads.c2_workload()
+    lens = [0, 1, 15, 16, 17, 200, 0, 1023, 4096, 64]  # inactive rows, tile and piece edges
+    edge = workloads.make_decode_workload("edges", 91, len(lens), 12, 2, 128, lens,
+                                          width=256, with_new_kv=True)
+    c1 = workloads.c1_workload()
+    big = workloads.make_decode_workload("bs32", 93, 5, 16, 2, 128, [3000, 17, 512, 0, 9000],
+                                         block_size=32, with_new_kv=True)
+    return [c2, edge, c1, big]
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_planned_decode_is_bit_identical_and_reusable(case):
+    w = _planned_cases()[case]
+    print(f"planned decode case {w.name}", flush=True)
+    d = w.to(DEV)
+    nb, bs, hkv = d.k_pool.shape[0], d.k_pool.shape[1], d.k_pool.shape[2]
+    plan = ops.paged_decode_plan(d.block_tables, d.context_lens, nb, hkv, bs)
+    # three "layers": own pools and queries, the same tables and lengths
+    for layer in range(3):
+        g = torch.Generator().manual_seed(100 * case + layer)
+        kp = torch.randn(d.k_pool.shape, generator=g).half().to(DEV)
+        vp = torch.randn(d.v_pool.shape, generator=g).half().to(DEV)
+        q = torch.randn(d.q.shape, generator=g).half().to(DEV)
+        kn = vn = None
+        if d.k_new is not None:
+            kn = torch.randn(d.k_new.shape, generator=g).half().to(DEV)
+            vn = torch.randn(d.v_new.shape, generator=g).half().to(DEV)
+        kp2, vp2 = kp.clone(), vp.clone()
+        ref = ops.paged_decode(q, kp, vp, d.block_tables, d.context_lens, k_new=kn, v_new=vn)
+        got = ops.paged_decode(q, kp2, vp2, d.block_tables, d.context_lens, k_new=kn, v_new=vn,
+                               plan=plan)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"{w.name} layer {layer}: planned output differs"
+        assert torch.equal(kp2, kp) and torch.equal(vp2, vp), f"{w.name}: page write differs"
+    # and against the oracle for the workload's own pools
+    out = ops.paged_decode(d.q, d.k_pool.clone(), d.v_pool.clone(), d.block_tables,
+                           d.context_lens, k_new=d.k_new, v_new=d.v_new, plan=plan)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(out.cpu().numpy(), exp, what=f"planned {w.name}")
+
+
+def test_planned_decode_rejects_a_foreign_plan():
+    w = workloads.c1_workload()
+    d = w.to(DEV)
+    nb, bs, hkv = d.k_pool.shape[0], d.k_pool.shape[1], d.k_pool.shape[2]
+    plan = ops.paged_decode_plan(d.block_tables, d.context_lens, nb, hkv, bs)
+    other = d.context_lens.clone()
+    with pytest.raises(ValueError, match="other block_tables"):
+        ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, other, plan=plan)
+    small = torch.empty(16, dtype=torch.uint8, device=DEV)
+    lib = _lib.load()
+    rc = lib.fe_paged_decode_plan(d.block_tables.data_ptr(), d.block_tables.shape[1],
+                                  d.context_lens.data_ptr(), nb, d.q.shape[0], hkv, bs, 0,
+                                  small.data_ptr(), small.numel(), None)
+    assert rc == _lib.FE_ERR_WORKSPACE
