@@ -67,6 +67,8 @@ def parse_args(argv=None):
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--pools", type=int, default=8, help="rotating KV pool copies (MALL flush)")
     p.add_argument("--target-splits", type=int, default=0)
+    p.add_argument("--dtype", choices=("f16", "bf16"), default="f16",
+                   help="element type of q / K / V (the configurations are quoted in f16)")
     p.add_argument("--unplanned", action="store_true",
                    help="time fe_paged_decode (no shared per-step plan)")
     p.add_argument("--cpu-seconds", type=float, default=6.0,
@@ -255,6 +257,9 @@ def main(argv=None) -> int:
     torch.cuda.set_device(dev)
     w = workloads.c2_workload()
     d = w.to(dev)
+    if args.dtype == "bf16":
+        for name in ("q", "k_pool", "v_pool", "k_new", "v_new"):
+            setattr(d, name, getattr(d, name).float().to(torch.bfloat16))
     n_pool = max(1, args.pools)
     pools = [(d.k_pool, d.v_pool)] + [(d.k_pool.clone(), d.v_pool.clone())
                                       for _ in range(n_pool - 1)]
@@ -330,6 +335,7 @@ def main(argv=None) -> int:
     c5 = None if args.no_c5 else c5_decode(args.c5_steps)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 
+    elem, sfx = ("Bf16", "_bf16") if args.dtype == "bf16" else ("Fp16", "")
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -341,7 +347,7 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": args.dtype,
         "data": "synthetic (seeded N(0,1) q/K/V, random block tables; random-init weights for c5)",
         "config": {
             "workload": "C2: paged decode attention + KV page write, one layer, Qwen2.5-1.5B heads "
@@ -366,11 +372,12 @@ def main(argv=None) -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "kernel": ("piece_decode_kernel<128, true, true> (fe_paged_decode_planned: page "
-                       "write + split-K attention + in-kernel LSE merge, one launch; achieved "
-                       "includes 1/28 of decode_plan_kernel per launch)") if planned else
-                      "piece_decode_kernel<128, true> (fe_paged_decode: page write + split-K "
-                      "attention + in-kernel LSE merge, one launch)",
+            "kernel": (f"piece_decode_kernel<128, true, true, {elem}> (fe_paged_decode_planned"
+                       f"{sfx}: page write + split-K attention + in-kernel LSE merge, one "
+                       "launch; achieved includes 1/28 of decode_plan_kernel per launch)")
+                      if planned else
+                      f"piece_decode_kernel<128, true, false, {elem}> (fe_paged_decode{sfx}: "
+                      "page write + split-K attention + in-kernel LSE merge, one launch)",
             "us_per_launch": round(per_launch_ms * 1e3, 3),
         },
         "c5": c5,

@@ -54,6 +54,11 @@ SIGNATURES: dict[str, tuple] = {
     "fe_prefill_paged": (_i, [_p, _p, _p, _p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _i,
                               _f, _p, _sz, _p]),
     "fe_prefill_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
+}
+# the bf16 forms take the fp16 entry points' arguments
+for _name in ("fe_paged_decode", "fe_paged_decode_planned", "fe_prefill_paged"):
+    SIGNATURES[_name + "_bf16"] = SIGNATURES[_name]
+SIGNATURES |= {
     # include/flexengine_amd_model.h
     "fe_rmsnorm": (_i, [_p, _i, _p, _p, _p, _p, _i, _i, _f, _p]),
     "fe_rope_qkv": (_i, [_p, _i64, _i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),

@@ -1,6 +1,6 @@
 """Per-configuration timings of the attention kernels (configs C1, C3, C4).
 
-    python -m flexengine_amd.bench_attention [--iters 50] [--configs c1,c3,c4]
+    python -m flexengine_amd.bench_attention [--iters 50] [--configs c1,c3,c4] [--dtype bf16]
 
 bench.py measures the headline config (C2); this script times the others the
 same way -- inputs resident in HBM, several rotating copies of the KV pool so
@@ -16,6 +16,8 @@ stream -- and prints one JSON line per config:
   in GB/s, and the whole step.
 
 Calls are replayed from a HIP graph, so each figure is GPU time per call.
+`--dtype bf16` runs the bf16 entry points on the same values rounded to bf16
+(C3's shared-prefix decode has no bf16 form and is skipped then).
 """
 from __future__ import annotations
 
@@ -57,13 +59,27 @@ def _timed(fn, iters: int, variants: int) -> float:
     return start.elapsed_time(end) / 1e3 / (reps * variants)
 
 
+def _cast(w, dtype):
+    """The workload (already on the device) with its 16-bit tensors in `dtype`."""
+    if dtype == torch.float16:
+        return w
+    for name in ("q", "k_pool", "v_pool", "k_new", "v_new"):
+        t = getattr(w, name, None)
+        if t is not None:
+            setattr(w, name, t.float().to(dtype))
+    if getattr(w, "decode", None) is not None:
+        w.decode.q = w.decode.q.float().to(dtype)
+        w.decode.k_pool, w.decode.v_pool = w.k_pool, w.v_pool
+    return w
+
+
 def _pools(w, copies: int):
     return [(w.k_pool, w.v_pool)] + [(w.k_pool.clone(), w.v_pool.clone()) for _ in range(copies - 1)]
 
 
 def bench_decode(name: str, w, iters: int, copies: int, unique_bytes: int | None = None,
-                 shared_prefix: bool = False) -> dict:
-    d = w.to("cuda:0")
+                 shared_prefix: bool = False, dtype=torch.float16) -> dict:
+    d = _cast(w.to("cuda:0"), dtype)
     pools = _pools(d, copies)
     out = torch.empty_like(d.q)
     if shared_prefix:
@@ -91,9 +107,9 @@ def bench_decode(name: str, w, iters: int, copies: int, unique_bytes: int | None
     return res
 
 
-def bench_c4(iters: int, copies: int) -> dict:
+def bench_c4(iters: int, copies: int, dtype=torch.float16) -> dict:
     w = workloads.c4_workload()
-    d = w.to("cuda:0")
+    d = _cast(w.to("cuda:0"), dtype)
     pools = _pools(d, copies)
     out = torch.empty_like(d.q)
     max_q = int((w.q_offsets[1:] - w.q_offsets[:-1]).max())
@@ -146,24 +162,29 @@ def main(argv=None) -> int:
     p.add_argument("--iters", type=int, default=200)
     p.add_argument("--copies", type=int, default=4, help="rotating KV pool copies")
     p.add_argument("--configs", default="c1,c3,c4")
+    p.add_argument("--dtype", choices=("f16", "bf16"), default="f16")
     args = p.parse_args(argv)
+    dt = torch.bfloat16 if args.dtype == "bf16" else torch.float16
     if not torch.cuda.is_available():
         print("bench_attention needs a ROCm GPU", file=sys.stderr)
         return 2
     cfgs = args.configs.split(",")
     if "c1" in cfgs:
-        print(json.dumps(bench_decode("C1", workloads.c1_workload(), args.iters, args.copies * 8)),
-              flush=True)
+        print(json.dumps(bench_decode("C1", workloads.c1_workload(), args.iters, args.copies * 8,
+                                      dtype=dt) | {"dtype": args.dtype}), flush=True)
     if "c3" in cfgs:
         w = workloads.c3_workload()
         hkv, d = w.k_pool.shape[2], w.k_pool.shape[3]
         # compulsory bytes: every distinct K/V row once, plus q and out
         unique = w.unique_tokens * 2 * hkv * d * 2 + 2 * w.q.numel() * 2
-        print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique)), flush=True)
-        print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique,
-                                      shared_prefix=True)), flush=True)
+        print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique, dtype=dt)
+                         | {"dtype": args.dtype}), flush=True)
+        if dt == torch.float16:
+            print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique,
+                                          shared_prefix=True) | {"dtype": args.dtype}), flush=True)
     if "c4" in cfgs:
-        print(json.dumps(bench_c4(args.iters, args.copies)), flush=True)
+        print(json.dumps(bench_c4(args.iters, args.copies, dt) | {"dtype": args.dtype}),
+              flush=True)
     return 0
 
 

@@ -65,7 +65,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 // the halves M[4j + l/4][l%4] (j = 0..3), M[r] being the 8 bytes addressed by
 // lane r of the group; lane (g, r) therefore addresses
 // V[key 4g + r/4][dims 16x + 4(r%4) .. +3].
-template <int D>
+template <int D, class E = Fp16>
 __device__ __forceinline__ void softmax_pv_tile(f32x4 sacc, int t0, int limit, float scale_log2,
                                                 const unsigned char* stage, float& m_run,
                                                 float& l_run, f32x4 (&o)[TileCfg<D>::NX]) {
@@ -95,17 +95,17 @@ __device__ __forceinline__ void softmax_pv_tile(f32x4 sacc, int t0, int limit, f
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = exp2_fast(sv[i] - m_use);
   l_run += (p[0] + p[1]) + (p[2] + p[3]);
-  const f16x4 pb = {(f16)p[0], (f16)p[1], (f16)p[2], (f16)p[3]};
+  const f16x4 pb = to16x4<E>(p[0], p[1], p[2], p[3]);
   const unsigned char* vb = stage + (4 * g + (n >> 2)) * C::ROWB + (n & 3) * 8;
 #pragma unroll
   for (int x = 0; x < C::NX; ++x) {
     const s16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (__attribute__((address_space(3))) s16x4*)(vb + 32 * x));
-    o[x] = mfma16(__builtin_bit_cast(f16x4, raw), pb, o[x]);
+    o[x] = mma16<E>(__builtin_bit_cast(f16x4, raw), pb, o[x]);
   }
 }
 
-template <int D>
+template <int D, class E = Fp16>
 struct TileCore {
   using C = TileCfg<D>;
 
@@ -190,8 +190,8 @@ struct TileCore {
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < C::NK; ++s) {
-      sacc = mfma16(lo4(kk[s]), lo4(qv[s]), sacc);
-      sacc = mfma16(hi4(kk[s]), hi4(qv[s]), sacc);
+      sacc = mma16<E>(lo4(kk[s]), lo4(qv[s]), sacc);
+      sacc = mma16<E>(hi4(kk[s]), hi4(qv[s]), sacc);
     }
     // stage the V rows of this tile (row-major, padded pitch)
     compiler_fence();
@@ -205,7 +205,7 @@ struct TileCore {
       }
     }
     compiler_fence();
-    softmax_pv_tile<D>(sacc, t0, limit, scale_log2, stage, m_run, l_run, o);
+    softmax_pv_tile<D, E>(sacc, t0, limit, scale_log2, stage, m_run, l_run, o);
     compiler_fence();
   }
 
@@ -238,7 +238,7 @@ struct TileCore {
 // form a list held one per lane (lane k: tile k, k < 64), filled from the block
 // tables before the first load, so no table access sits between two tiles'
 // K/V loads.
-template <int D>
+template <int D, class E = Fp16>
 struct TileListCore {
   using C = TileCfg<D>;
 
@@ -344,8 +344,8 @@ struct TileListCore {
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < C::NK; ++s) {
-      sacc = mfma16(lo4(kk[s]), lo4(qv[s]), sacc);
-      sacc = mfma16(hi4(kk[s]), hi4(qv[s]), sacc);
+      sacc = mma16<E>(lo4(kk[s]), lo4(qv[s]), sacc);
+      sacc = mma16<E>(hi4(kk[s]), hi4(qv[s]), sacc);
     }
     compiler_fence();
     {
@@ -358,7 +358,7 @@ struct TileListCore {
       }
     }
     compiler_fence();
-    softmax_pv_tile<D>(sacc, 0, tile_rows(k), scale_log2, stage, m_run, l_run, o);
+    softmax_pv_tile<D, E>(sacc, 0, tile_rows(k), scale_log2, stage, m_run, l_run, o);
     compiler_fence();
   }
 

@@ -106,6 +106,52 @@ __device__ __forceinline__ f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
+// ---- 16-bit element types of the attention kernels ----------------------------
+// K, V, q and outputs are fp16 (Fp16) or bf16 (Bf16).  Either way they live in
+// 16-bit registers as raw bits (the f16x4 / f16x8 storage types): the loads,
+// LDS staging, transposing reads and page writes do not look at the values.
+// Only the MFMA that consumes them and the conversions from fp32 depend on the
+// type.
+struct Fp16 {};
+struct Bf16 {};
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// 16x16x16 MFMA (k = 16) on 16-bit operands of type E
+template <class E>
+__device__ __forceinline__ f32x4 mma16(f16x4 a, f16x4 b, f32x4 c) {
+  if constexpr (__is_same(E, Bf16))
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a),
+                                                     __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+// 16x16x32 MFMA (k = 32, gfx950) on 16-bit operands of type E
+template <class E>
+__device__ __forceinline__ f32x4 mma32(f16x8 a, f16x8 b, f32x4 c) {
+  if constexpr (__is_same(E, Bf16))
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// fp32 -> the 16-bit bits of type E (round to nearest even)
+template <class E>
+__device__ __forceinline__ f16 to16(float x) {
+  if constexpr (__is_same(E, Bf16))
+    return __builtin_bit_cast(f16, (__bf16)x);
+  else
+    return (f16)x;
+}
+template <class E>
+__device__ __forceinline__ f16x4 to16x4(float a, float b, float c, float d) {
+  return f16x4{to16<E>(a), to16<E>(b), to16<E>(c), to16<E>(d)};
+}
+template <class E>
+__device__ __forceinline__ f16x4 to16x4(f32x4 v) {
+  return to16x4<E>(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ f16x4 lo4(f16x8 v) { return f16x4{v[0], v[1], v[2], v[3]}; }
 __device__ __forceinline__ f16x4 hi4(f16x8 v) { return f16x4{v[4], v[5], v[6], v[7]}; }
 

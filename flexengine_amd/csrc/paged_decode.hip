@@ -124,7 +124,7 @@ __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)
 // common case (ns <= kMergeBatch) is one round trip to memory and no barrier.
 constexpr int kMergeBatch = 16;
 
-template <int D>
+template <int D, class E = Fp16>
 __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, int first,
                                              int ns, bool pre = false) {
   const int G = a.G;
@@ -186,8 +186,7 @@ __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, 
     }
     const float inv = 1.f / den;
     *reinterpret_cast<f16x4*>(a.out + ((int64_t)b * a.Hq + h * G) * D + e4 * 4) =
-        f16x4{(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
-              (f16)(num[3] * inv)};
+        to16x4<E>(num * inv);
   }
 }
 
@@ -255,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const DecodeArgs 
       tile_list_row(a, pc, w);
 }
 
-template <int D, bool PAGE16, bool PLANNED = false>
+template <int D, bool PAGE16, bool PLANNED = false, class E = Fp16>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(PAGE16 ? FE_DECODE_WAVES_PER_EU : 2, 8)))
 void piece_decode_kernel(const DecodeArgs a) {
@@ -323,7 +322,7 @@ void piece_decode_kernel(const DecodeArgs a) {
   f32x4 o[C::NX];
   if constexpr (PAGE16) {
     // the wave's tiles t_first, t_first + 4, ... of the piece as a tile list
-    TileListCore<D> core;
+    TileListCore<D, E> core;
     core.k_pool = a.k_pool;
     core.v_pool = a.v_pool;
     core.rs = a.Hkv * D;
@@ -368,7 +367,7 @@ void piece_decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int x = 0; x < C::NX; ++x) o[x] = core.o[x];
   } else {
-    TileCore<D> core;
+    TileCore<D, E> core;
     setup_core<D>(core, a, pc, h, smem + w * C::STAGE);
     core.k_pool = a.k_pool;
     core.v_pool = a.v_pool;
@@ -426,8 +425,7 @@ void piece_decode_kernel(const DecodeArgs a) {
       f16* orow = a.out + ((int64_t)b * a.Hq + hq) * D + 4 * g;
 #pragma unroll
       for (int xi = 0; xi < XW; ++xi)
-        *reinterpret_cast<f16x4*>(orow + 16 * (w * XW + xi)) =
-            f16x4{(f16)ox[xi][0], (f16)ox[xi][1], (f16)ox[xi][2], (f16)ox[xi][3]};
+        *reinterpret_cast<f16x4*>(orow + 16 * (w * XW + xi)) = to16x4<E>(ox[xi]);
     }
     return;
   }
@@ -456,7 +454,7 @@ void piece_decode_kernel(const DecodeArgs a) {
   __syncthreads();
   if (!*flag) return;
   if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  merge_pieces<D>(a, b, h, pc.id - pc.split, pc.nsplit, pc.tok0 > 0);
+  merge_pieces<D, E>(a, b, h, pc.id - pc.split, pc.nsplit, pc.tok0 > 0);
 }
 
 // ---- balanced decode (block sizes that are multiples of 16) ----------------------
@@ -1199,23 +1197,29 @@ BalancedPlan plan_balanced(int batch, int hkv, int G, int block_size, int max_le
   return p;
 }
 
-template <int D>
+template <int D, class E>
 int launch_decode(const DecodeArgs& a, hipStream_t stream) {
   if (a.nwg > 0) {
-    hipLaunchKernelGGL((balanced_decode_kernel<D>), dim3(a.nwg), dim3(kBThreads),
-                       BLds<D>::bytes(a.B, a.G, a.states), stream, a);
-    return FE_LAUNCH_STATUS();
+    // the balanced kernel (shared-prefix suffixes) is fp16 only; decode_impl
+    // refuses bf16 shared-prefix calls before any launch
+    if constexpr (__is_same(E, Fp16)) {
+      hipLaunchKernelGGL((balanced_decode_kernel<D>), dim3(a.nwg), dim3(kBThreads),
+                         BLds<D>::bytes(a.B, a.G, a.states), stream, a);
+      return FE_LAUNCH_STATUS();
+    } else {
+      return FE_ERR_UNSUPPORTED;
+    }
   }
   const dim3 grid((a.target + 2 * a.B) * a.Hkv);
   if (a.plan != nullptr)
-    hipLaunchKernelGGL((piece_decode_kernel<D, true, true>), grid, dim3(kThreads),
+    hipLaunchKernelGGL((piece_decode_kernel<D, true, true, E>), grid, dim3(kThreads),
                        PieceLds<D>::bytes, stream, a);
   else if (a.BS % kTile == 0)
-    hipLaunchKernelGGL((piece_decode_kernel<D, true>), grid, dim3(kThreads), PieceLds<D>::bytes,
-                       stream, a);
+    hipLaunchKernelGGL((piece_decode_kernel<D, true, false, E>), grid, dim3(kThreads),
+                       PieceLds<D>::bytes, stream, a);
   else
-    hipLaunchKernelGGL((piece_decode_kernel<D, false>), grid, dim3(kThreads), PieceLds<D>::bytes,
-                       stream, a);
+    hipLaunchKernelGGL((piece_decode_kernel<D, false, false, E>), grid, dim3(kThreads),
+                       PieceLds<D>::bytes, stream, a);
   return FE_LAUNCH_STATUS();
 }
 
@@ -1243,7 +1247,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
                 const int32_t* context_lens, void* workspace, size_t workspace_bytes, int batch,
                 int num_q_heads, int kv_heads, int head_dim, int block_size, float scale,
                 int target_splits, CascadePrefix* cascade, hipStream_t stream,
-                const void* plan = nullptr, size_t plan_len = 0) {
+                const void* plan = nullptr, size_t plan_len = 0, bool bf16 = false) {
   FE_CHECK_ARG(batch >= 0 && num_q_heads > 0 && kv_heads > 0 && num_blocks > 0 &&
                table_stride > 0 && target_splits >= 0);
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
@@ -1255,6 +1259,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
   // the shared-prefix split needs 16-token-aligned suffixes (block-size-16k path)
   if (cascade && block_size % kTile != 0) return FE_ERR_UNSUPPORTED;
+  if (cascade && bf16) return FE_ERR_UNSUPPORTED;  // shared-prefix decode: fp16 only
   if (batch == 0) return FE_OK;
   FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && context_lens);
   FE_CHECK_ARG((k_new == nullptr) == (v_new == nullptr));
@@ -1364,8 +1369,8 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     a.pre_o = c.pre_o;
     a.pre_lse = c.pre_lse;
   }
-  if (head_dim == 64) return launch_decode<64>(a, s);
-  return launch_decode<128>(a, s);
+  if (bf16) return head_dim == 64 ? launch_decode<64, Bf16>(a, s) : launch_decode<128, Bf16>(a, s);
+  return head_dim == 64 ? launch_decode<64, Fp16>(a, s) : launch_decode<128, Fp16>(a, s);
 }
 
 }  // namespace
@@ -1436,6 +1441,37 @@ extern "C" int fe_paged_decode_planned(const void* q, int64_t q_batch_stride, vo
                      num_blocks, block_tables, table_stride, context_lens, workspace,
                      workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
                      target_splits, nullptr, (hipStream_t)stream, plan, plan_len);
+}
+
+extern "C" int fe_paged_decode_bf16(const void* q, int64_t q_batch_stride, void* out,
+                                    const void* k_new, const void* v_new,
+                                    int64_t new_batch_stride, void* k_pool, void* v_pool,
+                                    int num_blocks, const int32_t* block_tables, int table_stride,
+                                    const int32_t* context_lens, void* workspace,
+                                    size_t workspace_bytes, int batch, int num_q_heads,
+                                    int kv_heads, int head_dim, int block_size, float scale,
+                                    int target_splits, fe_stream_t stream) {
+  return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
+                     num_blocks, block_tables, table_stride, context_lens, workspace,
+                     workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
+                     target_splits, nullptr, (hipStream_t)stream, nullptr, 0, true);
+}
+
+extern "C" int fe_paged_decode_planned_bf16(const void* q, int64_t q_batch_stride, void* out,
+                                            const void* k_new, const void* v_new,
+                                            int64_t new_batch_stride, void* k_pool, void* v_pool,
+                                            int num_blocks, const int32_t* block_tables,
+                                            int table_stride, const int32_t* context_lens,
+                                            void* workspace, size_t workspace_bytes, int batch,
+                                            int num_q_heads, int kv_heads, int head_dim,
+                                            int block_size, float scale, int target_splits,
+                                            const void* plan, size_t plan_len,
+                                            fe_stream_t stream) {
+  if (plan == nullptr) return FE_ERR_INVALID_ARGUMENT;
+  return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
+                     num_blocks, block_tables, table_stride, context_lens, workspace,
+                     workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
+                     target_splits, nullptr, (hipStream_t)stream, plan, plan_len, true);
 }
 
 extern "C" size_t fe_paged_decode_shared_prefix_workspace_size(int batch, int num_q_heads,

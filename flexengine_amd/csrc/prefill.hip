@@ -871,7 +871,7 @@ constexpr int kMergeGrid = 4;  // merge workgroups per stream-K workgroup: one t
                                // the usual case (at most one split unit per range)
 constexpr int kMergeDescPerThread = 4;  // descriptors a thread counts (nwg_max <= 1024)
 
-template <int D>
+template <int D, class E = Fp16>
 __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(const PrefillArgs a) {
   constexpr int TPR = D / 4;                                // items per row
   constexpr int PER = kMergeRows * TPR / kMergeThreads;     // items per thread
@@ -974,8 +974,7 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(const Pref
       if ((int)(threadIdx.x + i * kMergeThreads) / TPR >= nrows) continue;
       const int rr = r0 + row[i];
       const int64_t orow = (int64_t)(md.q0 + rr / G) * a.Hq + md.h * G + rr % G;
-      *reinterpret_cast<f16x4*>(a.out + orow * D + d4[i]) =
-          f16x4{(f16)num[i][0], (f16)num[i][1], (f16)num[i][2], (f16)num[i][3]};
+      *reinterpret_cast<f16x4*>(a.out + orow * D + d4[i]) = to16x4<E>(num[i]);
     }
     __syncthreads();  // wts is free for the next task
   }
@@ -995,7 +994,7 @@ constexpr int kDmaThreads = 2 * kHalfWaves * kWave;
 // Units follow each other without a pipeline bubble: after a unit's last step
 // the next unit's block ids, queries and first block (into stage 0) are loaded
 // while the halves exchange their states (in the stage-1 objects) and store.
-template <int D, int RT, int H>
+template <int D, int RT, int H, class E>
 __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan& pl, int gid,
                                           int x_begin, int x_end, StreamPos sp, MergeDesc& md,
                                           int r, unsigned char* k0, unsigned char* v0,
@@ -1119,8 +1118,8 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
     }
 
     // ---- one block: S^T = K.Q^T, online softmax, O^T += V^T.P^T ----
-    const f16x8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f,
-                        (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
+    const f16 one = to16<E>(1.f);
+    const f16x8 ones = {one, one, one, one, one, one, one, one};
     auto compute = [&](int kb, const unsigned char* kbase,
                        const unsigned char* vbase) __attribute__((always_inline)) {
       // K fragments (16 keys x 32 dims, A operand): all reads issued ahead of
@@ -1142,7 +1141,7 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
 #pragma unroll
         for (int c = 0; c < P::NC; ++c)
 #pragma unroll
-          for (int rt = 0; rt < RT; ++rt) st[rt][kt] = mfma32(kf[kt][c], qv[rt][c], st[rt][kt]);
+          for (int rt = 0; rt < RT; ++rt) st[rt][kt] = mma32<E>(kf[kt][c], qv[rt][c], st[rt][kt]);
       // V fragments (transposing reads): lane (g, n) of a read addresses V[key
       // 32ps + 4g + n/4][dims 16x + 4(n%4) .. +3] (and the same 16 keys further
       // for the second half of the k = 32 operand; 32ps and 16 keep the row's
@@ -1196,7 +1195,8 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
           for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              p[4 * kt + i] = (f16)exp2_fast(__builtin_fmaf(sv[2 * ps + kt][i], a.scale_log2, neg_m));
+              p[4 * kt + i] =
+                  to16<E>(exp2_fast(__builtin_fmaf(sv[2 * ps + kt][i], a.scale_log2, neg_m)));
           pb[rt][ps] = p;
         }
       }
@@ -1207,10 +1207,10 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
           const f16x8 va = vf[x];
           if (ps == 0) vf[x] = vfrag(1, x);  // the next 32 keys' fragment, in flight meanwhile
 #pragma unroll
-          for (int rt = 0; rt < RT; ++rt) o[rt][x] = mfma32(va, pb[rt][ps], o[rt][x]);
+          for (int rt = 0; rt < RT; ++rt) o[rt][x] = mma32<E>(va, pb[rt][ps], o[rt][x]);
         }
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) lsum[rt] = mfma32(ones, pb[rt][ps], lsum[rt]);
+        for (int rt = 0; rt < RT; ++rt) lsum[rt] = mma32<E>(ones, pb[rt][ps], lsum[rt]);
       }
     };
 
@@ -1291,9 +1291,7 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
         f16* orow = a.out + orow_idx * D + 4 * g;
 #pragma unroll
         for (int xx = 0; xx < P::NX; ++xx)
-          *reinterpret_cast<f16x4*>(orow + 16 * xx) =
-              f16x4{(f16)(o[H][xx][0] * inv), (f16)(o[H][xx][1] * inv),
-                    (f16)(o[H][xx][2] * inv), (f16)(o[H][xx][3] * inv)};
+          *reinterpret_cast<f16x4*>(orow + 16 * xx) = to16x4<E>(o[H][xx] * inv);
       } else {
         const uint32_t prow = slot * kDmaRows + (st_row - st_r0);
         float* prow_o = a.part_o + (size_t)prow * D + 4 * g;
@@ -1309,7 +1307,7 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
   }
 }
 
-template <int D, int RT>
+template <int D, int RT, class E = Fp16>
 __global__ __launch_bounds__(kDmaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_dma_kernel(const PrefillArgs a) {
   using P = DCfg<D>;
@@ -1345,9 +1343,9 @@ void prefill_dma_kernel(const PrefillArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = w % kHalfWaves;
   if (w < kHalfWaves)
-    run_units<D, RT, 0>(a, pl, gid, x_begin, x_end, sp, md, r, k00, v00, k01, v01, k11, v11, xml);
+    run_units<D, RT, 0, E>(a, pl, gid, x_begin, x_end, sp, md, r, k00, v00, k01, v01, k11, v11, xml);
   else
-    run_units<D, RT, 1>(a, pl, gid, x_begin, x_end, sp, md, r, k10, v10, k11, v11, k01, v01, xml);
+    run_units<D, RT, 1, E>(a, pl, gid, x_begin, x_end, sp, md, r, k10, v10, k11, v11, k01, v01, xml);
   put_desc();
 }
 
@@ -1386,13 +1384,13 @@ int device_cus() {
 // One stream-K workgroup per CU (LDS: 128 KiB of stages at D = 128).
 inline int stream_wgs() { return device_cus(); }
 
-template <int D>
+template <int D, class E>
 void launch_prefill_dma(const PrefillArgs& a, hipStream_t stream) {
   constexpr int RT = kDmaRt;
-  hipLaunchKernelGGL((prefill_dma_kernel<D, RT>), dim3(a.nwg_max), dim3(kDmaThreads), 0, stream,
-                     a);
-  hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3(kMergeGrid * a.nwg_max), dim3(kMergeThreads),
-                     0, stream, a);
+  hipLaunchKernelGGL((prefill_dma_kernel<D, RT, E>), dim3(a.nwg_max), dim3(kDmaThreads), 0,
+                     stream, a);
+  hipLaunchKernelGGL((prefill_merge_kernel<D, E>), dim3(kMergeGrid * a.nwg_max),
+                     dim3(kMergeThreads), 0, stream, a);
 }
 
 constexpr int kMaxTickets = 65536;
@@ -1472,12 +1470,14 @@ extern "C" size_t fe_prefill_workspace_size(int num_seqs, int total_q, int num_q
   return need > sk ? need : sk;
 }
 
-extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, const void* v_pool,
-                                int num_blocks, const int32_t* block_tables, int table_stride,
-                                const int32_t* q_offsets, const int32_t* context_lens,
-                                int num_seqs, int total_q, int max_q_len, int num_q_heads,
-                                int kv_heads, int head_dim, int block_size, float scale,
-                                void* workspace, size_t workspace_bytes, fe_stream_t stream) {
+namespace {
+
+// fe_prefill_paged and its bf16 form: argument checks, workspace carving, launch.
+int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_pool, int num_blocks,
+                 const int32_t* block_tables, int table_stride, const int32_t* q_offsets,
+                 const int32_t* context_lens, int num_seqs, int total_q, int max_q_len,
+                 int num_q_heads, int kv_heads, int head_dim, int block_size, float scale,
+                 void* workspace, size_t workspace_bytes, fe_stream_t stream, bool bf16) {
   FE_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 &&
                kv_heads > 0 && num_blocks > 0 && table_stride > 0);
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
@@ -1535,14 +1535,43 @@ extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, co
   a.pre_lse = nullptr;
   a.tok0 = nullptr;
   hipStream_t s = (hipStream_t)stream;
-  if (dma) {
-    if (head_dim == 64) launch_prefill_dma<64>(a, s); else launch_prefill_dma<128>(a, s);
+  if (bf16 && !dma) return FE_ERR_UNSUPPORTED;  // bf16: the stream-K kernel only
+  if (dma && bf16) {
+    if (head_dim == 64) launch_prefill_dma<64, Bf16>(a, s); else launch_prefill_dma<128, Bf16>(a, s);
+  } else if (dma) {
+    if (head_dim == 64) launch_prefill_dma<64, Fp16>(a, s); else launch_prefill_dma<128, Fp16>(a, s);
   } else if (head_dim == 64) {
     if (p.rt == 2) launch_prefill<64, 2>(a, p.blocks, s); else launch_prefill<64, 1>(a, p.blocks, s);
   } else {
     if (p.rt == 2) launch_prefill<128, 2>(a, p.blocks, s); else launch_prefill<128, 1>(a, p.blocks, s);
   }
   return FE_LAUNCH_STATUS();
+}
+
+}  // namespace
+
+extern "C" int fe_prefill_paged(const void* q, void* out, const void* k_pool, const void* v_pool,
+                                int num_blocks, const int32_t* block_tables, int table_stride,
+                                const int32_t* q_offsets, const int32_t* context_lens,
+                                int num_seqs, int total_q, int max_q_len, int num_q_heads,
+                                int kv_heads, int head_dim, int block_size, float scale,
+                                void* workspace, size_t workspace_bytes, fe_stream_t stream) {
+  return prefill_impl(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride, q_offsets,
+                      context_lens, num_seqs, total_q, max_q_len, num_q_heads, kv_heads, head_dim,
+                      block_size, scale, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int fe_prefill_paged_bf16(const void* q, void* out, const void* k_pool,
+                                     const void* v_pool, int num_blocks,
+                                     const int32_t* block_tables, int table_stride,
+                                     const int32_t* q_offsets, const int32_t* context_lens,
+                                     int num_seqs, int total_q, int max_q_len, int num_q_heads,
+                                     int kv_heads, int head_dim, int block_size, float scale,
+                                     void* workspace, size_t workspace_bytes,
+                                     fe_stream_t stream) {
+  return prefill_impl(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride, q_offsets,
+                      context_lens, num_seqs, total_q, max_q_len, num_q_heads, kv_heads, head_dim,
+                      block_size, scale, workspace, workspace_bytes, stream, true);
 }
 
 namespace fe {

@@ -250,8 +250,8 @@ class _DeviceTables:
 
 class PagedKVCache:
     def __init__(self, layout: CacheLayout, device="cuda:0", dtype=torch.float16, fill=None):
-        if dtype != torch.float16:
-            raise ValueError(f"KV pools are float16 on the HIP kernels; got {dtype}")
+        if dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError(f"KV pools are float16 or bfloat16 on the HIP kernels; got {dtype}")
         self.layout = layout
         self.device = torch.device(device)
         self.dtype = dtype

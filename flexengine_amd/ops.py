@@ -17,6 +17,10 @@ import torch
 from flexengine_amd import _lib
 
 FP16 = torch.float16
+BF16 = torch.bfloat16
+# K/V element types of the attention entry points (the fe_*_bf16 forms take bf16);
+# the page writes and gathers copy 16-bit elements of either
+KV_DTYPES = (FP16, BF16)
 
 
 def _require_gpu(*tensors: torch.Tensor) -> torch.device:
@@ -39,11 +43,13 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-def _check_pool(k_pool: torch.Tensor, v_pool: torch.Tensor) -> tuple[int, int, int, int]:
+def _check_pool(k_pool: torch.Tensor, v_pool: torch.Tensor,
+                dtypes: tuple = (FP16,)) -> tuple[int, int, int, int]:
     if k_pool.shape != v_pool.shape or k_pool.ndim != 4:
         raise ValueError("K/V pools must both be [num_blocks, block_size, kv_heads, head_dim]")
-    if k_pool.dtype != FP16 or v_pool.dtype != FP16:
-        raise ValueError("K/V pools must be float16")
+    if k_pool.dtype not in dtypes or v_pool.dtype != k_pool.dtype:
+        names = " or ".join(str(t).replace("torch.", "") for t in dtypes)
+        raise ValueError(f"K/V pools must be {names} (both the same)")
     if not (k_pool.is_contiguous() and v_pool.is_contiguous()):
         raise ValueError("K/V pools must be contiguous")
     nb, bs, hkv, d = k_pool.shape
@@ -64,10 +70,10 @@ def write_kv(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_p
              slot_block: torch.Tensor, slot_offset: torch.Tensor) -> None:
     """k_pool[slot_block[t], slot_offset[t]] = k_new[t] (and v); negative blocks are skipped."""
     dev = _require_gpu(k_new, v_new, k_pool, v_pool, slot_block, slot_offset)
-    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool, KV_DTYPES)
     if k_new.shape != v_new.shape or k_new.ndim != 3 or tuple(k_new.shape[1:]) != (hkv, d):
         raise ValueError("K/V shapes must be [tokens, kv_heads, head_dim]")
-    if k_new.dtype != FP16 or v_new.dtype != FP16:
+    if k_new.dtype != k_pool.dtype or v_new.dtype != k_pool.dtype:
         raise ValueError("wrong KV dtype")
     if k_new.stride() != v_new.stride() or k_new.stride(2) != 1 or k_new.stride(1) != d:
         raise ValueError("new K/V rows must have contiguous heads and equal strides")
@@ -87,10 +93,10 @@ def write_kv_ragged(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tens
     rows q_offsets[s]..q_offsets[s+1]-1 are the last positions of sequence s's
     context_lens[s] tokens (the arrays prefill_paged takes; fe_write_kv_ragged)."""
     dev = _require_gpu(k_new, v_new, k_pool, v_pool, block_tables, q_offsets, context_lens)
-    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool, KV_DTYPES)
     if k_new.shape != v_new.shape or k_new.ndim != 3 or tuple(k_new.shape[1:]) != (hkv, d):
         raise ValueError("K/V shapes must be [tokens, kv_heads, head_dim]")
-    if k_new.dtype != FP16 or v_new.dtype != FP16:
+    if k_new.dtype != k_pool.dtype or v_new.dtype != k_pool.dtype:
         raise ValueError("wrong KV dtype")
     if k_new.stride() != v_new.stride() or k_new.stride(2) != 1 or k_new.stride(1) != d:
         raise ValueError("new K/V rows must have contiguous heads and equal strides")
@@ -146,14 +152,14 @@ def gather_kv(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Te
               total_tokens: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Materialises every sequence's K/V rows: returns [total_tokens, kv_heads, head_dim] pair."""
     dev = _require_gpu(k_pool, v_pool, block_tables, context_lens, out_offsets)
-    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool, KV_DTYPES)
     block_tables = _int32(block_tables, "block_tables")
     context_lens = _int32(context_lens, "context_lens")
     out_offsets = _int32(out_offsets, "out_offsets")
     batch = context_lens.shape[0]
     if block_tables.ndim != 2 or block_tables.shape[0] != batch or out_offsets.shape != (batch + 1,):
         raise ValueError("block_tables [batch, W], context_lens [batch], out_offsets [batch+1]")
-    k_out = torch.empty((total_tokens, hkv, d), dtype=FP16, device=dev)
+    k_out = torch.empty((total_tokens, hkv, d), dtype=k_pool.dtype, device=dev)
     v_out = torch.empty_like(k_out)
     _lib.call("fe_gather_kv", k_pool.data_ptr(), v_pool.data_ptr(), nb, block_tables.data_ptr(),
               block_tables.shape[1], context_lens.data_ptr(), out_offsets.data_ptr(),
@@ -219,9 +225,10 @@ def decode_workspace(device: torch.device, nbytes: int, kind: str = "decode") ->
 def _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_new, out):
     """Checks of the decode entry points; returns the normalised arguments."""
     dev = _require_gpu(q, k_pool, v_pool, block_tables, context_lens, k_new, v_new, out)
-    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
-    if q.ndim != 3 or q.shape[2] != d or q.dtype != FP16:
-        raise ValueError("q must be float16 [batch, num_q_heads, head_dim]")
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool, KV_DTYPES)
+    dt = k_pool.dtype
+    if q.ndim != 3 or q.shape[2] != d or q.dtype != dt:
+        raise ValueError("q must be [batch, num_q_heads, head_dim] of the pools' dtype")
     batch, hq, _ = q.shape
     if q.stride(2) != 1 or q.stride(1) != d:
         raise ValueError("q heads must be contiguous")
@@ -237,15 +244,15 @@ def _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_
     if k_new is not None:
         if k_new.shape != (batch, hkv, d) or v_new.shape != k_new.shape:
             raise ValueError("k_new/v_new must be [batch, kv_heads, head_dim]")
-        if k_new.dtype != FP16 or v_new.dtype != FP16:
-            raise ValueError("k_new/v_new must be float16")
+        if k_new.dtype != dt or v_new.dtype != dt:
+            raise ValueError("k_new/v_new must have the pools' dtype")
         if k_new.stride() != v_new.stride() or k_new.stride(2) != 1 or k_new.stride(1) != d:
             raise ValueError("k_new/v_new heads must be contiguous with equal strides")
         new_stride = k_new.stride(0)
     if out is None:
-        out = torch.empty((batch, hq, d), dtype=FP16, device=dev)
-    elif out.shape != (batch, hq, d) or out.dtype != FP16 or not out.is_contiguous():
-        raise ValueError("out must be a contiguous float16 [batch, num_q_heads, head_dim]")
+        out = torch.empty((batch, hq, d), dtype=dt, device=dev)
+    elif out.shape != (batch, hq, d) or out.dtype != dt or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [batch, num_q_heads, head_dim] of q's dtype")
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     return dev, nb, bs, hkv, d, batch, hq, block_tables, context_lens, new_stride, out, scale
@@ -294,8 +301,8 @@ def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                  plan: DecodePlan | None = None) -> torch.Tensor:
     """Single-token paged decode attention over one layer's pools.
 
-    q [B, Hq, D] fp16 (rows may be strided, heads contiguous); pools
-    [NB, BS, Hkv, D]; block_tables int32 [B, W]; context_lens int32 [B]
+    q [B, Hq, D] fp16 or bf16, the pools' dtype (rows may be strided, heads
+    contiguous); pools [NB, BS, Hkv, D]; block_tables int32 [B, W]; context_lens int32 [B]
     (0 = inactive row -> zeros).  With k_new/v_new ([B, Hkv, D]) the new token's
     K/V are written to the pool at position context_lens-1 in the same launch.
     With `plan` (paged_decode_plan on these block_tables / context_lens) the
@@ -312,15 +319,16 @@ def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
             block_tables.shape[1], context_lens.data_ptr(), workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), batch, hq, hkv, d, bs, float(scale),
             int(target_splits))
+    sfx = "_bf16" if q.dtype == BF16 else ""
     if plan is None:
-        _lib.call("fe_paged_decode", *args, _stream(dev))
+        _lib.call("fe_paged_decode" + sfx, *args, _stream(dev))
         return out
     shape = (batch, hkv, block_tables.shape[1], bs, nb, int(target_splits))
     if plan.shape != shape or plan.tables_ptr != block_tables.data_ptr() or \
             plan.lens_ptr != context_lens.data_ptr():
         raise ValueError("the plan was computed for other block_tables / context_lens or sizes")
-    _lib.call("fe_paged_decode_planned", *args, plan.buffer.data_ptr(), plan.buffer.numel(),
-              _stream(dev))
+    _lib.call("fe_paged_decode_planned" + sfx, *args, plan.buffer.data_ptr(),
+              plan.buffer.numel(), _stream(dev))
     return out
 
 
@@ -341,6 +349,8 @@ def paged_decode_shared_prefix(q: torch.Tensor, k_pool: torch.Tensor, v_pool: to
     Same result as paged_decode: the shared keys are attended once per group,
     the private suffixes per row, merged by log-sum-exp (fe_paged_decode_shared_prefix).
     """
+    if k_pool.dtype != FP16:
+        raise ValueError("the shared-prefix decode takes float16 pools")
     (dev, nb, bs, hkv, d, batch, hq, block_tables, context_lens, new_stride, out,
      scale) = _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_new, out)
     group_offsets = _int32(group_offsets, "group_offsets")
@@ -392,11 +402,13 @@ def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                   context_lens: torch.Tensor, max_q_len: int, *, scale: float | None = None,
                   out: torch.Tensor | None = None) -> torch.Tensor:
     """Ragged causal prefill: q [total_q, Hq, D]; sequence s owns rows
-    q_offsets[s]:q_offsets[s+1] at positions context_lens[s]-n_s .. context_lens[s]-1."""
+    q_offsets[s]:q_offsets[s+1] at positions context_lens[s]-n_s .. context_lens[s]-1.
+    fp16 or bf16 (q, out and the pools alike; bf16 needs block sizes that are
+    multiples of 16)."""
     dev = _require_gpu(q, k_pool, v_pool, block_tables, q_offsets, context_lens, out)
-    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
-    if q.ndim != 3 or q.shape[2] != d or q.dtype != FP16 or not q.is_contiguous():
-        raise ValueError("q must be a contiguous float16 [total_q, num_q_heads, head_dim]")
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool, KV_DTYPES)
+    if q.ndim != 3 or q.shape[2] != d or q.dtype != k_pool.dtype or not q.is_contiguous():
+        raise ValueError("q must be a contiguous [total_q, num_q_heads, head_dim] of the pools' dtype")
     total_q, hq, _ = q.shape
     if hq % hkv:
         raise ValueError("Q heads must be a multiple of KV heads")
@@ -408,11 +420,13 @@ def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
         raise ValueError("q_offsets [S+1], block_tables [S, W], context_lens [S]")
     if out is None:
         out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of q's shape and dtype")
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     need = int(_lib.load().fe_prefill_workspace_size(num_seqs, total_q, hq, hkv, d))
     ws = decode_workspace(dev, need, kind="prefill")
-    _lib.call("fe_prefill_paged", q.data_ptr(), out.data_ptr(), k_pool.data_ptr(),
+    _lib.call("fe_prefill_paged_bf16" if q.dtype == BF16 else "fe_prefill_paged", q.data_ptr(), out.data_ptr(), k_pool.data_ptr(),
               v_pool.data_ptr(), nb, block_tables.data_ptr(), block_tables.shape[1],
               q_offsets.data_ptr(), context_lens.data_ptr(), num_seqs, total_q, int(max_q_len),
               hq, hkv, d, bs, float(scale), ws.data_ptr(), ws.numel(), _stream(dev))

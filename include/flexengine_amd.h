@@ -221,6 +221,34 @@ int fe_paged_decode_planned(const void* q, int64_t q_batch_stride, void* out,
                             const void* plan, size_t plan_bytes, fe_stream_t stream);
 
 /*
+ * bf16 forms of fe_paged_decode and fe_paged_decode_planned: the same
+ * arguments and results with q, out, k_new, v_new and the pools in bfloat16
+ * (products on v_mfma_f32_16x16x16_bf16, probabilities rounded to bf16 for
+ * the PV product, fp32 accumulation and merge).  Replace the same reference
+ * routes for the bfloat16 models and caches the reference builds
+ * (src/flexengine/inference/models/qwen2.py:54, engine/kv_cache/allocator.py:24);
+ * the plan and the workspace are the fp16 forms' (dtype-free).
+ */
+int fe_paged_decode_bf16(const void* q, int64_t q_batch_stride, void* out,
+                         const void* k_new, const void* v_new, int64_t new_batch_stride,
+                         void* k_pool, void* v_pool, int num_blocks,
+                         const int32_t* block_tables, int table_stride,
+                         const int32_t* context_lens,
+                         void* workspace, size_t workspace_bytes,
+                         int batch, int num_q_heads, int kv_heads, int head_dim,
+                         int block_size, float scale, int target_splits,
+                         fe_stream_t stream);
+int fe_paged_decode_planned_bf16(const void* q, int64_t q_batch_stride, void* out,
+                                 const void* k_new, const void* v_new, int64_t new_batch_stride,
+                                 void* k_pool, void* v_pool, int num_blocks,
+                                 const int32_t* block_tables, int table_stride,
+                                 const int32_t* context_lens,
+                                 void* workspace, size_t workspace_bytes,
+                                 int batch, int num_q_heads, int kv_heads, int head_dim,
+                                 int block_size, float scale, int target_splits,
+                                 const void* plan, size_t plan_bytes, fe_stream_t stream);
+
+/*
  * fe_paged_decode without a workspace argument, for callers that cannot
  * allocate device memory: code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc.  No counterpart in the reference.
@@ -324,6 +352,23 @@ int fe_prefill_paged(const void* q, void* out,
                      int num_q_heads, int kv_heads, int head_dim,
                      int block_size, float scale,
                      void* workspace, size_t workspace_bytes, fe_stream_t stream);
+
+/*
+ * bf16 form of fe_prefill_paged: the same arguments and results with q, out
+ * and the pools in bfloat16 (v_mfma_f32_16x16x32_bf16, probabilities rounded
+ * to bf16 for the PV product, fp32 accumulation).  Block sizes must be
+ * multiples of 16 (FE_ERR_UNSUPPORTED otherwise); the workspace is
+ * fe_prefill_workspace_size's.  Replaces the same per-request route for the
+ * bfloat16 models the reference builds (qwen2.py:54).
+ */
+int fe_prefill_paged_bf16(const void* q, void* out,
+                          const void* k_pool, const void* v_pool, int num_blocks,
+                          const int32_t* block_tables, int table_stride,
+                          const int32_t* q_offsets, const int32_t* context_lens,
+                          int num_seqs, int total_q, int max_q_len,
+                          int num_q_heads, int kv_heads, int head_dim,
+                          int block_size, float scale,
+                          void* workspace, size_t workspace_bytes, fe_stream_t stream);
 
 /*
  * Bytes of device workspace fe_prefill_paged needs for these sizes (its key
