@@ -84,8 +84,7 @@ struct PrefillArgs {
   float* part_o;     // [KS][total_q * Hq][D] normalised partial outputs (KS > 1); the
                      // stream-K kernel's partials [2 * nwg_max * 128][D]
   float* part_lse;   // [KS][total_q * Hq] base-2 LSE of each partial
-  struct MergeDesc* merge;  // stream-K kernel: [nwg_max] split units to merge
-  int* tickets;      // [row blocks * Hkv], zero between calls
+  int* tickets;      // [row blocks * Hkv] (stream-K kernel: [nwg_max]), zero between calls
   int64_t q_stride;  // elements from one query row (token or sequence) to the next
   int W, S, total_q, Hq, Hkv, G, BS, bs_log2, NB, KS;
   int nwg_max;       // stream-K kernel: workgroups of the launch
@@ -657,9 +656,13 @@ __device__ __forceinline__ void dma_run(const PrefillArgs& a, int h, int w, int 
 // of context lengths.  A unit covered by one workgroup is written directly; a
 // unit split between workgroups gets a normalised fp32 partial and base-2 LSE
 // from each contributor (slot 2g, or 2g + 1 for the last unit of a range that
-// started in an earlier one), and a second launch merges them.  The launch
-// boundary orders the partials' stores before the merge's loads, so no
-// counter, fence or cache-bypassing access is involved.
+// started in an earlier one), written with device-coherent stores that the
+// contributor waits for before drawing a ticket; the contributor drawing the
+// last ticket merges the partials (device-coherent loads) into the output and
+// resets the ticket (the protocol of the decode's split-K merge).  A split
+// unit starts in the range of exactly one workgroup x0 (it runs past the end
+// of that range), so its ticket is tickets[x0] and its contributors are the
+// workgroups x0 .. owner(last block).
 //
 // Key blocks per row block, in closed form: a row block whose last row is y
 // (row = position * G + head) reads keys up to c + y / G, so it has
@@ -763,6 +766,10 @@ struct StreamPlan {
 // ceil(nb_max / (kMaxContrib - 2)) blocks, so a unit of nb_max blocks meets at
 // most kMaxContrib - 1 of them.
 constexpr int kMaxContrib = 32;
+// Partials a split unit's merging lanes load per round trip.
+constexpr int kMergeBatch = 2;
+// Stream-K workgroups at most (a split unit's ticket is tickets[x0], x0 < nwg).
+constexpr int kMaxStreamWgs = 1024;
 
 __device__ __forceinline__ StreamPlan stream_plan(const PrefillArgs& a) {
   const int lane = lane_id();
@@ -845,139 +852,76 @@ __device__ __forceinline__ bool stream_locate(const PrefillArgs& a, const SeqWor
 }
 
 
-// What the merge launch needs of a split unit, written by the unit's first
-// contributor g (the unit starts in g's range and runs past its end; a range
-// starts at most one such unit, its last) into entry blockIdx.x of
-// PrefillArgs::merge; cnt = 0 where workgroup blockIdx.x has none.  The
-// contributors are g .. g + cnt - 1; the unit is the first unit of every
-// range after g's, so their slots are 2 (g + k), and g's slot is `slot0`.
-struct MergeDesc {
-  int cnt, slot0, q0, h;  // contributors, g's partial slot, first query row, KV head
-  int r0, r_end, pad0, pad1;  // the unit's rows [r0, r_end) (row = position * G + head)
-};
+// The split units' partial slots (2 per workgroup of 128 rows): one buffer
+// descriptor per array over all of them (the host keeps them < 2 GiB).
+template <int D>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc_o(const PrefillArgs& a, int nwg) {
+  return __builtin_amdgcn_make_buffer_rsrc(a.part_o, 0, (int)(2 * nwg * kDmaRows * D * sizeof(float)),
+                                           0x00020000);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc_lse(const PrefillArgs& a, int nwg) {
+  return __builtin_amdgcn_make_buffer_rsrc(a.part_lse, 0, (int)(2 * nwg * kDmaRows * sizeof(float)),
+                                           0x00020000);
+}
 
-// Merge launch, after the stream-K launch on the same stream (whose partials
-// and descriptors it therefore reads with plain loads).  The split units are
-// the descriptors with cnt >= 2, in descriptor order; task j is quarter j % 4
-// (32 rows) of split unit j / 4, and workgroup b takes tasks b, b + grid, ...
-// so the merge spreads over the whole grid however few units are split.  Per
-// task the rows' weights go to LDS, then items (row, 4 dims) go to consecutive
-// threads, which sum the contributors' partials MAXK at a time with all their
-// loads in flight.
-constexpr int kMergeThreads = 256;
-constexpr int kMergeRows = 32;                       // rows per task
-constexpr int kMergeParts = kDmaRows / kMergeRows;   // tasks per split unit
-constexpr int kMergeGrid = 4;  // merge workgroups per stream-K workgroup: one task each in
-                               // the usual case (at most one split unit per range)
-constexpr int kMergeDescPerThread = 4;  // descriptors a thread counts (nwg_max <= 1024)
-
-template <int D, class E = Fp16>
-__global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(const PrefillArgs a) {
-  constexpr int TPR = D / 4;                                // items per row
-  constexpr int PER = kMergeRows * TPR / kMergeThreads;     // items per thread
-  constexpr int MAXK = 4;
-  constexpr int NWAVE = kMergeThreads / kWave;
-  constexpr int DPT = kMergeDescPerThread;
-  __shared__ float wts[kMergeRows][kMaxContrib];
-  __shared__ int wave_total[NWAVE];
-  __shared__ int task_desc;
-  // ---- the split units: thread t holds descriptors t, t + 256, ... (loads in flight together) ----
-  const int ndesc = a.nwg_max;
-  bool split[DPT];
+// Merges rows of a split unit into the fp16 output: lane (g, n) owns one row
+// (urow within the unit, output row orow) and dims 16x + 4g .. +3.  Contributor
+// k of the unit's ncontrib (workgroups x0 + k) left its normalised partial in
+// slot slot_x0 (k = 0) or 2 (x0 + k); contributor `self` (-1: none) is taken
+// from (M, den, num) instead, which start as that workgroup's own state.
+// kMergeBatch partials per round trip, combined with a running maximum.
+template <int D, class E>
+__device__ __forceinline__ void merge_split_rows(const PrefillArgs& a, __amdgpu_buffer_rsrc_t ro,
+                                                 __amdgpu_buffer_rsrc_t rl, int x0, int ncontrib,
+                                                 uint32_t slot_x0, int self, uint32_t urow,
+                                                 int64_t orow, float M, float den,
+                                                 f32x4 (&num)[D / 16]) {
+  constexpr int NX = D / 16;
+  const int g = lane_id() >> 4;
+  for (int c0 = 0; c0 < ncontrib; c0 += kMergeBatch) {
+    float lv[kMergeBatch];
+    f32x4 ov[kMergeBatch][NX];
 #pragma unroll
-  for (int j = 0; j < DPT; ++j) {
-    const int i = threadIdx.x + j * kMergeThreads;
-    split[j] = i < ndesc && a.merge[i].cnt >= 2;
-  }
-  // split units are numbered in the order (j, t): descriptor t + 256 j
-  const int w = threadIdx.x / kWave;
-  int excl[DPT], total = 0;
+    for (int k = 0; k < kMergeBatch; ++k) {
+      lv[k] = kNegInf;
+      const int kc = c0 + k;
+      if (kc < ncontrib && kc != self) {  // wave-uniform
+        const uint32_t prow = (kc == 0 ? slot_x0 : 2u * (x0 + kc)) * kDmaRows + urow;
+        lv[k] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(rl, prow * (uint32_t)sizeof(float), 0,
+                                                        kSc1));
 #pragma unroll
-  for (int j = 0; j < DPT; ++j) {
-    const int incl = wave_scan_incl_i(split[j] ? 1 : 0);
-    if (lane_id() == kWave - 1) wave_total[w] = incl;
-    __syncthreads();
-    int before = 0, sum = 0;
+        for (int xx = 0; xx < NX; ++xx)
+          ov[k][xx] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         ro, (prow * D + 16 * xx + 4 * g) * (uint32_t)sizeof(float), 0, kSc1));
+      } else {
 #pragma unroll
-    for (int k = 0; k < NWAVE; ++k) {
-      before += k < w ? wave_total[k] : 0;
-      sum += wave_total[k];
-    }
-    excl[j] = total + before + incl - (split[j] ? 1 : 0);
-    total += sum;
-    __syncthreads();
-  }
-  const int G = a.G;
-  for (int task = blockIdx.x; task < total * kMergeParts; task += gridDim.x) {
-    const int u = task / kMergeParts, part = task % kMergeParts;
-#pragma unroll
-    for (int j = 0; j < DPT; ++j)
-      if (split[j] && excl[j] == u) task_desc = threadIdx.x + j * kMergeThreads;
-    __syncthreads();
-    const MergeDesc md = a.merge[task_desc];
-    __syncthreads();  // task_desc is read before the next task writes it
-    const int cnt = min(md.cnt, kMaxContrib);
-    const int r0 = md.r0 + part * kMergeRows;
-    const int nrows = min(md.r_end - r0, kMergeRows);
-    if (nrows <= 0) continue;  // uniform over the workgroup
-    const int prow0 = part * kMergeRows;
-    const int g0 = md.slot0 >> 1;
-    auto slot_of = [&](int k) __attribute__((always_inline)) {
-      return k == 0 ? md.slot0 : 2 * (g0 + k);
-    };
-    // weights: every (row, contributor) LSE load in flight, then one thread per
-    // row normalises exp2(lse_k - max) in LDS
-    for (int i = threadIdx.x; i < nrows * cnt; i += kMergeThreads) {
-      const int r = i / cnt, k = i - r * cnt;
-      wts[r][k] = a.part_lse[slot_of(k) * kDmaRows + prow0 + r];
-    }
-    __syncthreads();
-    for (int r = threadIdx.x; r < nrows; r += kMergeThreads) {
-      float* wr = wts[r];
-      float M = kNegInf;
-      for (int k = 0; k < cnt; ++k) M = fmaxf(M, wr[k]);
-      float den = 0.f;
-      for (int k = 0; k < cnt; ++k) den += wr[k] != kNegInf ? exp2f(wr[k] - M) : 0.f;
-      const float inv = den > 0.f ? 1.f / den : 0.f;
-      for (int k = 0; k < cnt; ++k) wr[k] = wr[k] != kNegInf ? exp2f(wr[k] - M) * inv : 0.f;
-    }
-    __syncthreads();
-    int row[PER], d4[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int it = threadIdx.x + i * kMergeThreads;
-      row[i] = min(it / TPR, nrows - 1);  // rows past nrows are computed and not stored
-      d4[i] = (it % TPR) * 4;
-    }
-    f32x4 num[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) num[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int c0 = 0; c0 < cnt; c0 += MAXK) {
-      f32x4 ov[PER][MAXK];
-#pragma unroll
-      for (int k = 0; k < MAXK; ++k) {
-        const float* base =
-            a.part_o + ((int64_t)slot_of(min(c0 + k, cnt - 1)) * kDmaRows + prow0) * D;
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-          ov[i][k] = *reinterpret_cast<const f32x4*>(base + row[i] * D + d4[i]);
+        for (int xx = 0; xx < NX; ++xx) ov[k][xx] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-#pragma unroll
-      for (int k = 0; k < MAXK; ++k)
-        if (c0 + k < cnt) {
-#pragma unroll
-          for (int i = 0; i < PER; ++i) num[i] += wts[row[i]][c0 + k] * ov[i][k];
-        }
     }
+    float bm = kNegInf;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      if ((int)(threadIdx.x + i * kMergeThreads) / TPR >= nrows) continue;
-      const int rr = r0 + row[i];
-      const int64_t orow = (int64_t)(md.q0 + rr / G) * a.Hq + md.h * G + rr % G;
-      *reinterpret_cast<f16x4*>(a.out + orow * D + d4[i]) = to16x4<E>(num[i]);
+    for (int k = 0; k < kMergeBatch; ++k) bm = fmaxf(bm, lv[k]);
+    const float newM = fmaxf(M, bm);
+    const float alpha = M == kNegInf ? 0.f : exp2f(M - newM);
+    den *= alpha;
+#pragma unroll
+    for (int xx = 0; xx < NX; ++xx) num[xx] *= alpha;
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const float wv = lv[k] != kNegInf ? exp2f(lv[k] - newM) : 0.f;
+      den += wv;
+#pragma unroll
+      for (int xx = 0; xx < NX; ++xx) num[xx] += wv * ov[k][xx];
     }
-    __syncthreads();  // wts is free for the next task
+    M = newM;
   }
+  const float dinv = den > 0.f ? 1.f / den : 0.f;
+  f16* out = a.out + orow * D + 4 * g;
+#pragma unroll
+  for (int xx = 0; xx < NX; ++xx)
+    *reinterpret_cast<f16x4*>(out + 16 * xx) = to16x4<E>(num[xx] * dinv);
 }
 
 // The stream-K kernel's workgroup: two halves of kHalfWaves waves, each wave
@@ -990,17 +934,18 @@ constexpr int kDmaThreads = 2 * kHalfWaves * kWave;
 
 // The units of workgroup gid's range [x_begin, x_end) for the waves of half H
 // (wave r of the half); k0 .. v1 are the half's stage objects, pk1 / pv1 the
-// partner half's stage-1 objects and xml the exchange of row maxima and sums.
-// Units follow each other without a pipeline bubble: after a unit's last step
-// the next unit's block ids, queries and first block (into stage 0) are loaded
-// while the halves exchange their states (in the stage-1 objects) and store.
+// partner half's stage-1 objects, xml the exchange of row maxima and sums and
+// last the workgroup's ticket result.  Units follow each other without a
+// pipeline bubble: after a unit's last step the next unit's block ids, queries
+// and first block (into stage 0) are loaded while the halves exchange their
+// states (in the stage-1 objects) and store.
 template <int D, int RT, int H, class E>
 __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan& pl, int gid,
-                                          int x_begin, int x_end, StreamPos sp, MergeDesc& md,
-                                          int r, unsigned char* k0, unsigned char* v0,
+                                          int x_begin, int x_end, StreamPos sp, int r,
+                                          unsigned char* k0, unsigned char* v0,
                                           unsigned char* k1, unsigned char* v1,
                                           const unsigned char* pk1, const unsigned char* pv1,
-                                          float* xml) {
+                                          float* xml, int* last) {
   using P = DCfg<D>;
   static_assert(RT == 2, "each half's wave exchanges one of its two row tiles");
   static_assert(2 * P::NX * kWave * 16 <= P::MAT, "two waves' tiles per stage object");
@@ -1021,7 +966,7 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
   // ---- the current unit (wave-uniform, except the lanes' rows) ----
   int x = x_begin;
   int h = 0, q0 = 0, total_rows = 0, cached = 0, r0 = 0, r_last = 0, key_end = 0;
-  int kb_lo = 0, kb_hi = 0, kb_first = 0, unit_start = 0, wr0 = 0, unmasked_blocks = 0;
+  int kb_lo = 0, kb_hi = 0, kb_first = 0, unit_start = 0, nb = 0, wr0 = 0, unmasked_blocks = 0;
   bool split = false, has_rows = false;
   const int32_t* trow = a.tables;
   int kb_base = 0, idv = 0;
@@ -1047,19 +992,11 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
     r0 = sp.rb * kDmaRows;
     r_last = min(r0 + kDmaRows, total_rows) - 1;
     key_end = cached + r_last / G + 1;  // keys the row block reads
-    const int nb = rb_blocks(a, sp.w, sp.rb);
+    nb = rb_blocks(a, sp.w, sp.rb);
     kb_lo = sp.kb;
     kb_hi = min(nb, kb_lo + (x_end - x));
     unit_start = x - kb_lo;
     split = kb_lo > 0 || kb_hi < nb;  // other workgroups hold blocks of the unit
-    if (kb_hi < nb && unit_start >= x_begin) {  // this range's last unit, merged later
-      md.cnt = pl.rg.owner(unit_start + nb - 1) - gid + 1;
-      md.slot0 = 2 * gid + (x_begin < unit_start ? 1 : 0);
-      md.q0 = q0;
-      md.h = h;
-      md.r0 = r0;
-      md.r_end = r_last + 1;
-    }
     wr0 = r0 + r * 16 * RT;  // first row of this wave
     has_rows = wr0 <= r_last;
     trow = a.tables + (int64_t)sp.s * a.W;
@@ -1101,6 +1038,11 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
     }
     return true;
   };
+
+  // the range's first unit when it is split and the range holds more: its
+  // ticket is drawn one barrier later, and its merge, if it falls to this
+  // workgroup, waits for the end of the range
+  bool pend = false;
 
   open_unit();
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1241,9 +1183,13 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
     // ---- what the store of this unit needs; then the next unit's loads ----
     const bool st_ok = has_rows && valid[H];
     const int st_row = wr0 + 16 * H + n;
-    const int st_q0 = q0, st_h = h, st_r0 = r0;
+    const int st_q0 = q0, st_h = h, st_r0 = r0, total_rows_st = total_rows;
     const bool st_split = split;
     const uint32_t slot = 2u * gid + (x_begin < unit_start ? 1u : 0u);
+    // a split unit's contributors: workgroups x0 .. x0 + ncontrib - 1
+    const int x0 = st_split ? pl.rg.owner(unit_start) : 0;
+    const int ncontrib = st_split ? pl.rg.owner(unit_start + nb - 1) - x0 + 1 : 1;
+    const uint32_t slot_x0 = 2u * x0 + (pl.rg.start(x0) < unit_start ? 1u : 0u);
     const int x_next = x + (kb_hi - kb_lo);
     const bool more = x_next < x_end && next_unit();
     if (more) {
@@ -1282,28 +1228,120 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
     }
 
     // ---- the whole unit here: store.  Part of it: normalised partial and
-    //      base-2 LSE (fp32) for the merge launch ----
-    if (st_ok) {
-      const float l = lsum[H][0];
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-      if (!st_split) {
-        const int64_t orow_idx = (int64_t)(st_q0 + st_row / G) * a.Hq + st_h * G + st_row % G;
-        f16* orow = a.out + orow_idx * D + 4 * g;
+    //      base-2 LSE (fp32, device-coherent stores), then the unit's ticket;
+    //      the last contributor merges every partial of the unit's rows ----
+    const int64_t st_orow =
+        (int64_t)(st_q0 + st_row / G) * a.Hq + st_h * G + st_row % G;  // output row
+    if (!st_split) {
+      if (st_ok) {
+        const float l = lsum[H][0];
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        f16* orow = a.out + st_orow * D + 4 * g;
 #pragma unroll
         for (int xx = 0; xx < P::NX; ++xx)
           *reinterpret_cast<f16x4*>(orow + 16 * xx) = to16x4<E>(o[H][xx] * inv);
-      } else {
-        const uint32_t prow = slot * kDmaRows + (st_row - st_r0);
-        float* prow_o = a.part_o + (size_t)prow * D + 4 * g;
+      }
+    } else {
+      const __amdgpu_buffer_rsrc_t ro = part_rsrc_o<D>(a, pl.rg.nwg);
+      const __amdgpu_buffer_rsrc_t rl = part_rsrc_lse(a, pl.rg.nwg);
+      const uint32_t urow = (uint32_t)(st_row - st_r0);  // row within the unit
+      const float l = lsum[H][0];
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const float own_lse = l > 0.f ? m_run[H] + log2f(l) : kNegInf;
+      // At the end of its range the workgroup is usually the unit's last
+      // contributor (the others took the unit's later blocks at the start of
+      // theirs): if all of them have drawn their tickets, it merges from its
+      // registers and stores no partial of its own.
+      bool fast = false;
+      if (!more) {
+        if (threadIdx.x == 0)
+          *last = __hip_atomic_load(a.tickets + x0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  ncontrib - 1;
+        __syncthreads();
+        fast = *last;  // workgroup-uniform
+      }
+      if (!fast) {
+        if (st_ok) {
+          const uint32_t prow = slot * kDmaRows + urow;
 #pragma unroll
-        for (int xx = 0; xx < P::NX; ++xx)
-          *reinterpret_cast<f32x4*>(prow_o + 16 * xx) = o[H][xx] * inv;
-        if (g == 0) a.part_lse[prow] = l > 0.f ? m_run[H] + log2f(l) : kNegInf;
+          for (int xx = 0; xx < P::NX; ++xx)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4, o[H][xx] * inv), ro,
+                (prow * D + 16 * xx + 4 * g) * (uint32_t)sizeof(float), 0, kSc1);
+          if (g == 0)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, own_lse), rl,
+                                                  prow * (uint32_t)sizeof(float), 0, kSc1);
+        }
+        if (more) {
+          // the range's first unit: what its merge needs, kept in LDS
+          pend = true;
+          if (threadIdx.x == 0) {
+            last[2] = x0;
+            last[3] = ncontrib;
+            last[4] = (int)slot_x0;
+            last[5] = st_q0;
+            last[6] = st_h;
+            last[7] = st_r0;
+            last[8] = total_rows_st;
+          }
+        } else {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial is complete
+          __syncthreads();  // every thread has read *last
+          if (threadIdx.x == 0)
+            *last = __hip_atomic_fetch_add(a.tickets + x0, 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) == ncontrib - 1;
+          __syncthreads();
+        }
+      }
+      if (fast || (!more && *last)) {  // workgroup-uniform
+        if (threadIdx.x == 0)
+          __hip_atomic_store(a.tickets + x0, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (st_ok) {
+          f32x4 num[P::NX];
+#pragma unroll
+          for (int xx = 0; xx < P::NX; ++xx)
+            num[xx] = fast ? o[H][xx] * inv : f32x4{0.f, 0.f, 0.f, 0.f};
+          merge_split_rows<D, E>(a, ro, rl, x0, ncontrib, slot_x0, fast ? gid - x0 : -1, urow,
+                                 st_orow, fast ? own_lse : kNegInf,
+                                 fast && own_lse != kNegInf ? 1.f : 0.f, num);
+        }
       }
     }
     if (!more) break;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next unit's ids, queries, block
     __syncthreads();  // ... and the exchange has been read before stage 1 is refilled
+    // the first unit's partial is complete in every wave: draw its ticket (the
+    // result is read at the end of the range)
+    if (st_split && threadIdx.x == 0)
+      last[1] = __hip_atomic_fetch_add(a.tickets + x0, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == ncontrib - 1;
+  }
+  if (pend) {
+    __syncthreads();  // last[1] was written before a barrier of a later step
+    if (last[1]) {
+      // the merge of the range's first unit fell to this workgroup (its other
+      // contributors finished later)
+      const int f_x0 = __builtin_amdgcn_readfirstlane(last[2]);
+      const int f_n = __builtin_amdgcn_readfirstlane(last[3]);
+      const uint32_t f_slot_x0 = (uint32_t)__builtin_amdgcn_readfirstlane(last[4]);
+      const int f_q0 = __builtin_amdgcn_readfirstlane(last[5]);
+      const int f_h = __builtin_amdgcn_readfirstlane(last[6]);
+      const int f_r0 = __builtin_amdgcn_readfirstlane(last[7]);
+      const int f_rows = min(f_r0 + kDmaRows, __builtin_amdgcn_readfirstlane(last[8])) - f_r0;
+      if (threadIdx.x == 0)
+        __hip_atomic_store(a.tickets + f_x0, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int urow = r * 16 * RT + 16 * H + n;
+      if (urow < f_rows) {
+        const int row = f_r0 + urow;
+        f32x4 num[P::NX];
+#pragma unroll
+        for (int xx = 0; xx < P::NX; ++xx) num[xx] = f32x4{0.f, 0.f, 0.f, 0.f};
+        merge_split_rows<D, E>(a, part_rsrc_o<D>(a, pl.rg.nwg), part_rsrc_lse(a, pl.rg.nwg), f_x0,
+                               f_n, f_slot_x0, -1, (uint32_t)urow,
+                               (int64_t)(f_q0 + row / G) * a.Hq + f_h * G + row % G, kNegInf,
+                               0.f, num);
+      }
+    }
   }
 }
 
@@ -1323,30 +1361,29 @@ void prefill_dma_kernel(const PrefillArgs a) {
   __shared__ __align__(16) unsigned char k11[P::MAT];
   __shared__ __align__(16) unsigned char v11[P::MAT];
   __shared__ float xml[2 * kHalfWaves * 2 * kWave];  // row maxima and sums exchanged at unit ends
+  // whether this workgroup drew the last ticket of its range's last unit [0]
+  // and of its first unit [1], when split; [2..8]: the first unit's merge
+  // parameters
+  __shared__ int last[9];
 
-  // this workgroup's merge descriptor: empty unless its last unit is split and
-  // starts in its range
-  MergeDesc md{};
-  auto put_desc = [&]() __attribute__((always_inline)) {
-    if (threadIdx.x == 0) a.merge[blockIdx.x] = md;
-  };
   const StreamPlan pl = stream_plan(a);
   const int nwg = pl.rg.nwg;
-  if ((int)blockIdx.x >= nwg) return put_desc();
+  if ((int)blockIdx.x >= nwg) return;
   const int gid = logical_wg(blockIdx.x, nwg);
   const int x_begin = pl.rg.start(gid);
   const int x_end = pl.rg.start(gid + 1);
-  if (x_begin >= x_end) return put_desc();
+  if (x_begin >= x_end) return;
   StreamPos sp;
-  if (!stream_locate(a, pl.w0, x_begin, sp)) return put_desc();
+  if (!stream_locate(a, pl.w0, x_begin, sp)) return;
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = w % kHalfWaves;
   if (w < kHalfWaves)
-    run_units<D, RT, 0, E>(a, pl, gid, x_begin, x_end, sp, md, r, k00, v00, k01, v01, k11, v11, xml);
+    run_units<D, RT, 0, E>(a, pl, gid, x_begin, x_end, sp, r, k00, v00, k01, v01, k11, v11, xml,
+                           last);
   else
-    run_units<D, RT, 1, E>(a, pl, gid, x_begin, x_end, sp, md, r, k10, v10, k11, v11, k01, v01, xml);
-  put_desc();
+    run_units<D, RT, 1, E>(a, pl, gid, x_begin, x_end, sp, r, k10, v10, k11, v11, k01, v01, xml,
+                           last);
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1389,8 +1426,6 @@ void launch_prefill_dma(const PrefillArgs& a, hipStream_t stream) {
   constexpr int RT = kDmaRt;
   hipLaunchKernelGGL((prefill_dma_kernel<D, RT, E>), dim3(a.nwg_max), dim3(kDmaThreads), 0,
                      stream, a);
-  hipLaunchKernelGGL((prefill_merge_kernel<D, E>), dim3(kMergeGrid * a.nwg_max),
-                     dim3(kMergeThreads), 0, stream, a);
 }
 
 constexpr int kMaxTickets = 65536;
@@ -1436,7 +1471,7 @@ inline Plan plan(int num_seqs, int total_q, int num_q_heads, int kv_heads) {
 // block counts stay within the 32-bit closed form of the work split.
 inline bool stream_ok(int block_size, int table_stride, int total_q, int G, int num_seqs,
                       int kv_heads, int nwg) {
-  if (block_size % 16 != 0 || nwg <= 0 || nwg > kMergeDescPerThread * kMergeThreads) return false;
+  if (block_size % 16 != 0 || nwg <= 0 || nwg > kMaxStreamWgs) return false;
   const int64_t max_ctx = (int64_t)table_stride * block_size;
   const int64_t units = ((int64_t)total_q * G + kDmaRows - 1) / kDmaRows + num_seqs;
   // closed-form operands within 32 bits; total key blocks within 31 bits (a
@@ -1448,8 +1483,7 @@ inline bool stream_ok(int block_size, int table_stride, int total_q, int G, int 
 // Partial slots of the stream-K kernel: two per workgroup, 128 rows each.
 inline size_t stream_ws_bytes(int head_dim) {
   const size_t rows = (size_t)2 * stream_wgs() * kDmaRows;
-  return kTicketBytes + align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float)) +
-         align256((size_t)stream_wgs() * sizeof(MergeDesc));
+  return kTicketBytes + align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
 }
 
 }  // namespace
@@ -1516,7 +1550,6 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   ws += align256(rows * head_dim * sizeof(float));
   a.part_lse = (float*)ws;
   ws += align256(rows * sizeof(float));
-  a.merge = dma ? (MergeDesc*)ws : nullptr;
   a.W = table_stride;
   a.S = num_seqs;
   a.total_q = total_q;
@@ -1613,7 +1646,6 @@ int cascade_prefix_launch(const CascadePrefix& c, hipStream_t stream) {
   a.NB = c.num_blocks;
   a.KS = p.ks;
   a.nwg_max = 0;
-  a.merge = nullptr;
   a.scale_log2 = c.scale * kLog2e;
   a.prefix_len = c.prefix_len;
   a.pre_o = c.pre_o;
