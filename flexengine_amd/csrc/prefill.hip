@@ -867,17 +867,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc_lse(const PrefillArg
 // Merges rows of a split unit into the fp16 output: lane (g, n) owns one row
 // (urow within the unit, output row orow) and dims 16x + 4g .. +3.  Contributor
 // k of the unit's ncontrib (workgroups x0 + k) left its normalised partial in
-// slot slot_x0 (k = 0) or 2 (x0 + k); contributor `self` (-1: none) is taken
-// from (M, den, num) instead, which start as that workgroup's own state.
-// kMergeBatch partials per round trip, combined with a running maximum.
+// slot slot_x0 (k = 0) or 2 (x0 + k); contributor `self` (-1: none) did not,
+// and its values (own_o, own_lse: exactly what it would have stored) are used
+// in its place.  Contributors are combined in slot order, kMergeBatch per round
+// trip with a running maximum, so the result does not depend on which
+// contributor merges.
 template <int D, class E>
 __device__ __forceinline__ void merge_split_rows(const PrefillArgs& a, __amdgpu_buffer_rsrc_t ro,
                                                  __amdgpu_buffer_rsrc_t rl, int x0, int ncontrib,
                                                  uint32_t slot_x0, int self, uint32_t urow,
-                                                 int64_t orow, float M, float den,
-                                                 f32x4 (&num)[D / 16]) {
+                                                 int64_t orow, const f32x4 (&own_o)[D / 16],
+                                                 float own_lse) {
   constexpr int NX = D / 16;
   const int g = lane_id() >> 4;
+  float M = kNegInf, den = 0.f;
+  f32x4 num[NX];
+#pragma unroll
+  for (int xx = 0; xx < NX; ++xx) num[xx] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int c0 = 0; c0 < ncontrib; c0 += kMergeBatch) {
     float lv[kMergeBatch];
     f32x4 ov[kMergeBatch][NX];
@@ -885,7 +891,11 @@ __device__ __forceinline__ void merge_split_rows(const PrefillArgs& a, __amdgpu_
     for (int k = 0; k < kMergeBatch; ++k) {
       lv[k] = kNegInf;
       const int kc = c0 + k;
-      if (kc < ncontrib && kc != self) {  // wave-uniform
+      if (kc == self) {  // wave-uniform
+        lv[k] = own_lse;
+#pragma unroll
+        for (int xx = 0; xx < NX; ++xx) ov[k][xx] = own_o[xx];
+      } else if (kc < ncontrib) {  // wave-uniform
         const uint32_t prow = (kc == 0 ? slot_x0 : 2u * (x0 + kc)) * kDmaRows + urow;
         lv[k] = __builtin_bit_cast(
             float, __builtin_amdgcn_raw_buffer_load_b32(rl, prow * (uint32_t)sizeof(float), 0,
@@ -1297,13 +1307,11 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
         if (threadIdx.x == 0)
           __hip_atomic_store(a.tickets + x0, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (st_ok) {
-          f32x4 num[P::NX];
+          f32x4 own[P::NX];
 #pragma unroll
-          for (int xx = 0; xx < P::NX; ++xx)
-            num[xx] = fast ? o[H][xx] * inv : f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int xx = 0; xx < P::NX; ++xx) own[xx] = o[H][xx] * inv;
           merge_split_rows<D, E>(a, ro, rl, x0, ncontrib, slot_x0, fast ? gid - x0 : -1, urow,
-                                 st_orow, fast ? own_lse : kNegInf,
-                                 fast && own_lse != kNegInf ? 1.f : 0.f, num);
+                                 st_orow, own, own_lse);
         }
       }
     }
@@ -1333,13 +1341,11 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
       const int urow = r * 16 * RT + 16 * H + n;
       if (urow < f_rows) {
         const int row = f_r0 + urow;
-        f32x4 num[P::NX];
-#pragma unroll
-        for (int xx = 0; xx < P::NX; ++xx) num[xx] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 none[P::NX] = {};
         merge_split_rows<D, E>(a, part_rsrc_o<D>(a, pl.rg.nwg), part_rsrc_lse(a, pl.rg.nwg), f_x0,
                                f_n, f_slot_x0, -1, (uint32_t)urow,
-                               (int64_t)(f_q0 + row / G) * a.Hq + f_h * G + row % G, kNegInf,
-                               0.f, num);
+                               (int64_t)(f_q0 + row / G) * a.Hq + f_h * G + row % G, none,
+                               kNegInf);
       }
     }
   }

@@ -151,3 +151,25 @@ def test_split_prefill_repeated_calls_and_shapes_share_the_workspace():
     for _ in range(3):
         np.testing.assert_array_equal(_run(*a), first_a)
         np.testing.assert_array_equal(_run(*b), first_b)
+
+
+def test_stream_k_merge_is_deterministic_whoever_merges():
+    """A split unit is merged by whichever contributor draws the last ticket, from its
+    registers or from memory: the result must not depend on which (same bits on every
+    call), and must match the oracle.  C4 splits nearly every unit; 12 calls on 4
+    rotating pool copies vary the timing."""
+    w = workloads.c4_workload()
+    d = w.to(DEV)
+    max_q = int((w.q_offsets[1:] - w.q_offsets[:-1]).max())
+    pools = [(d.k_pool, d.v_pool)] + [(d.k_pool.clone(), d.v_pool.clone()) for _ in range(3)]
+    outs = []
+    for i in range(12):
+        kp, vp = pools[i % 4]
+        outs.append(ops.prefill_paged(d.q, kp, vp, d.block_tables, d.q_offsets, d.context_lens,
+                                      max_q))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs[1:], 1):
+        assert torch.equal(o, outs[0]), f"call {i} differs from call 0"
+    exp = R.prefill_reference(w.q.numpy(), w.q_offsets.numpy(), w.context_lens.numpy(),
+                              w.k_pool.numpy(), w.v_pool.numpy(), w.block_tables.numpy(), 16)
+    assert_attention_close(outs[0].cpu().numpy(), exp, what="C4 repeated")
