@@ -55,8 +55,13 @@ SIGNATURES: dict[str, tuple] = {
                               _f, _p, _sz, _p]),
     "fe_prefill_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
 }
+SIGNATURES["fe_prefill_plan_size"] = (_sz, [_i, _i, _i, _i])
+SIGNATURES["fe_prefill_plan"] = (_i, [_p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p])
+SIGNATURES["fe_prefill_paged_planned"] = (
+    _i, SIGNATURES["fe_prefill_paged"][1][:-1] + [_p, _sz, _p])
 # the bf16 forms take the fp16 entry points' arguments
-for _name in ("fe_paged_decode", "fe_paged_decode_planned", "fe_prefill_paged"):
+for _name in ("fe_paged_decode", "fe_paged_decode_planned", "fe_prefill_paged",
+              "fe_prefill_paged_planned"):
     SIGNATURES[_name + "_bf16"] = SIGNATURES[_name]
 SIGNATURES |= {
     # include/flexengine_amd_model.h

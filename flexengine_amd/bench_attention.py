@@ -12,8 +12,9 @@ stream -- and prints one JSON line per config:
   the compulsory unique bytes, and the "effective" GB/s over the logical bytes,
   for the plain decode and for the shared-prefix (cascade) decode.
 * C4 (mixed step): the ragged prefill launch in TFLOP/s over the valid
-  query-key pairs against the 2.5 PFLOP/s fp16 MFMA peak, the 48 decode rows
-  in GB/s, and the whole step.
+  query-key pairs against the 2.5 PFLOP/s fp16 MFMA peak (also with the
+  step's plan, fe_prefill_plan once per 28 calls as in a 28-layer model step),
+  the 48 decode rows in GB/s, and the whole step.
 
 Calls are replayed from a HIP graph, so each figure is GPU time per call.
 `--dtype bf16` runs the bf16 entry points on the same values rounded to bf16
@@ -30,6 +31,7 @@ import torch
 from flexengine_amd import ops, workloads
 
 HBM_PEAK = 8.0e12
+LAYERS = 28  # Qwen2.5-1.5B: calls per model step that share one plan
 MFMA_FP16_PEAK = 2.5e15
 
 
@@ -118,6 +120,19 @@ def bench_c4(iters: int, copies: int, dtype=torch.float16) -> dict:
         kp, vp = pools[i % len(pools)]
         ops.prefill_paged(d.q, kp, vp, d.block_tables, d.q_offsets, d.context_lens, max_q, out=out)
 
+    # one plan per model step of 28 layers (fe_prefill_plan), charged 1/28 per call
+    hq, hkv = d.q.shape[1], d.k_pool.shape[2]
+    plan = ops.prefill_paged_plan(d.q_offsets, d.context_lens, d.q.shape[0], hq, hkv,
+                                  d.block_tables.shape[1], d.k_pool.shape[1])
+
+    def prefill_planned(i):
+        kp, vp = pools[i % len(pools)]
+        if i % LAYERS == 0:
+            ops.prefill_paged_plan(d.q_offsets, d.context_lens, d.q.shape[0], hq, hkv,
+                                   d.block_tables.shape[1], d.k_pool.shape[1], out=plan)
+        ops.prefill_paged(d.q, kp, vp, d.block_tables, d.q_offsets, d.context_lens, max_q,
+                          out=out, plan=plan)
+
     dec = d.decode
     dout = torch.empty_like(dec.q)
 
@@ -143,6 +158,7 @@ def bench_c4(iters: int, copies: int, dtype=torch.float16) -> dict:
         main.wait_stream(side)
 
     t_pre = _timed(prefill, iters, len(pools))
+    t_plan = _timed(prefill_planned, iters, LAYERS) if plan is not None else None
     t_dec = _timed(decode, iters, len(pools))
     t_all = _timed(both, iters, len(pools))
     t_ovl = _timed(both_overlapped, iters, len(pools))
@@ -151,6 +167,9 @@ def bench_c4(iters: int, copies: int, dtype=torch.float16) -> dict:
     return {"config": "C4", "prefill_us": round(t_pre * 1e6, 2), "prefill_flops": flops,
             "prefill_TFLOP_s": round(flops / t_pre / 1e12, 1),
             "pct_mfma_fp16_peak": round(100 * flops / t_pre / MFMA_FP16_PEAK, 2),
+            "prefill_planned_us": None if t_plan is None else round(t_plan * 1e6, 2),
+            "pct_mfma_fp16_peak_planned":
+                None if t_plan is None else round(100 * flops / t_plan / MFMA_FP16_PEAK, 2),
             "decode_us": round(t_dec * 1e6, 2), "decode_bytes": dbytes,
             "decode_GB_s": round(dbytes / t_dec / 1e9, 1), "step_us": round(t_all * 1e6, 2),
             "step_overlap_us": round(t_ovl * 1e6, 2),

@@ -85,6 +85,9 @@ struct PrefillArgs {
                      // stream-K kernel's partials [2 * nwg_max * 128][D]
   float* part_lse;   // [KS][total_q * Hq] base-2 LSE of each partial
   int* tickets;      // [row blocks * Hkv] (stream-K kernel: [nwg_max]), zero between calls
+  // stream-K kernel: the step's plan (fe_prefill_plan), null to derive the
+  // work split in the launch
+  const int* plan;
   int64_t q_stride;  // elements from one query row (token or sequence) to the next
   int W, S, total_q, Hq, Hkv, G, BS, bs_log2, NB, KS;
   int nwg_max;       // stream-K kernel: workgroups of the launch
@@ -1351,7 +1354,48 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
   }
 }
 
-template <int D, int RT, class E = Fp16>
+// ---- per-step plan of the stream-K kernel (fe_prefill_plan) -----------------
+//
+// The work split depends only on q_offsets, context_lens and the sizes, which
+// every layer of a model step shares: fe_prefill_plan computes it once -- the
+// ranges and, per workgroup, its range and first unit -- and
+// fe_prefill_paged_planned reads it with one load instead of the scans of
+// stream_plan and stream_locate.  Layout (int32): a header of kPPlanInts
+// (nwg, T, q, r of the Ranges), then kPPlanInts per workgroup: x_begin,
+// x_end, has work, logical id, then the StreamPos s, h, rb, kb, q0, n,
+// cached, R, tb.
+constexpr int kPPlanInts = 16;
+inline size_t pplan_bytes() { return (size_t)(1 + kMaxStreamWgs) * kPPlanInts * sizeof(int32_t); }
+
+// One wave per workgroup entry of the launch the plan is for (grid nwg_max).
+__global__ __launch_bounds__(kWave) void prefill_plan_kernel(const PrefillArgs a, int* plan) {
+  const StreamPlan pl = stream_plan(a);
+  const int nwg = pl.rg.nwg;
+  const int lane = lane_id();
+  if (blockIdx.x == 0 && lane < kPPlanInts) {
+    const int hdr[4] = {nwg, pl.rg.T, pl.rg.q, pl.rg.r};
+    plan[lane] = lane < 4 ? hdr[lane] : 0;
+  }
+  int e[13] = {};
+  if ((int)blockIdx.x < nwg) {
+    const int gid = logical_wg(blockIdx.x, nwg);
+    const int x_begin = pl.rg.start(gid);
+    const int x_end = pl.rg.start(gid + 1);
+    StreamPos sp{};
+    if (x_begin < x_end && stream_locate(a, pl.w0, x_begin, sp)) {
+      const int v[13] = {x_begin, x_end, 1, gid, sp.s, sp.h, sp.rb, sp.kb,
+                         sp.w.q0, sp.w.n, sp.w.cached, sp.w.R, sp.w.tb};
+#pragma unroll
+      for (int i = 0; i < 13; ++i) e[i] = v[i];
+    }
+  }
+  int out = 0;
+#pragma unroll
+  for (int i = 0; i < 13; ++i) out = lane == i ? e[i] : out;
+  if (lane < kPPlanInts) plan[kPPlanInts + (int)blockIdx.x * kPPlanInts + lane] = out;
+}
+
+template <int D, int RT, class E = Fp16, bool PLANNED = false>
 __global__ __launch_bounds__(kDmaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_dma_kernel(const PrefillArgs a) {
   using P = DCfg<D>;
@@ -1372,15 +1416,41 @@ void prefill_dma_kernel(const PrefillArgs a) {
   // parameters
   __shared__ int last[9];
 
-  const StreamPlan pl = stream_plan(a);
-  const int nwg = pl.rg.nwg;
-  if ((int)blockIdx.x >= nwg) return;
-  const int gid = logical_wg(blockIdx.x, nwg);
-  const int x_begin = pl.rg.start(gid);
-  const int x_end = pl.rg.start(gid + 1);
-  if (x_begin >= x_end) return;
+  StreamPlan pl;
   StreamPos sp;
-  if (!stream_locate(a, pl.w0, x_begin, sp)) return;
+  int gid, x_begin, x_end;
+  if constexpr (PLANNED) {
+    // the ranges and this workgroup's first unit from the plan: its header and
+    // entry in one round trip (lanes 0-15 the entry, 16-31 the header)
+    const int lane = lane_id();
+    const int v = lane < kPPlanInts
+                      ? a.plan[kPPlanInts + (int)blockIdx.x * kPPlanInts + lane]
+                      : (lane < 2 * kPPlanInts ? a.plan[lane - kPPlanInts] : 0);
+    pl.rg = Ranges{readlane_i(v, 16 + 1), readlane_i(v, 16 + 0), readlane_i(v, 16 + 2),
+                   readlane_i(v, 16 + 3)};
+    pl.w0 = SeqWork{};
+    if ((int)blockIdx.x >= pl.rg.nwg || readlane_i(v, 2) == 0) return;
+    x_begin = readlane_i(v, 0);
+    x_end = readlane_i(v, 1);
+    gid = readlane_i(v, 3);
+    sp.s = readlane_i(v, 4);
+    sp.h = readlane_i(v, 5);
+    sp.rb = readlane_i(v, 6);
+    sp.kb = readlane_i(v, 7);
+    sp.w.q0 = readlane_i(v, 8);
+    sp.w.n = readlane_i(v, 9);
+    sp.w.cached = readlane_i(v, 10);
+    sp.w.R = readlane_i(v, 11);
+    sp.w.tb = readlane_i(v, 12);
+  } else {
+    pl = stream_plan(a);
+    if ((int)blockIdx.x >= pl.rg.nwg) return;
+    gid = logical_wg(blockIdx.x, pl.rg.nwg);
+    x_begin = pl.rg.start(gid);
+    x_end = pl.rg.start(gid + 1);
+    if (x_begin >= x_end) return;
+    if (!stream_locate(a, pl.w0, x_begin, sp)) return;
+  }
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = w % kHalfWaves;
@@ -1430,8 +1500,12 @@ inline int stream_wgs() { return device_cus(); }
 template <int D, class E>
 void launch_prefill_dma(const PrefillArgs& a, hipStream_t stream) {
   constexpr int RT = kDmaRt;
-  hipLaunchKernelGGL((prefill_dma_kernel<D, RT, E>), dim3(a.nwg_max), dim3(kDmaThreads), 0,
-                     stream, a);
+  if (a.plan != nullptr)
+    hipLaunchKernelGGL((prefill_dma_kernel<D, RT, E, true>), dim3(a.nwg_max), dim3(kDmaThreads),
+                       0, stream, a);
+  else
+    hipLaunchKernelGGL((prefill_dma_kernel<D, RT, E>), dim3(a.nwg_max), dim3(kDmaThreads), 0,
+                       stream, a);
 }
 
 constexpr int kMaxTickets = 65536;
@@ -1517,7 +1591,8 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
                  const int32_t* block_tables, int table_stride, const int32_t* q_offsets,
                  const int32_t* context_lens, int num_seqs, int total_q, int max_q_len,
                  int num_q_heads, int kv_heads, int head_dim, int block_size, float scale,
-                 void* workspace, size_t workspace_bytes, fe_stream_t stream, bool bf16) {
+                 void* workspace, size_t workspace_bytes, fe_stream_t stream, bool bf16,
+                 const void* step_plan = nullptr, size_t plan_bytes = 0) {
   FE_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 &&
                kv_heads > 0 && num_blocks > 0 && table_stride > 0);
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
@@ -1536,6 +1611,10 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   const Plan p = plan(num_seqs, total_q, num_q_heads, kv_heads);
   // split-K tickets of prefill_kernel: one per (row block, KV head)
   if (!dma && (int64_t)p.blocks * kv_heads > kMaxTickets) return FE_ERR_UNSUPPORTED;
+  // a plan is for the stream-K kernel (fe_prefill_plan refuses the sizes it cannot take)
+  if (step_plan != nullptr && !dma) return FE_ERR_UNSUPPORTED;
+  if (step_plan != nullptr && (plan_bytes < pplan_bytes() || !aligned16(step_plan)))
+    return FE_ERR_WORKSPACE;
   const size_t need = fe_prefill_workspace_size(num_seqs, total_q, num_q_heads, kv_heads, head_dim);
   if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
     return FE_ERR_WORKSPACE;
@@ -1573,6 +1652,7 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   a.pre_o = nullptr;
   a.pre_lse = nullptr;
   a.tok0 = nullptr;
+  a.plan = (const int*)step_plan;
   hipStream_t s = (hipStream_t)stream;
   if (bf16 && !dma) return FE_ERR_UNSUPPORTED;  // bf16: the stream-K kernel only
   if (dma && bf16) {
@@ -1613,6 +1693,73 @@ extern "C" int fe_prefill_paged_bf16(const void* q, void* out, const void* k_poo
                       block_size, scale, workspace, workspace_bytes, stream, true);
 }
 
+extern "C" size_t fe_prefill_plan_size(int num_seqs, int total_q, int num_q_heads,
+                                       int kv_heads) {
+  if (num_seqs < 0 || total_q < 0 || num_q_heads <= 0 || kv_heads <= 0) return 0;
+  return pplan_bytes();
+}
+
+extern "C" int fe_prefill_plan(const int32_t* q_offsets, const int32_t* context_lens,
+                               int num_seqs, int total_q, int num_q_heads, int kv_heads,
+                               int table_stride, int block_size, void* plan, size_t plan_bytes,
+                               fe_stream_t stream) {
+  FE_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && num_q_heads > 0 && kv_heads > 0 &&
+               table_stride > 0);
+  FE_CHECK_ARG(num_q_heads % kv_heads == 0);
+  const int bs_log2 = log2_exact(block_size);
+  if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
+  const int nwg = stream_wgs();
+  if (!stream_ok(block_size, table_stride, total_q, num_q_heads / kv_heads, num_seqs, kv_heads,
+                 nwg))
+    return FE_ERR_UNSUPPORTED;
+  if (plan == nullptr || plan_bytes < pplan_bytes() || !aligned16(plan)) return FE_ERR_WORKSPACE;
+  if (num_seqs == 0 || total_q == 0) return FE_OK;
+  FE_CHECK_ARG(q_offsets && context_lens);
+  PrefillArgs a{};
+  a.q_off = q_offsets;
+  a.ctx = context_lens;
+  a.W = table_stride;
+  a.S = num_seqs;
+  a.total_q = total_q;
+  a.Hq = num_q_heads;
+  a.Hkv = kv_heads;
+  a.G = num_q_heads / kv_heads;
+  a.BS = block_size;
+  a.bs_log2 = bs_log2;
+  a.nwg_max = nwg;
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(nwg), dim3(kWave), 0, (hipStream_t)stream, a,
+                     (int*)plan);
+  return FE_LAUNCH_STATUS();
+}
+
+extern "C" int fe_prefill_paged_planned(const void* q, void* out, const void* k_pool,
+                                        const void* v_pool, int num_blocks,
+                                        const int32_t* block_tables, int table_stride,
+                                        const int32_t* q_offsets, const int32_t* context_lens,
+                                        int num_seqs, int total_q, int max_q_len, int num_q_heads,
+                                        int kv_heads, int head_dim, int block_size, float scale,
+                                        void* workspace, size_t workspace_bytes, const void* plan,
+                                        size_t plan_bytes, fe_stream_t stream) {
+  FE_CHECK_ARG(plan != nullptr);
+  return prefill_impl(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride, q_offsets,
+                      context_lens, num_seqs, total_q, max_q_len, num_q_heads, kv_heads, head_dim,
+                      block_size, scale, workspace, workspace_bytes, stream, false, plan,
+                      plan_bytes);
+}
+
+extern "C" int fe_prefill_paged_planned_bf16(
+    const void* q, void* out, const void* k_pool, const void* v_pool, int num_blocks,
+    const int32_t* block_tables, int table_stride, const int32_t* q_offsets,
+    const int32_t* context_lens, int num_seqs, int total_q, int max_q_len, int num_q_heads,
+    int kv_heads, int head_dim, int block_size, float scale, void* workspace,
+    size_t workspace_bytes, const void* plan, size_t plan_bytes, fe_stream_t stream) {
+  FE_CHECK_ARG(plan != nullptr);
+  return prefill_impl(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride, q_offsets,
+                      context_lens, num_seqs, total_q, max_q_len, num_q_heads, kv_heads, head_dim,
+                      block_size, scale, workspace, workspace_bytes, stream, true, plan,
+                      plan_bytes);
+}
+
 namespace fe {
 
 size_t cascade_prefix_scratch_bytes(int num_groups, int batch, int hq, int hkv, int d) {
@@ -1628,6 +1775,7 @@ int cascade_prefix_launch(const CascadePrefix& c, hipStream_t stream) {
   if ((int64_t)c.num_blocks * c.bs >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
   if (!(c.scale > 0.f)) return FE_ERR_INVALID_ARGUMENT;  // row max on unscaled scores
   PrefillArgs a;
+  a.plan = nullptr;
   a.q = (const f16*)c.q;
   a.out = nullptr;
   a.k_pool = (const f16*)c.k_pool;

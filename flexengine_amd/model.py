@@ -9,8 +9,10 @@ no network for checkpoints).
   chunk (request_id, input_ids, start) is a run of tokens at absolute
   positions start..start+n-1; per layer the new K/V rows are written to the
   paged pool *before* attention, and attention is causal per request.  All
-  chunks' K/V go through one fe_write_kv launch and all chunks' attention
-  through one fe_prefill_paged launch (the reference loops over requests).
+  chunks' K/V go through one fe_write_kv_ragged launch and all chunks'
+  attention through one fe_prefill_paged_planned launch (the reference loops
+  over requests), whose work split one fe_prefill_plan launch per forward
+  computes for every layer.
   Returns the last-token logits of each chunk.
 * decode_static(input_ids, positions, block_tables, active_mask, cache) -- the
   graph-compatible one-token step of qwen2.py:138-186 over fixed padded batch
@@ -176,13 +178,18 @@ class Qwen2Model:
                                  dtype=torch.int32).to(dev)
         ctx = torch.tensor([c.start + n for c, n in zip(chunks, lengths)], dtype=torch.int32).to(dev)
         max_q = max(lengths)
+        # the prefill's work split of this step, shared by every layer (None when
+        # the sizes take the tile kernel)
+        plan = ops.prefill_paged_plan(q_offsets, ctx, len(pos_list),
+                                      self.cfg.num_attention_heads, self.cfg.num_key_value_heads,
+                                      width, bs)
         x = self.embed.index_select(0, ids)
         h, _ = ops.rmsnorm(x, self.layer_weights[0].input_norm, self.cfg.rms_norm_eps)
         for layer, lw in enumerate(self.layer_weights):
             q, k, v = self._qkv(h, lw, positions)
             ops.write_kv_ragged(k, v, cache.k[layer], cache.v[layer], tables, q_offsets, ctx)
             attn = ops.prefill_paged(q, cache.k[layer], cache.v[layer], tables, q_offsets, ctx,
-                                     max_q, scale=self.scale)
+                                     max_q, scale=self.scale, plan=plan)
             h = self._after_attention(x, attn, lw, self._next_norm(layer))
         ends = torch.tensor([sum(lengths[:j + 1]) - 1 for j in range(len(lengths))],
                             dtype=torch.long).to(dev)

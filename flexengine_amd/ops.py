@@ -397,14 +397,57 @@ def lse_merge(part_out: torch.Tensor, part_lse: torch.Tensor,
 # prefill
 # ---------------------------------------------------------------------------------------
 
+@dataclass(frozen=True)
+class PrefillPlan:
+    """A step's stream-K prefill work split (fe_prefill_plan), for the tensors
+    and sizes it was computed from."""
+    buffer: torch.Tensor
+    q_offsets_ptr: int
+    lens_ptr: int
+    shape: tuple  # (num_seqs, total_q, num_q_heads, kv_heads, table_stride, block_size)
+
+
+def prefill_paged_plan(q_offsets: torch.Tensor, context_lens: torch.Tensor, total_q: int,
+                       num_q_heads: int, kv_heads: int, table_stride: int, block_size: int, *,
+                       out: PrefillPlan | None = None) -> PrefillPlan | None:
+    """The work split every layer's prefill_paged(..., plan=) of one step reuses (the
+    offsets and lengths must not change between those calls); None when the sizes
+    take the tile kernel, which has no plan.  `out` reuses an earlier plan's buffer."""
+    dev = _require_gpu(q_offsets, context_lens)
+    q_offsets = _int32(q_offsets, "q_offsets")
+    context_lens = _int32(context_lens, "context_lens")
+    num_seqs = context_lens.shape[0]
+    shape = (num_seqs, int(total_q), int(num_q_heads), int(kv_heads), int(table_stride),
+             int(block_size))
+    need = int(_lib.load().fe_prefill_plan_size(num_seqs, int(total_q), int(num_q_heads),
+                                                int(kv_heads)))
+    if out is not None:
+        if out.shape != shape:
+            raise ValueError(f"plan buffer is for sizes {out.shape}, not {shape}")
+        buffer = out.buffer
+    else:
+        buffer = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    rc = _lib.load().fe_prefill_plan(q_offsets.data_ptr(), context_lens.data_ptr(), num_seqs,
+                                     int(total_q), int(num_q_heads), int(kv_heads),
+                                     int(table_stride), int(block_size), buffer.data_ptr(),
+                                     buffer.numel(), _stream(dev))
+    if rc == _lib.FE_ERR_UNSUPPORTED:
+        return None
+    _lib.check("fe_prefill_plan", rc)
+    return PrefillPlan(buffer, q_offsets.data_ptr(), context_lens.data_ptr(), shape)
+
+
 def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                   block_tables: torch.Tensor, q_offsets: torch.Tensor,
                   context_lens: torch.Tensor, max_q_len: int, *, scale: float | None = None,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
+                  out: torch.Tensor | None = None,
+                  plan: PrefillPlan | None = None) -> torch.Tensor:
     """Ragged causal prefill: q [total_q, Hq, D]; sequence s owns rows
     q_offsets[s]:q_offsets[s+1] at positions context_lens[s]-n_s .. context_lens[s]-1.
     fp16 or bf16 (q, out and the pools alike; bf16 needs block sizes that are
-    multiples of 16)."""
+    multiples of 16).  With `plan` (prefill_paged_plan on these q_offsets /
+    context_lens and sizes) the launch reads its work split from it
+    (fe_prefill_paged_planned); same results."""
     dev = _require_gpu(q, k_pool, v_pool, block_tables, q_offsets, context_lens, out)
     nb, bs, hkv, d = _check_pool(k_pool, v_pool, KV_DTYPES)
     if q.ndim != 3 or q.shape[2] != d or q.dtype != k_pool.dtype or not q.is_contiguous():
@@ -426,10 +469,20 @@ def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
         scale = 1.0 / math.sqrt(d)
     need = int(_lib.load().fe_prefill_workspace_size(num_seqs, total_q, hq, hkv, d))
     ws = decode_workspace(dev, need, kind="prefill")
-    _lib.call("fe_prefill_paged_bf16" if q.dtype == BF16 else "fe_prefill_paged", q.data_ptr(), out.data_ptr(), k_pool.data_ptr(),
-              v_pool.data_ptr(), nb, block_tables.data_ptr(), block_tables.shape[1],
-              q_offsets.data_ptr(), context_lens.data_ptr(), num_seqs, total_q, int(max_q_len),
-              hq, hkv, d, bs, float(scale), ws.data_ptr(), ws.numel(), _stream(dev))
+    args = (q.data_ptr(), out.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), nb,
+            block_tables.data_ptr(), block_tables.shape[1], q_offsets.data_ptr(),
+            context_lens.data_ptr(), num_seqs, total_q, int(max_q_len), hq, hkv, d, bs,
+            float(scale), ws.data_ptr(), ws.numel())
+    sfx = "_bf16" if q.dtype == BF16 else ""
+    if plan is None:
+        _lib.call("fe_prefill_paged" + sfx, *args, _stream(dev))
+        return out
+    shape = (num_seqs, total_q, hq, hkv, block_tables.shape[1], bs)
+    if plan.shape != shape or plan.q_offsets_ptr != q_offsets.data_ptr() or \
+            plan.lens_ptr != context_lens.data_ptr():
+        raise ValueError("the plan was computed for other q_offsets / context_lens or sizes")
+    _lib.call("fe_prefill_paged_planned" + sfx, *args, plan.buffer.data_ptr(),
+              plan.buffer.numel(), _stream(dev))
     return out
 
 

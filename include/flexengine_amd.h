@@ -371,6 +371,44 @@ int fe_prefill_paged_bf16(const void* q, void* out,
                           void* workspace, size_t workspace_bytes, fe_stream_t stream);
 
 /*
+ * Prefill plan of one model step: the stream-K work split of fe_prefill_paged
+ * -- every workgroup's range of key blocks and its first unit -- depends only
+ * on q_offsets, context_lens and the sizes, which all layers of a step share.
+ * fe_prefill_plan computes it once into a caller-owned device buffer of
+ * fe_prefill_plan_size(...) bytes (16-byte aligned); fe_prefill_paged_planned
+ * (and its bf16 form) is fe_prefill_paged reading the split from it, with the
+ * same results.  The plan must come from the same q_offsets, context_lens,
+ * table_stride, block_size and head counts, and be complete (stream order)
+ * before the planned calls.  Sizes the stream-K kernel does not take (block
+ * sizes not a multiple of 16, or beyond its 32-bit work split) return
+ * FE_ERR_UNSUPPORTED from fe_prefill_plan; such steps call fe_prefill_paged.
+ * No counterpart in the reference: its prefill has no work split to plan; one
+ * plan serves the 28 per-layer calls of qwen2.py:117-126's ragged forward.
+ */
+size_t fe_prefill_plan_size(int num_seqs, int total_q, int num_q_heads, int kv_heads);
+int fe_prefill_plan(const int32_t* q_offsets, const int32_t* context_lens, int num_seqs,
+                    int total_q, int num_q_heads, int kv_heads, int table_stride,
+                    int block_size, void* plan, size_t plan_bytes, fe_stream_t stream);
+int fe_prefill_paged_planned(const void* q, void* out,
+                             const void* k_pool, const void* v_pool, int num_blocks,
+                             const int32_t* block_tables, int table_stride,
+                             const int32_t* q_offsets, const int32_t* context_lens,
+                             int num_seqs, int total_q, int max_q_len,
+                             int num_q_heads, int kv_heads, int head_dim,
+                             int block_size, float scale,
+                             void* workspace, size_t workspace_bytes,
+                             const void* plan, size_t plan_bytes, fe_stream_t stream);
+int fe_prefill_paged_planned_bf16(const void* q, void* out,
+                                  const void* k_pool, const void* v_pool, int num_blocks,
+                                  const int32_t* block_tables, int table_stride,
+                                  const int32_t* q_offsets, const int32_t* context_lens,
+                                  int num_seqs, int total_q, int max_q_len,
+                                  int num_q_heads, int kv_heads, int head_dim,
+                                  int block_size, float scale,
+                                  void* workspace, size_t workspace_bytes,
+                                  const void* plan, size_t plan_bytes, fe_stream_t stream);
+
+/*
  * Bytes of device workspace fe_prefill_paged needs for these sizes (its key
  * splits keep fp32 partial outputs there).  Like the decode workspace it must
  * be zero-filled before its first use; every call leaves its ticket region

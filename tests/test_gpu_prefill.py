@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from flexengine_amd import attention, ops, workloads
+from flexengine_amd import _lib, attention, ops, workloads
 from flexengine_amd.kv_cache import CacheLayout, PagedKVCache
 from oracle import paged_ref as R
 from tests.parity import assert_attention_close
@@ -173,3 +173,68 @@ def test_stream_k_merge_is_deterministic_whoever_merges():
     exp = R.prefill_reference(w.q.numpy(), w.q_offsets.numpy(), w.context_lens.numpy(),
                               w.k_pool.numpy(), w.v_pool.numpy(), w.block_tables.numpy(), 16)
     assert_attention_close(outs[0].cpu().numpy(), exp, what="C4 repeated")
+
+
+# --------------------------------------------------------------------------------------
+# prefill plan (fe_prefill_plan / fe_prefill_paged_planned): one plan per model step,
+# reused by every layer; results must be bit-identical to the unplanned launch
+# --------------------------------------------------------------------------------------
+
+def _planned_prefill_cases():
+    w = workloads.c4_workload()
+    c4 = (w.q, w.q_offsets, w.context_lens, w.block_tables, w.k_pool, w.v_pool, 16)
+    small = _case(61, [130, 7, 1], [0, 40, 999]) + (16,)
+    bs32 = _case(62, [70, 3], [25, 200], 16, 2, 128, 32) + (32,)
+    d64 = _case(63, [300, 1, 45], [0, 2048, 17], 14, 2, 64, 16) + (16,)
+    return {"C4": c4, "small": small, "bs32": bs32, "d64-g7": d64}
+
+
+@pytest.mark.parametrize("name", ["C4", "small", "bs32", "d64-g7"])
+def test_planned_prefill_is_bit_identical_and_reusable(name):
+    q, offs, ctx, tables, kp, vp, bs = _planned_prefill_cases()[name]
+    print(f"planned prefill case {name}", flush=True)
+    hq, hkv = q.shape[1], kp.shape[2]
+    offs_d, ctx_d, tables_d = offs.to(DEV), ctx.to(DEV), tables.to(DEV)
+    max_q = int((offs[1:] - offs[:-1]).max())
+    plan = ops.prefill_paged_plan(offs_d, ctx_d, q.shape[0], hq, hkv, tables.shape[1], bs)
+    assert plan is not None
+    # three "layers": own pools and queries, the same offsets, lengths and tables
+    for layer in range(3):
+        g = torch.Generator().manual_seed(200 + layer)
+        ql = torch.randn(q.shape, generator=g).half().to(DEV)
+        kl = torch.randn(kp.shape, generator=g).half().to(DEV)
+        vl = torch.randn(vp.shape, generator=g).half().to(DEV)
+        ref = ops.prefill_paged(ql, kl, vl, tables_d, offs_d, ctx_d, max_q)
+        got = ops.prefill_paged(ql, kl, vl, tables_d, offs_d, ctx_d, max_q, plan=plan)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"{name} layer {layer}: planned output differs"
+    got = ops.prefill_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), tables_d, offs_d, ctx_d, max_q,
+                            plan=plan)
+    exp = R.prefill_reference(q.numpy(), offs.numpy(), ctx.numpy(), kp.numpy(), vp.numpy(),
+                              tables.numpy(), bs)
+    assert_attention_close(got.cpu().numpy(), exp, what=f"planned {name}")
+
+
+def test_planned_prefill_bf16_and_refusals():
+    """The bf16 planned form matches the bf16 unplanned one bit for bit; a plan for other
+    tensors is refused; block sizes the stream-K kernel does not take have no plan."""
+    q, offs, ctx, tables, kp, vp, bs = _planned_prefill_cases()["small"]
+    qb, kb, vb = (t.float().to(torch.bfloat16).to(DEV) for t in (q, kp, vp))
+    offs_d, ctx_d, tables_d = offs.to(DEV), ctx.to(DEV), tables.to(DEV)
+    max_q = int((offs[1:] - offs[:-1]).max())
+    plan = ops.prefill_paged_plan(offs_d, ctx_d, q.shape[0], q.shape[1], kp.shape[2],
+                                  tables.shape[1], bs)
+    ref = ops.prefill_paged(qb, kb, vb, tables_d, offs_d, ctx_d, max_q)
+    got = ops.prefill_paged(qb, kb, vb, tables_d, offs_d, ctx_d, max_q, plan=plan)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.bfloat16 and torch.equal(got, ref)
+    with pytest.raises(ValueError, match="other q_offsets"):
+        ops.prefill_paged(qb, kb, vb, tables_d, offs_d, ctx_d.clone(), max_q, plan=plan)
+    q4, offs4, ctx4, tables4, _, _ = _case(64, [20], [7], 8, 8, 64, 4)
+    assert ops.prefill_paged_plan(offs4.to(DEV), ctx4.to(DEV), q4.shape[0], 8, 8,
+                                  tables4.shape[1], 4) is None
+    small = torch.empty(16, dtype=torch.uint8, device=DEV)
+    rc = _lib.load().fe_prefill_plan(offs_d.data_ptr(), ctx_d.data_ptr(), ctx.shape[0],
+                                     q.shape[0], q.shape[1], kp.shape[2], tables.shape[1], bs,
+                                     small.data_ptr(), small.numel(), None)
+    assert rc == _lib.FE_ERR_WORKSPACE
