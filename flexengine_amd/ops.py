@@ -132,10 +132,12 @@ def write_kv_decode(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tens
                     context_lens: torch.Tensor) -> None:
     """Writes row b at position context_lens[b]-1 of sequence b; rows with length 0 are skipped."""
     dev = _require_gpu(k_new, v_new, k_pool, v_pool, block_tables, context_lens)
-    nb, bs, hkv, d = _check_pool(k_pool, v_pool)
+    nb, bs, hkv, d = _check_pool(k_pool, v_pool, KV_DTYPES)
     batch = k_new.shape[0]
     if k_new.shape != v_new.shape or tuple(k_new.shape[1:]) != (hkv, d):
         raise ValueError("K/V shapes must be [batch, kv_heads, head_dim]")
+    if k_new.dtype != k_pool.dtype or v_new.dtype != k_pool.dtype:
+        raise ValueError("wrong KV dtype")
     if k_new.stride() != v_new.stride() or k_new.stride(2) != 1 or k_new.stride(1) != d:
         raise ValueError("new K/V rows must have contiguous heads and equal strides")
     block_tables = _int32(block_tables, "block_tables")

@@ -234,3 +234,44 @@ def test_bf16_unsupported_forms_are_refused():
         ops.paged_decode(w.q.half(), w.k_pool, w.v_pool, w.block_tables, w.context_lens)
     with pytest.raises(ValueError, match="same"):
         ops.paged_decode(w.q, w.k_pool, w.v_pool.half(), w.block_tables, w.context_lens)
+
+
+def test_bf16_page_writes_and_gather_are_byte_copies():
+    """fe_write_kv, fe_write_kv_decode and fe_gather_kv move 16-bit words: with bf16 pools
+    they are bit-exact against the oracle's copies of the int16 bits; a new-row dtype that
+    differs from the pools' is refused."""
+    g = torch.Generator().manual_seed(505)
+    nb, bs, h, d, b = 48, 16, 2, 128, 5
+    kp = torch.randn(nb, bs, h, d, generator=g).to(BF16)
+    vp = torch.randn(nb, bs, h, d, generator=g).to(BF16)
+    tables = torch.randperm(nb, generator=g)[: b * 8].view(b, 8).to(torch.int32)
+    ctx = torch.tensor([1, 0, 16, 17, 128], dtype=torch.int32)
+    kn = torch.randn(b, h, d, generator=g).to(BF16)
+    vn = torch.randn(b, h, d, generator=g).to(BF16)
+    ek, ev = kp.view(torch.int16).numpy().copy(), vp.view(torch.int16).numpy().copy()
+    R.write_kv_decode(ek, ev, tables.numpy(), ctx.numpy(), kn.view(torch.int16).numpy(),
+                      vn.view(torch.int16).numpy(), bs)
+    kd, vd = kp.to(DEV), vp.to(DEV)
+    ops.write_kv_decode(kn.to(DEV), vn.to(DEV), kd, vd, tables.to(DEV), ctx.to(DEV))
+    torch.cuda.synchronize()
+    assert kd.cpu().view(torch.int16).numpy().tobytes() == ek.tobytes()
+    assert vd.cpu().view(torch.int16).numpy().tobytes() == ev.tobytes()
+    # slot writes of 3 rows, then the gather of every row of sequence 3
+    rows_k = torch.randn(3, h, d, generator=g).to(BF16)
+    blocks = tables[3, :1].repeat(3)
+    offs = torch.tensor([2, 3, 4], dtype=torch.int32)
+    ops.write_kv(rows_k.to(DEV), rows_k.to(DEV), kd, vd, blocks.to(DEV), offs.to(DEV))
+    R.write_kv(ek, ev, tables[3].tolist(), 2, rows_k.view(torch.int16).numpy(),
+               rows_k.view(torch.int16).numpy(), bs)
+    n = int(ctx[3])
+    ko, vo = ops.gather_kv(kd, vd, tables[3:4].to(DEV), ctx[3:4].to(DEV),
+                           torch.tensor([0, n], dtype=torch.int32, device=DEV), n)
+    torch.cuda.synchronize()
+    assert ko.dtype == BF16
+    assert ko.cpu().view(torch.int16).numpy().tobytes() == \
+        R.materialize(ek, tables[3].tolist(), n, bs).tobytes()
+    assert vo.cpu().view(torch.int16).numpy().tobytes() == \
+        R.materialize(ev, tables[3].tolist(), n, bs).tobytes()
+    with pytest.raises(ValueError, match="wrong KV dtype"):
+        ops.write_kv_decode(kn.half().to(DEV), vn.half().to(DEV), kd, vd, tables.to(DEV),
+                            ctx.to(DEV))
