@@ -757,7 +757,7 @@ struct Ranges {
   }
 };
 
-// The split every workgroup of the two launches derives from the sizes: the
+// The split every workgroup (and the step's plan) derives from the sizes: the
 // ranges (T key blocks in all, nwg workgroups, a multiple of 8 from 8 on) and
 // this lane's sequence of the first 64 (kept for stream_locate).
 struct StreamPlan {
