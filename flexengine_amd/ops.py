@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import contextlib
 from dataclasses import dataclass
+import functools
 import math
 
 import torch
@@ -35,7 +36,21 @@ def _require_gpu(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+@functools.lru_cache(maxsize=4096)
+def _pure_size(name: str, *args: int) -> int:
+    """A workspace size that depends on its integer arguments only (memoised: a
+    ctypes round trip per launch is host time the eager step pays)."""
+    return int(getattr(_lib.load(), name)(*args))
+
+
 def _stream(dev: torch.device) -> int:
+    """The current HIP stream of `dev` (the raw handle: torch.cuda.current_stream
+    builds a Stream object per call, ~4 us of host time on every launch)."""
+    if _RAW_STREAM is not None and dev.index is not None:
+        return _RAW_STREAM(dev.index)
     return torch.cuda.current_stream(dev).cuda_stream
 
 
@@ -532,6 +547,13 @@ ROWS64_MAX_ROWS = 64
 # 25.6 us).  For wide outputs (q/k/v, o, gate/up, LM head) the library GEMM measured
 # 10-45% faster at 64 rows.
 ROWS64_MIN_DEPTH = 4
+# Outside graph capture a 64-row step is bound by the host's launch rate: a library
+# GEMM call costs ~20 us of host time against ~4 us for the HIP kernel, which then
+# wins on every projection although its kernel is up to ~30% slower on wide outputs;
+# inside a captured graph the launches are paid once and the kernel time decides.
+# Outputs wider than this (the LM head: the step's last launch, whose kernel time the
+# host waits out) stay on the library GEMM.
+ROWS64_EAGER_MAX_N = 32768
 
 
 def gemm_rows64(x: torch.Tensor, weight: torch.Tensor,
@@ -549,7 +571,7 @@ def gemm_rows64(x: torch.Tensor, weight: torch.Tensor,
     m, k = x.shape
     n = weight.shape[0]
     out = torch.empty((m, n), dtype=FP16, device=dev)
-    need = int(_lib.load().fe_gemm_rows64_workspace_size(m, n, k))
+    need = _pure_size("fe_gemm_rows64_workspace_size", m, n, k)
     ws = decode_workspace(dev, need, kind="rows64")
     _lib.call("fe_gemm_rows64", x.data_ptr(), m, k, weight.data_ptr(), n, _ptr(bias),
               out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
@@ -559,12 +581,14 @@ def gemm_rows64(x: torch.Tensor, weight: torch.Tensor,
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
     """x @ weight^T (+ bias): the skinny HIP GEMM's fp32 partials (bias left to the
     consumer) for at most SKINNY_MAX_ROWS rows, fe_gemm_rows64 in fp16 (bias added)
-    up to ROWS64_MAX_ROWS rows when K >= ROWS64_MIN_DEPTH * N, the library GEMM in
-    fp16 otherwise."""
+    up to ROWS64_MAX_ROWS rows when K >= ROWS64_MIN_DEPTH * N or, outside graph
+    capture, N <= ROWS64_EAGER_MAX_N; the library GEMM in fp16 otherwise."""
     if x.shape[0] <= SKINNY_MAX_ROWS and x.shape[1] % 32 == 0:
         return gemm_skinny(x.contiguous(), weight)
-    if (x.shape[0] <= ROWS64_MAX_ROWS and x.shape[1] % 32 == 0
-            and x.shape[1] >= ROWS64_MIN_DEPTH * weight.shape[0]):
+    if x.shape[0] <= ROWS64_MAX_ROWS and x.shape[1] % 32 == 0 and (
+            x.shape[1] >= ROWS64_MIN_DEPTH * weight.shape[0]
+            or (weight.shape[0] <= ROWS64_EAGER_MAX_N
+                and not torch.cuda.is_current_stream_capturing())):
         return gemm_rows64(x, weight, bias)
     return torch.nn.functional.linear(x, weight, bias)
 
@@ -647,7 +671,7 @@ def _operand(x, weight: torch.Tensor):
 def _fused_ws(dev: torch.device, m: int, n: int, k: int) -> torch.Tensor:
     """The per-device workspace of the fused projections (split-K tickets + partial
     tiles), grown when a larger shape needs more; zero-filled when created."""
-    need = int(_lib.load().fe_gemm_fused_workspace_size(m, n, k))
+    need = _pure_size("fe_gemm_fused_workspace_size", m, n, k)
     return decode_workspace(dev, need, kind="gemm")
 
 
