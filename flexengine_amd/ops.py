@@ -585,12 +585,26 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     capture, N <= ROWS64_EAGER_MAX_N; the library GEMM in fp16 otherwise."""
     if x.shape[0] <= SKINNY_MAX_ROWS and x.shape[1] % 32 == 0:
         return gemm_skinny(x.contiguous(), weight)
-    if x.shape[0] <= ROWS64_MAX_ROWS and x.shape[1] % 32 == 0 and (
-            x.shape[1] >= ROWS64_MIN_DEPTH * weight.shape[0]
-            or (weight.shape[0] <= ROWS64_EAGER_MAX_N
-                and not torch.cuda.is_current_stream_capturing())):
-        return gemm_rows64(x, weight, bias)
+    if x.shape[0] <= ROWS64_MAX_ROWS and x.shape[1] % 32 == 0:
+        if x.shape[1] >= ROWS64_MIN_DEPTH * weight.shape[0]:
+            return gemm_rows64(x, weight, bias)
+        if weight.shape[0] <= ROWS64_EAGER_MAX_N and not torch.cuda.is_current_stream_capturing():
+            _warm_library_gemm(x, weight)
+            return gemm_rows64(x, weight, bias)
     return torch.nn.functional.linear(x, weight, bias)
+
+
+_LIBRARY_GEMM_WARM: set = set()
+
+
+def _warm_library_gemm(x: torch.Tensor, weight: torch.Tensor) -> None:
+    """One eager library GEMM per device and dtype before the eager path stops using
+    it: a graph captured later takes the library GEMM for these shapes, and its
+    first use must not fall inside the capture (the library sets itself up then)."""
+    key = (x.device, x.dtype)
+    if key not in _LIBRARY_GEMM_WARM:
+        torch.nn.functional.linear(x[:1], weight[:16])
+        _LIBRARY_GEMM_WARM.add(key)
 
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
