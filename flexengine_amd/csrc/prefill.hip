@@ -161,10 +161,6 @@ __device__ __forceinline__ bool locate_rows(const PrefillArgs& a, int item, RowB
   return false;
 }
 
-__device__ __forceinline__ f32x4 mfma32(f16x8 a, f16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
 // Cascade mode: the decode row b shares group s's prefix when its context
 // reaches past it; its own decode then starts at the prefix end.  Written by
 // the first workgroup for every decode row (0 = no shared prefix).
@@ -184,7 +180,7 @@ __device__ void write_suffix_starts(const PrefillArgs& a) {
   }
 }
 
-template <int D, int RT, bool CASCADE>
+template <int D, int RT, bool CASCADE, class E = Fp16>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void prefill_kernel(const PrefillArgs a) {
   using P = PCfg<D, RT>;
@@ -342,7 +338,7 @@ void prefill_kernel(const PrefillArgs a) {
         const f16x8 kv =
             *reinterpret_cast<const f16x8*>(kbase + (16 * kt + n) * P::KP + (32 * c + 8 * g) * 2);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) st[rt][kt] = mfma32(kv, qv[rt][c], st[rt][kt]);
+        for (int rt = 0; rt < RT; ++rt) st[rt][kt] = mma32<E>(kv, qv[rt][c], st[rt][kt]);
       }
     }
 
@@ -391,8 +387,14 @@ void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float e = exp2_fast(__builtin_fmaf(sv[2 * ps + kt][i], a.scale_log2, neg_m));
-            lsum += e;
-            p[4 * kt + i] = (f16)e;
+            const f16 pe = to16<E>(e);
+            p[4 * kt + i] = pe;
+            // bf16: the row sum takes the rounded weights that multiply V (the
+            // fp16 rounding error is small enough to sum e itself)
+            if constexpr (__is_same(E, Bf16))
+              lsum += (float)__builtin_bit_cast(__bf16, pe);
+            else
+              lsum += e;
           }
         pb[rt][ps] = p;
       }
@@ -412,7 +414,7 @@ void prefill_kernel(const PrefillArgs a) {
         const f16x4 l4 = __builtin_bit_cast(f16x4, lo), h4 = __builtin_bit_cast(f16x4, hi);
         const f16x8 va = {l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) o[rt][x] = mfma32(va, pb[rt][ps], o[rt][x]);
+        for (int rt = 0; rt < RT; ++rt) o[rt][x] = mma32<E>(va, pb[rt][ps], o[rt][x]);
       }
     }
 
@@ -447,9 +449,7 @@ void prefill_kernel(const PrefillArgs a) {
       f16* orow = a.out + orow_idx * D + 4 * g;
 #pragma unroll
       for (int x = 0; x < P::NX; ++x)
-        *reinterpret_cast<f16x4*>(orow + 16 * x) =
-            f16x4{(f16)(o[rt][x][0] * inv), (f16)(o[rt][x][1] * inv),
-                  (f16)(o[rt][x][2] * inv), (f16)(o[rt][x][3] * inv)};
+        *reinterpret_cast<f16x4*>(orow + 16 * x) = to16x4<E>(o[rt][x] * inv);
     } else {
       // device-coherent stores through one wave-uniform descriptor per array
       // (the host keeps the partial arrays under 2 GiB)
@@ -514,9 +514,7 @@ void prefill_kernel(const PrefillArgs a) {
       *reinterpret_cast<f32x4*>(a.pre_o + orow_idx * D + d4) = num * inv;
       if (d4 == 0) a.pre_lse[orow_idx] = den > 0.f ? M + log2f(den) : kNegInf;
     } else {
-      *reinterpret_cast<f16x4*>(a.out + orow_idx * D + d4) =
-          f16x4{(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
-                (f16)(num[3] * inv)};
+      *reinterpret_cast<f16x4*>(a.out + orow_idx * D + d4) = to16x4<E>(num * inv);
     }
   }
 }
@@ -1470,10 +1468,10 @@ inline int log2_exact(int x) {
   return l;
 }
 
-template <int D, int RT, bool CASCADE = false>
+template <int D, int RT, bool CASCADE = false, class E = Fp16>
 void launch_prefill(const PrefillArgs& a, int blocks, hipStream_t stream) {
   using P = PCfg<D, RT>;
-  hipLaunchKernelGGL((prefill_kernel<D, RT, CASCADE>), dim3(blocks * a.Hkv * a.KS),
+  hipLaunchKernelGGL((prefill_kernel<D, RT, CASCADE, E>), dim3(blocks * a.Hkv * a.KS),
                      dim3(kThreads), 2 * P::STAGE, stream, a);
 }
 
@@ -1654,11 +1652,18 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   a.tok0 = nullptr;
   a.plan = (const int*)step_plan;
   hipStream_t s = (hipStream_t)stream;
-  if (bf16 && !dma) return FE_ERR_UNSUPPORTED;  // bf16: the stream-K kernel only
   if (dma && bf16) {
     if (head_dim == 64) launch_prefill_dma<64, Bf16>(a, s); else launch_prefill_dma<128, Bf16>(a, s);
   } else if (dma) {
     if (head_dim == 64) launch_prefill_dma<64, Fp16>(a, s); else launch_prefill_dma<128, Fp16>(a, s);
+  } else if (bf16) {
+    if (head_dim == 64) {
+      if (p.rt == 2) launch_prefill<64, 2, false, Bf16>(a, p.blocks, s);
+      else launch_prefill<64, 1, false, Bf16>(a, p.blocks, s);
+    } else {
+      if (p.rt == 2) launch_prefill<128, 2, false, Bf16>(a, p.blocks, s);
+      else launch_prefill<128, 1, false, Bf16>(a, p.blocks, s);
+    }
   } else if (head_dim == 64) {
     if (p.rt == 2) launch_prefill<64, 2>(a, p.blocks, s); else launch_prefill<64, 1>(a, p.blocks, s);
   } else {

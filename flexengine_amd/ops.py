@@ -461,8 +461,7 @@ def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                   plan: PrefillPlan | None = None) -> torch.Tensor:
     """Ragged causal prefill: q [total_q, Hq, D]; sequence s owns rows
     q_offsets[s]:q_offsets[s+1] at positions context_lens[s]-n_s .. context_lens[s]-1.
-    fp16 or bf16 (q, out and the pools alike; bf16 needs block sizes that are
-    multiples of 16).  With `plan` (prefill_paged_plan on these q_offsets /
+    fp16 or bf16 (q, out and the pools alike).  With `plan` (prefill_paged_plan on these q_offsets /
     context_lens and sizes) the launch reads its work split from it
     (fe_prefill_paged_planned); same results."""
     dev = _require_gpu(q, k_pool, v_pool, block_tables, q_offsets, context_lens, out)

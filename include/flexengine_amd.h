@@ -354,10 +354,10 @@ int fe_prefill_paged(const void* q, void* out,
                      void* workspace, size_t workspace_bytes, fe_stream_t stream);
 
 /*
- * bf16 form of fe_prefill_paged: the same arguments and results with q, out
- * and the pools in bfloat16 (v_mfma_f32_16x16x32_bf16, probabilities rounded
- * to bf16 for the PV product, fp32 accumulation).  Block sizes must be
- * multiples of 16 (FE_ERR_UNSUPPORTED otherwise); the workspace is
+ * bf16 form of fe_prefill_paged: the same arguments, block sizes and results
+ * with q, out and the pools in bfloat16 (v_mfma_f32_16x16x32_bf16,
+ * probabilities rounded to bf16 for the PV product, fp32 accumulation and row
+ * sums of the rounded probabilities); the workspace is
  * fe_prefill_workspace_size's.  Replaces the same per-request route for the
  * bfloat16 models the reference builds (qwen2.py:54).
  */

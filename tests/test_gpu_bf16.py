@@ -217,13 +217,21 @@ def test_bf16_per_request_interface():
     assert torch.equal(k_back.cpu(), keys)
 
 
+@pytest.mark.parametrize("hq,hkv,d,bs,n_new,cached", [
+    (8, 8, 64, 4, [20], [7]),               # the tile kernel, one row tile per wave
+    (14, 2, 64, 1, [37, 5], [0, 300]),       # block size 1
+    (12, 2, 128, 8, [3], [900]),             # few row blocks: key splits merged by ticket
+    (12, 2, 128, 8, [150, 90], [60, 500]),   # many rows: two row tiles per wave
+])
+def test_bf16_prefill_small_blocks(hq, hkv, d, bs, n_new, cached):
+    """Block sizes below 16 run the tile kernel (prefill_kernel) in its bf16 form."""
+    case = _prefill_case(hq * bs + d + sum(n_new), n_new, cached, hq, hkv, d, bs)
+    print(f"bf16 prefill bs={bs} {hq}/{hkv}/{d} n={n_new} c={cached}", flush=True)
+    close_bf16(_prefill(*case), _prefill_oracle(*case, bs), f"bf16 prefill bs={bs} n={n_new}")
+
+
 def test_bf16_unsupported_forms_are_refused():
-    """bf16 prefill needs block sizes that are multiples of 16; the shared-prefix decode
-    and mixed dtypes are refused before any launch."""
-    case = _prefill_case(5, [20], [7], 8, 8, 64, bs=4)
-    with pytest.raises(_lib.FlexEngineAMDError) as e:
-        _prefill(*case)
-    assert e.value.code == _lib.FE_ERR_UNSUPPORTED
+    """The shared-prefix decode and mixed dtypes are refused before any launch."""
     w = to_bf16(workloads.c1_workload()).to(DEV)
     b = w.q.shape[0]
     with pytest.raises(ValueError, match="float16 pools"):
