@@ -354,6 +354,7 @@ struct CascadePrefix {
   float* pre_lse;    // [batch * hq]
   int32_t* tok0;     // [batch]
   void* scratch;     // key-split partials, cascade_prefix_scratch_bytes
+  bool bf16;         // q and the pools are bfloat16 (fp16 otherwise)
 };
 __attribute__((visibility("hidden"))) size_t cascade_prefix_scratch_bytes(int num_groups,
                                                                           int batch, int hq,

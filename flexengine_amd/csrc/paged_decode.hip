@@ -518,7 +518,7 @@ struct BLds {
   }
 };
 
-template <int D>
+template <int D, class E = Fp16>
 __global__ __launch_bounds__(kBThreads) void balanced_decode_kernel(const DecodeArgs a) {
   using C = TileCfg<D>;
   using Lds = BLds<D>;
@@ -864,8 +864,7 @@ __global__ __launch_bounds__(kBThreads) void balanced_decode_kernel(const Decode
             acc = (w1 * acc + w2 * op) * (1.f / (w1 + w2));
           }
         }
-        *reinterpret_cast<f16x4*>(a.out + r * D + d0) =
-            f16x4{(f16)acc[0], (f16)acc[1], (f16)acc[2], (f16)acc[3]};
+        *reinterpret_cast<f16x4*>(a.out + r * D + d0) = to16x4<E>(acc);
       } else {
         const int slot = 2 * wg + (sg == s_first ? 0 : 1);
         const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
@@ -904,8 +903,8 @@ __global__ __launch_bounds__(kBThreads) void balanced_decode_kernel(const Decode
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < C::NK; ++s) {
-      sacc = mfma16(lo4(kk[s]), lo4(qv[s]), sacc);
-      sacc = mfma16(hi4(kk[s]), hi4(qv[s]), sacc);
+      sacc = mma16<E>(lo4(kk[s]), lo4(qv[s]), sacc);
+      sacc = mma16<E>(hi4(kk[s]), hi4(qv[s]), sacc);
     }
     compiler_fence();
     {
@@ -917,7 +916,7 @@ __global__ __launch_bounds__(kBThreads) void balanced_decode_kernel(const Decode
       }
     }
     compiler_fence();
-    softmax_pv_tile<D>(sacc, 0, tile_rows(k), a.scale_log2, stage, m_run, l_run, o);
+    softmax_pv_tile<D, E>(sacc, 0, tile_rows(k), a.scale_log2, stage, m_run, l_run, o);
     compiler_fence();
     const int nr = tile_newrow(k);
     if (nr >= 0) {  // write the decoded token's row to the pool
@@ -1062,9 +1061,7 @@ __global__ __launch_bounds__(kBThreads) void balanced_decode_kernel(const Decode
       }
     }
     const float inv = 1.f / den;
-    *reinterpret_cast<f16x4*>(a.out + r * D + e4 * 4) =
-        f16x4{(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
-              (f16)(num[3] * inv)};
+    *reinterpret_cast<f16x4*>(a.out + r * D + e4 * 4) = to16x4<E>(num * inv);
   }
 }
 
@@ -1200,15 +1197,9 @@ BalancedPlan plan_balanced(int batch, int hkv, int G, int block_size, int max_le
 template <int D, class E>
 int launch_decode(const DecodeArgs& a, hipStream_t stream) {
   if (a.nwg > 0) {
-    // the balanced kernel (shared-prefix suffixes) is fp16 only; decode_impl
-    // refuses bf16 shared-prefix calls before any launch
-    if constexpr (__is_same(E, Fp16)) {
-      hipLaunchKernelGGL((balanced_decode_kernel<D>), dim3(a.nwg), dim3(kBThreads),
-                         BLds<D>::bytes(a.B, a.G, a.states), stream, a);
-      return FE_LAUNCH_STATUS();
-    } else {
-      return FE_ERR_UNSUPPORTED;
-    }
+    hipLaunchKernelGGL((balanced_decode_kernel<D, E>), dim3(a.nwg), dim3(kBThreads),
+                       BLds<D>::bytes(a.B, a.G, a.states), stream, a);
+    return FE_LAUNCH_STATUS();
   }
   const dim3 grid((a.target + 2 * a.B) * a.Hkv);
   if (a.plan != nullptr)
@@ -1259,7 +1250,6 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
   // the shared-prefix split needs 16-token-aligned suffixes (block-size-16k path)
   if (cascade && block_size % kTile != 0) return FE_ERR_UNSUPPORTED;
-  if (cascade && bf16) return FE_ERR_UNSUPPORTED;  // shared-prefix decode: fp16 only
   if (batch == 0) return FE_OK;
   FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && context_lens);
   FE_CHECK_ARG((k_new == nullptr) == (v_new == nullptr));
@@ -1356,6 +1346,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     c.bs = block_size;
     c.scale = scale;
     c.tickets = a.tickets;  // each launch leaves the tickets it used at zero
+    c.bf16 = bf16;
     c.tok0 = (int32_t*)cw;
     cw += align256((size_t)batch * sizeof(int32_t));
     c.pre_o = (float*)cw;
@@ -1488,19 +1479,22 @@ extern "C" size_t fe_paged_decode_shared_prefix_workspace_size(int batch, int nu
          cascade_prefix_scratch_bytes(num_groups, batch, num_q_heads, kv_heads, head_dim);
 }
 
-extern "C" int fe_paged_decode_shared_prefix(
-    const void* q, int64_t q_batch_stride, void* out, const void* k_new, const void* v_new,
-    int64_t new_batch_stride, void* k_pool, void* v_pool, int num_blocks,
-    const int32_t* block_tables, int table_stride, const int32_t* context_lens,
-    const int32_t* group_offsets, const int32_t* group_prefix_lens, int num_groups,
-    void* workspace, size_t workspace_bytes, int batch, int num_q_heads, int kv_heads,
-    int head_dim, int block_size, float scale, int target_splits, fe_stream_t stream) {
+namespace {
+
+int shared_prefix_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_new,
+                       const void* v_new, int64_t new_batch_stride, void* k_pool, void* v_pool,
+                       int num_blocks, const int32_t* block_tables, int table_stride,
+                       const int32_t* context_lens, const int32_t* group_offsets,
+                       const int32_t* group_prefix_lens, int num_groups, void* workspace,
+                       size_t workspace_bytes, int batch, int num_q_heads, int kv_heads,
+                       int head_dim, int block_size, float scale, int target_splits,
+                       fe_stream_t stream, bool bf16) {
   FE_CHECK_ARG(num_groups >= 0 && num_groups <= batch + 1);
   if (num_groups == 0 || batch == 0)
     return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
                        num_blocks, block_tables, table_stride, context_lens, workspace,
                        workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
-                       target_splits, nullptr, (hipStream_t)stream);
+                       target_splits, nullptr, (hipStream_t)stream, nullptr, 0, bf16);
   FE_CHECK_ARG(group_offsets && group_prefix_lens);
   CascadePrefix c{};
   c.group_offsets = group_offsets;
@@ -1509,7 +1503,37 @@ extern "C" int fe_paged_decode_shared_prefix(
   return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
                      num_blocks, block_tables, table_stride, context_lens, workspace,
                      workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
-                     target_splits, &c, (hipStream_t)stream);
+                     target_splits, &c, (hipStream_t)stream, nullptr, 0, bf16);
+}
+
+}  // namespace
+
+extern "C" int fe_paged_decode_shared_prefix(
+    const void* q, int64_t q_batch_stride, void* out, const void* k_new, const void* v_new,
+    int64_t new_batch_stride, void* k_pool, void* v_pool, int num_blocks,
+    const int32_t* block_tables, int table_stride, const int32_t* context_lens,
+    const int32_t* group_offsets, const int32_t* group_prefix_lens, int num_groups,
+    void* workspace, size_t workspace_bytes, int batch, int num_q_heads, int kv_heads,
+    int head_dim, int block_size, float scale, int target_splits, fe_stream_t stream) {
+  return shared_prefix_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool,
+                            v_pool, num_blocks, block_tables, table_stride, context_lens,
+                            group_offsets, group_prefix_lens, num_groups, workspace,
+                            workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size,
+                            scale, target_splits, stream, false);
+}
+
+extern "C" int fe_paged_decode_shared_prefix_bf16(
+    const void* q, int64_t q_batch_stride, void* out, const void* k_new, const void* v_new,
+    int64_t new_batch_stride, void* k_pool, void* v_pool, int num_blocks,
+    const int32_t* block_tables, int table_stride, const int32_t* context_lens,
+    const int32_t* group_offsets, const int32_t* group_prefix_lens, int num_groups,
+    void* workspace, size_t workspace_bytes, int batch, int num_q_heads, int kv_heads,
+    int head_dim, int block_size, float scale, int target_splits, fe_stream_t stream) {
+  return shared_prefix_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool,
+                            v_pool, num_blocks, block_tables, table_stride, context_lens,
+                            group_offsets, group_prefix_lens, num_groups, workspace,
+                            workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size,
+                            scale, target_splits, stream, true);
 }
 
 // ---------------------------------------------------------------------------

@@ -1810,7 +1810,15 @@ int cascade_prefix_launch(const CascadePrefix& c, hipStream_t stream) {
   a.pre_o = c.pre_o;
   a.pre_lse = c.pre_lse;
   a.tok0 = c.tok0;
-  if (c.d == 64) {
+  if (c.bf16) {
+    if (c.d == 64) {
+      if (p.rt == 2) launch_prefill<64, 2, true, Bf16>(a, p.blocks, stream);
+      else launch_prefill<64, 1, true, Bf16>(a, p.blocks, stream);
+    } else {
+      if (p.rt == 2) launch_prefill<128, 2, true, Bf16>(a, p.blocks, stream);
+      else launch_prefill<128, 1, true, Bf16>(a, p.blocks, stream);
+    }
+  } else if (c.d == 64) {
     if (p.rt == 2) launch_prefill<64, 2, true>(a, p.blocks, stream);
     else launch_prefill<64, 1, true>(a, p.blocks, stream);
   } else {

@@ -317,6 +317,25 @@ int fe_paged_decode_shared_prefix(const void* q, int64_t q_batch_stride, void* o
                                   fe_stream_t stream);
 
 /*
+ * bf16 form of fe_paged_decode_shared_prefix: the same arguments, workspace
+ * and results with q, out, the pools and the new rows in bfloat16 (the
+ * prefix pass and the suffix decode on the bf16 matrix-core products,
+ * probabilities rounded to bf16, fp32 merge).  Replaces the same route for the
+ * bfloat16 models the reference builds (qwen2.py:54).
+ */
+int fe_paged_decode_shared_prefix_bf16(const void* q, int64_t q_batch_stride, void* out,
+                                       const void* k_new, const void* v_new,
+                                       int64_t new_batch_stride, void* k_pool, void* v_pool,
+                                       int num_blocks, const int32_t* block_tables,
+                                       int table_stride, const int32_t* context_lens,
+                                       const int32_t* group_offsets,
+                                       const int32_t* group_prefix_lens, int num_groups,
+                                       void* workspace, size_t workspace_bytes,
+                                       int batch, int num_q_heads, int kv_heads, int head_dim,
+                                       int block_size, float scale, int target_splits,
+                                       fe_stream_t stream);
+
+/*
  * Log-sum-exp merge of split attention results:
  *   LSE[r]   = log(sum_s exp(part_lse[s, r]))
  *   out[r,:] = sum_s exp(part_lse[s, r] - LSE[r]) * part_out[s, r, :]

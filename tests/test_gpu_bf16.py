@@ -230,14 +230,64 @@ def test_bf16_prefill_small_blocks(hq, hkv, d, bs, n_new, cached):
     close_bf16(_prefill(*case), _prefill_oracle(*case, bs), f"bf16 prefill bs={bs} n={n_new}")
 
 
+# --------------------------------------------------------------------------------------
+# shared-prefix (cascade) decode
+# --------------------------------------------------------------------------------------
+
+def _shared_prefix(w: workloads.DecodeWorkload, fuse: bool):
+    d = w.to(DEV)
+    out = ops.paged_decode_shared_prefix(
+        d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens,
+        d.meta["group_offsets"].to(DEV), d.meta["prefix_lens"].to(DEV),
+        k_new=d.k_new if fuse else None, v_new=d.v_new if fuse else None)
+    torch.cuda.synchronize()
+    return out, d
+
+
+def test_bf16_shared_prefix_c3_shape():
+    """C3's shape at 2 groups x 8 (the piece kernel runs the suffixes below 128 rows)."""
+    w = to_bf16(workloads.c3_workload(groups=2, per_group=8))
+    got, _ = _shared_prefix(w, fuse=False)
+    exp, _, _ = oracle_decode(w)
+    close_bf16(got, exp, "bf16 cascade C3 (2x8)")
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", [(12, 2, 128, 16), (14, 2, 64, 32)])
+def test_bf16_shared_prefix_edge_groups(hq, hkv, d, bs):
+    """Groups of 3 (prefix of 40 tokens: whole blocks only), 1 and 0 members and one of
+    5 whose members end at the prefix, inside it and inactive; rows outside every group.
+    No decode-step write: a member ending at the prefix would write its token into a
+    shared block, which the caller must not ask for (the reference refuses it)."""
+    groups = [(3, 40), (1, 64), (0, 32), (5, 512)]
+    w = to_bf16(workloads.shared_prefix_workload(21, groups, singles=3, hq=hq, hkv=hkv, d=d,
+                                                 block_size=bs,
+                                                 member_lens={5: 512, 6: 505, 7: 0}))
+    print(f"bf16 cascade edges {hq}/{hkv}/{d}/{bs}", flush=True)
+    got, _ = _shared_prefix(w, fuse=False)
+    exp, _, _ = oracle_decode(w)
+    close_bf16(got, exp, f"bf16 cascade edges {hq}/{hkv}/{d}/{bs}")
+    assert not got[7].any(), "inactive member must give exact zeros"
+
+
+def test_bf16_balanced_cascade_with_page_write():
+    """160 rows: the suffixes run on the balanced kernel in its bf16 form."""
+    groups = [(48, 256), (32, 64), (24, 1000), (1, 512)]
+    lens = {50: 0, 105: 1, 106: 16, 107: 17, 108: 3000}
+    w = to_bf16(workloads.shared_prefix_workload(77, groups, singles=55, hq=12, hkv=2, d=128,
+                                                 block_size=16, tail=(1, 700), member_lens=lens,
+                                                 with_new_kv=True))
+    assert w.batch == 160
+    got, dv = _shared_prefix(w, fuse=True)
+    exp, kp, vp = oracle_decode(w)
+    assert torch.count_nonzero(got[50]) == 0
+    close_bf16(got, exp, "bf16 balanced cascade")
+    assert dv.k_pool.cpu().view(torch.int16).numpy().tobytes() == kp.tobytes()
+    assert dv.v_pool.cpu().view(torch.int16).numpy().tobytes() == vp.tobytes()
+
+
 def test_bf16_unsupported_forms_are_refused():
-    """The shared-prefix decode and mixed dtypes are refused before any launch."""
+    """Mixed dtypes are refused before any launch."""
     w = to_bf16(workloads.c1_workload()).to(DEV)
-    b = w.q.shape[0]
-    with pytest.raises(ValueError, match="float16 pools"):
-        ops.paged_decode_shared_prefix(w.q, w.k_pool, w.v_pool, w.block_tables, w.context_lens,
-                                       torch.tensor([0, b], dtype=torch.int32, device=DEV),
-                                       torch.tensor([16], dtype=torch.int32, device=DEV))
     with pytest.raises(ValueError, match="pools' dtype"):
         ops.paged_decode(w.q.half(), w.k_pool, w.v_pool, w.block_tables, w.context_lens)
     with pytest.raises(ValueError, match="same"):
