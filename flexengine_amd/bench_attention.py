@@ -17,8 +17,7 @@ stream -- and prints one JSON line per config:
   the 48 decode rows in GB/s, and the whole step.
 
 Calls are replayed from a HIP graph, so each figure is GPU time per call.
-`--dtype bf16` runs the bf16 entry points on the same values rounded to bf16
-(C3's shared-prefix decode has no bf16 form and is skipped then).
+`--dtype bf16` runs the bf16 entry points on the same values rounded to bf16.
 """
 from __future__ import annotations
 
@@ -198,9 +197,9 @@ def main(argv=None) -> int:
         unique = w.unique_tokens * 2 * hkv * d * 2 + 2 * w.q.numel() * 2
         print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique, dtype=dt)
                          | {"dtype": args.dtype}), flush=True)
-        if dt == torch.float16:
-            print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique,
-                                          shared_prefix=True) | {"dtype": args.dtype}), flush=True)
+        print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique,
+                                      shared_prefix=True, dtype=dt) | {"dtype": args.dtype}),
+              flush=True)
     if "c4" in cfgs:
         print(json.dumps(bench_c4(args.iters, args.copies, dt) | {"dtype": args.dtype}),
               flush=True)
