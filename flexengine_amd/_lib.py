@@ -54,6 +54,7 @@ SIGNATURES: dict[str, tuple] = {
                                                 _p, _p, _p, _i, _p, _sz, _i, _i, _i, _i, _i, _f,
                                                 _i, _p]),
     "fe_lse_merge": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),
+    "fe_lse_merge_bf16": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),
     "fe_prefill_paged": (_i, [_p, _p, _p, _p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _i,
                               _f, _p, _sz, _p]),
     "fe_prefill_workspace_size": (_sz, [_i, _i, _i, _i, _i]),

@@ -1066,6 +1066,7 @@ __global__ __launch_bounds__(kBThreads) void balanced_decode_kernel(const Decode
 }
 
 // General LSE merge of S partial results (natural-log LSE at the boundary).
+template <class E>
 __global__ __launch_bounds__(kThreads) void lse_merge_kernel(const float* __restrict__ po,
                                                              const float* __restrict__ plse,
                                                              int S, int R, int D, f16* out,
@@ -1084,7 +1085,7 @@ __global__ __launch_bounds__(kThreads) void lse_merge_kernel(const float* __rest
     float num = 0.f;
     for (int s = 0; s < S; ++s)
       num += exp2f(plse[(int64_t)s * R + r] * kLog2e - M) * po[((int64_t)s * R + r) * D + d];
-    out[(int64_t)r * D + d] = (f16)(num / den);
+    out[(int64_t)r * D + d] = to16<E>(num / den);
   }
   if (out_lse && threadIdx.x == 0) out_lse[r] = (M + log2f(den)) / kLog2e;
 }
@@ -1623,14 +1624,32 @@ extern "C" int fe_paged_decode_noalloc(const void* q, int64_t q_batch_stride, vo
                      (hipStream_t)stream);
 }
 
-extern "C" int fe_lse_merge(const float* part_out, const float* part_lse, int num_splits,
-                            int rows, int head_dim, void* out, float* out_lse,
-                            fe_stream_t stream) {
+namespace {
+
+template <class E>
+int lse_merge_impl(const float* part_out, const float* part_lse, int num_splits, int rows,
+                   int head_dim, void* out, float* out_lse, fe_stream_t stream) {
   FE_CHECK_ARG(num_splits > 0 && rows >= 0 && head_dim > 0);
   if (rows == 0) return FE_OK;
   FE_CHECK_ARG(part_out && part_lse && out);
   const int threads = head_dim >= 256 ? 256 : (head_dim >= 128 ? 128 : 64);
-  hipLaunchKernelGGL(lse_merge_kernel, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(lse_merge_kernel<E>, dim3(rows), dim3(threads), 0, (hipStream_t)stream,
                      part_out, part_lse, num_splits, rows, head_dim, (f16*)out, out_lse);
   return FE_LAUNCH_STATUS();
+}
+
+}  // namespace
+
+extern "C" int fe_lse_merge(const float* part_out, const float* part_lse, int num_splits,
+                            int rows, int head_dim, void* out, float* out_lse,
+                            fe_stream_t stream) {
+  return lse_merge_impl<Fp16>(part_out, part_lse, num_splits, rows, head_dim, out, out_lse,
+                              stream);
+}
+
+extern "C" int fe_lse_merge_bf16(const float* part_out, const float* part_lse, int num_splits,
+                                 int rows, int head_dim, void* out, float* out_lse,
+                                 fe_stream_t stream) {
+  return lse_merge_impl<Bf16>(part_out, part_lse, num_splits, rows, head_dim, out, out_lse,
+                              stream);
 }

@@ -393,9 +393,12 @@ def paged_decode_shared_prefix(q: torch.Tensor, k_pool: torch.Tensor, v_pool: to
     return out
 
 
-def lse_merge(part_out: torch.Tensor, part_lse: torch.Tensor,
-              with_lse: bool = False) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
-    """Merges S split results: part_out fp32 [S, R, D], part_lse fp32 [S, R] (natural log)."""
+def lse_merge(part_out: torch.Tensor, part_lse: torch.Tensor, with_lse: bool = False,
+              dtype: torch.dtype = FP16) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+    """Merges S split results: part_out fp32 [S, R, D], part_lse fp32 [S, R] (natural log);
+    the output [R, D] in `dtype` (float16: fe_lse_merge, bfloat16: fe_lse_merge_bf16)."""
+    if dtype not in KV_DTYPES:
+        raise ValueError("the merged output is float16 or bfloat16")
     dev = _require_gpu(part_out, part_lse)
     if part_out.ndim != 3 or part_lse.shape != part_out.shape[:2]:
         raise ValueError("part_out must be [S, R, D] and part_lse [S, R]")
@@ -403,9 +406,10 @@ def lse_merge(part_out: torch.Tensor, part_lse: torch.Tensor,
         raise ValueError("partials must be float32")
     part_out, part_lse = part_out.contiguous(), part_lse.contiguous()
     s, r, d = part_out.shape
-    out = torch.empty((r, d), dtype=FP16, device=dev)
+    out = torch.empty((r, d), dtype=dtype, device=dev)
     out_lse = torch.empty((r,), dtype=torch.float32, device=dev) if with_lse else None
-    _lib.call("fe_lse_merge", part_out.data_ptr(), part_lse.data_ptr(), s, r, d, out.data_ptr(),
+    sfx = "_bf16" if dtype == BF16 else ""
+    _lib.call("fe_lse_merge" + sfx, part_out.data_ptr(), part_lse.data_ptr(), s, r, d, out.data_ptr(),
               _ptr(out_lse), _stream(dev))
     return (out, out_lse) if with_lse else out
 

@@ -352,6 +352,11 @@ int fe_lse_merge(const float* part_out, const float* part_lse, int num_splits,
                  int rows, int head_dim, void* out, float* out_lse,
                  fe_stream_t stream);
 
+/* bf16 form of fe_lse_merge: the same arguments, out bfloat16 [rows, head_dim]
+ * (rounded to nearest even) for the bfloat16 models of qwen2.py:54. */
+int fe_lse_merge_bf16(const float* part_out, const float* part_lse, int num_splits,
+                      int rows, int head_dim, void* out, float* out_lse, fe_stream_t stream);
+
 /*
  * Ragged chunked-prefill attention over paged KV (causal), fp16 MFMA:
  * sequence s owns query rows [q_offsets[s], q_offsets[s+1]) of q/out

@@ -108,6 +108,7 @@ def test_host_side_validation_rejects_before_launch(lib):
     # empty work is a successful no-op
     assert lib.fe_write_kv(null, null, 256, null, null, 4, null, null, 0, 2, 128, 16, null) == 0
     assert lib.fe_lse_merge(null, null, 1, 0, 128, null, null, null) == 0
+    assert lib.fe_lse_merge_bf16(null, null, 1, 0, 128, null, null, null) == 0
 
 
 def test_workspace_size_grows_with_batch_and_target(lib):

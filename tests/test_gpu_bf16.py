@@ -285,6 +285,22 @@ def test_bf16_balanced_cascade_with_page_write():
     assert dv.v_pool.cpu().view(torch.int16).numpy().tobytes() == vp.tobytes()
 
 
+def test_bf16_lse_merge():
+    """fe_lse_merge_bf16 on fp32 partials of a split attention (zero-length splits
+    included) against the oracle's merge, output rounded to bf16."""
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((6, 128))
+    k = rng.standard_normal((300, 128))
+    v = rng.standard_normal((300, 128))
+    po, pl = R.split_attention(q, k, v, [0, 50, 50, 170, 300])
+    out, lse = ops.lse_merge(torch.tensor(po, dtype=torch.float32, device=DEV),
+                             torch.tensor(pl, dtype=torch.float32, device=DEV), with_lse=True,
+                             dtype=BF16)
+    exp_o, exp_l = R.lse_merge(po, pl)
+    close_bf16(out, exp_o, "bf16 lse merge")
+    np.testing.assert_allclose(lse.cpu().numpy(), exp_l, atol=1e-4)
+
+
 def test_bf16_unsupported_forms_are_refused():
     """Mixed dtypes are refused before any launch."""
     w = to_bf16(workloads.c1_workload()).to(DEV)
