@@ -207,7 +207,11 @@ def hold_workspaces():
     try:
         yield held
     finally:
-        _HOLDERS.remove(held)
+        # by identity: list equality would compare the held tensors elementwise
+        for i in range(len(_HOLDERS) - 1, -1, -1):
+            if _HOLDERS[i] is held:
+                del _HOLDERS[i]
+                break
 
 
 def decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_context: int,

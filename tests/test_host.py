@@ -346,3 +346,25 @@ def test_replay_pads_with_zeros_and_a_zero_mask():
                      "positions": torch.zeros(1, 1, dtype=torch.long)})   # bucket 1 not captured
     with pytest.raises(ValueError):
         m.capture(3, decode, {"input_ids": torch.ones(3, 1)})             # not a bucket
+
+
+def test_nested_workspace_scopes_close_by_identity():
+    # the outer scope holds [A, B], the inner one [B, A]: closing the inner scope
+    # must neither compare A with B elementwise nor remove the outer scope
+    from flexengine_amd import ops
+    cpu = torch.device("cpu")
+    with ops.hold_workspaces() as outer:
+        a = ops.decode_workspace(cpu, 4 << 20, kind="test-nest-a")
+        b = ops.decode_workspace(cpu, 8 << 20, kind="test-nest-b")
+        with ops.hold_workspaces() as inner:
+            ops.decode_workspace(cpu, 8 << 20, kind="test-nest-b")
+            ops.decode_workspace(cpu, 4 << 20, kind="test-nest-a")
+            assert [t is x for t, x in zip(inner, (b, a))] == [True, True]
+        assert ops._HOLDERS[-1] is outer
+        assert not any(h is inner for h in ops._HOLDERS)
+        # a scope equal to the outer one element by element closes itself only
+        with ops.hold_workspaces() as same:
+            ops.decode_workspace(cpu, 4 << 20, kind="test-nest-a")
+            ops.decode_workspace(cpu, 8 << 20, kind="test-nest-b")
+        assert ops._HOLDERS[-1] is outer and same == outer
+    assert not any(h is outer for h in ops._HOLDERS)
