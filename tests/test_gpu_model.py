@@ -192,7 +192,8 @@ def c5():
     lengths = torch.randint(512, 4097, (C5_ROWS,), generator=gen).tolist()
     tokens = torch.randint(0, model.cfg.vocab_size, (C5_ROWS,), generator=gen).tolist()
     bs = 16
-    blocks = sum((n + C5_STEPS + bs) // bs + 1 for n in lengths) + 64
+    # spare blocks: the scratch requests of a bucket-8 and a bucket-64 graph step
+    blocks = sum((n + C5_STEPS + bs) // bs + 1 for n in lengths) + 64 + 64
     cache = PagedKVCache(CacheLayout(model.layers, blocks, bs, model.nkv, model.dim), device=DEV)
     g = torch.Generator(device=DEV)
     g.manual_seed(5)
@@ -326,9 +327,10 @@ def _near(got_rows, ref, what):
 
 def test_c5_eager_b64_and_bucket8_replays_against_fp32(c5):
     """Batch invariance at 64 rows: one eager decode_static step over all 64 rows
-    (library GEMMs + unfused layer kernels) and eight bucket-8 graph replays of the
-    same rows (fused projections), on the same cache state, each against a plain
-    PyTorch float32 decode step of the same model."""
+    (fe_gemm_rows64 for every projection but the LM head, unfused layer kernels)
+    and eight bucket-8 graph replays of the same rows (fused projections), on the
+    same cache state, each against a plain PyTorch float32 decode step of the same
+    model."""
     model, cache, step, st = c5
     chunks = [Chunk(f"r{b}", [st["tok"][b]], st["pos"][b]) for b in range(C5_ROWS)]
     eager = _eager(model, cache, step, chunks)
@@ -341,3 +343,25 @@ def test_c5_eager_b64_and_bucket8_replays_against_fp32(c5):
     _near(eager, ref, "C5 eager B=64 vs fp32")
     _near(rows, ref, "C5 8 x bucket 8 vs fp32")
     _near(rows, eager.float(), "C5 8 x bucket 8 vs eager B=64")
+
+
+def test_c5_b64_graph_replays_against_fp32_and_eager(c5):
+    """The 64-row step as bench.py's c5.b64_graph runs it: decode_static captured in
+    a 64-row bucket, where ops.linear routes differently than eagerly (inside a
+    capture only the deep down projection takes fe_gemm_rows64; q/k/v, o, gate/up
+    and the LM head take the library GEMM).  Two replays on the same cache state,
+    each against the float32 decode and the eager 64-row step."""
+    from flexengine_amd.graphs import DecodeGraphManager
+    model, cache, step8, st = c5
+    step = GraphDecodeStep(model, cache, max_model_len=4096 + C5_STEPS + 32,
+                           manager=DecodeGraphManager(DEV, buckets=(C5_ROWS,)))
+    chunks = [Chunk(f"r{b}", [st["tok"][b]], st["pos"][b]) for b in range(C5_ROWS)]
+    ref = _fp32_decode_reference(model, cache, chunks)
+    eager = _eager(model, cache, step, chunks)
+    for rep in range(2):
+        out = step(chunks)
+        assert out is not None, "the 64-row bucket fell back"
+        _near(out, ref, f"C5 64-row graph replay {rep} vs fp32")
+        _near(out, eager.float(), f"C5 64-row graph replay {rep} vs eager B=64")
+    stats = step.manager.stats()
+    assert stats["captures"] == 1 and stats["replays"] == 2 and stats["fallbacks"] == 0

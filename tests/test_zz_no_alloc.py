@@ -7,6 +7,9 @@ byte-identical; both are also held to the hot-path tolerance against the
 float64 oracle.  Two calls in a row, the second on a smaller batch (the
 scratch keeps the first call's partials), then a call that needs more scratch
 than the array holds, which must be refused before anything is launched.
+The captured form is checked first, so that in a process that runs this file
+alone the first call on the device (which looks up the array and records its
+ticket-clear kernel) happens inside the graph capture.
 """
 from __future__ import annotations
 
@@ -30,6 +33,59 @@ def _args(d, out, k_new=True):
              d.block_tables.data_ptr(), d.block_tables.shape[1], d.context_lens.data_ptr()),
             (d.q.shape[0], d.q.shape[1], hkv, hd, bs, 1.0 / hd ** 0.5, 0,
              torch.cuda.current_stream().cuda_stream))
+
+
+def _run_workspace_form(w):
+    """(out, k_pool, v_pool) of fe_paged_decode with a fresh caller-owned workspace."""
+    d = w.to(DEV)
+    out = torch.full_like(d.q, float("nan"))
+    head, tail = _args(d, out)
+    need = ops.decode_workspace_bytes(w.batch, w.q.shape[1], w.q.shape[2],
+                                      w.block_tables.shape[1] * w.block_size)
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    rc = _lib.load().fe_paged_decode(*head, ws.data_ptr(), need, *tail)
+    assert rc == 0, _lib.error_string(rc)
+    torch.cuda.synchronize()
+    return out.cpu(), d.k_pool.cpu(), d.v_pool.cpu()
+
+
+def _same_bits(a, b):
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_aa_noalloc_decode_captured_in_a_graph_replays_like_the_workspace_form():
+    """fe_paged_decode_noalloc recorded into a HIP graph (torch.cuda.graph) at C2 and
+    replayed twice: each replay's output and fused page write byte-identical to the
+    workspace form's.  Then eager calls after the first allocate nothing: the
+    device's free memory is unchanged across them."""
+    w = workloads.c2_workload()
+    o_ws, k_ws, v_ws = _run_workspace_form(w)
+    d = w.to(DEV)
+    out = torch.full_like(d.q, float("nan"))
+    lib = _lib.load()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        head, tail = _args(d, out)    # the capture stream is current here
+        rc = lib.fe_paged_decode_noalloc(*head, *tail)
+    assert rc == 0, _lib.error_string(rc)
+    for rep in range(2):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert _same_bits(out.cpu(), o_ws), f"replay {rep}"
+        assert _same_bits(d.k_pool.cpu(), k_ws) and _same_bits(d.v_pool.cpu(), v_ws), f"replay {rep}"
+    del g
+    head, tail = _args(d, out)
+    assert lib.fe_paged_decode_noalloc(*head, *tail) == 0
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        assert lib.fe_paged_decode_noalloc(*head, *tail) == 0
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    assert _same_bits(out.cpu(), o_ws)
 
 
 def _run_both(w):
