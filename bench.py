@@ -11,8 +11,10 @@ attention over its paged K/V and the LSE merge, with every input resident in HBM
 The decode plan (fe_paged_decode_plan: the split-K partition and the block rows
 of every workgroup) is computed once per model decode step and shared by its 28
 layers; the timed region runs it before step 0, 28, 56, ... (ceil(steps / 28)
-plan launches), so each step carries 1/28 of its cost.  --unplanned times
-fe_paged_decode instead (partition and tables at the start of every launch).
+plan launches in `steps` steps, the share the record states).  --unplanned
+times fe_paged_decode instead (partition and tables at the start of every
+launch); the unplanned launch is also timed beside the planned one and reported
+as roofline.us_per_launch_unplanned.
 
 Timing: exactly --steps steps between two synchronisations, replayed from HIP
 graphs (one graph cycling once over the rotating pools, replayed as often as it
@@ -23,9 +25,15 @@ bytes per step / wall time per step.  roofline.achieved = algorithmic bytes per
 launch / (HIP-event time of the timed region on the launch stream / steps).
 
 Also on the line:
-* c5: decode tok/s of the random-init Qwen2.5-1.5B (graph buckets 1 and 8, batch
-  64 eager and as a graph; contexts U{512..4096}), with the HBM bytes per step
-  and their fraction of 8 TB/s;
+* c3: the shared-prefix batch (B=256, 8 groups of 32 sharing 2048 tokens) through
+  the plain decode and the cascade decode (fe_paged_decode_shared_prefix), as GB/s
+  over the compulsory unique bytes and their fraction of 8 TB/s;
+* c4: the mixed step -- the ragged prefill (unplanned, and with the step's plan
+  charged 1/28) in TFLOP/s against the 2.5 PFLOP/s fp16 MFMA peak, the 48 decode
+  rows in GB/s, and the whole step;
+* c5: decode tok/s of the random-init Qwen2.5-1.5B (graph buckets 1, 2, 4 and 8,
+  batch 64 eager and as a graph; contexts U{512..4096}), with the HBM bytes per
+  step and their fraction of 8 TB/s;
 * reference_microbench: the reference's kernel microbenchmark shape
   (src/flexengine/research/profiling/kernel.py:14-41: one request of 512 tokens,
   12/2 heads, D 128, per-request attention_for_request, 10 warm-up + 50 timed
@@ -75,6 +83,8 @@ def parse_args(argv=None):
                    help="time budget per CPU-baseline route and config")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-c5", action="store_true", help="skip the Qwen2.5-1.5B decode tok/s")
+    p.add_argument("--no-c3c4", action="store_true", help="skip the C3 and C4 figures")
+    p.add_argument("--c3c4-iters", type=int, default=112)
     p.add_argument("--c5-steps", type=int, default=16)
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                    help="only run a device-to-device copy of MB MiB --steps times (calibrates the "
@@ -223,7 +233,8 @@ def c5_decode(steps: int) -> dict:
 
     model = Qwen2Model(Qwen2Config(), "cuda:0", seed=5)
     res = {}
-    for key, batch, mode in (("bucket1_graph", 1, "bucket"), ("bucket8_graph", 8, "bucket"),
+    for key, batch, mode in (("bucket1_graph", 1, "bucket"), ("bucket2_graph", 2, "bucket"),
+                             ("bucket4_graph", 4, "bucket"), ("bucket8_graph", 8, "bucket"),
                              ("b64_eager", 64, "eager"), ("b64_graph", 64, "graph")):
         r = bench_model.run(model, batch, steps, 3, mode)
         _progress(f"C5 {key}: {r['tok_s']} tok/s")
@@ -236,6 +247,34 @@ def c5_decode(steps: int) -> dict:
     res["workload"] = ("C5: random-init Qwen2.5-1.5B (28 layers, 12/2 heads, D 128, fp16), KV "
                        "N(0,1) with L ~ U{512..4096}, greedy; buckets via hipGraph replay")
     return res
+
+
+def c3_c4(iters: int) -> tuple[dict, dict]:
+    """C3 (plain and cascade decode) and C4 (prefill, decode rows, step), timed as
+    flexengine_amd.bench_attention does (HIP graphs, rotating pool copies)."""
+    import torch
+
+    from flexengine_amd import bench_attention as BA
+    from flexengine_amd import workloads
+
+    w = workloads.c3_workload()
+    hkv, d = w.k_pool.shape[2], w.k_pool.shape[3]
+    unique = w.unique_tokens * 2 * hkv * d * 2 + 2 * w.q.numel() * 2
+    plain = BA.bench_decode("C3", w, iters, 4, unique)
+    cascade = BA.bench_decode("C3", w, iters, 4, unique, shared_prefix=True)
+    del w
+    torch.cuda.empty_cache()
+    keys = ("us_per_call", "GB_s", "pct_hbm_peak", "effective_GB_s")
+    c3 = {"plain": {k: plain[k] for k in keys}, "cascade": {k: cascade[k] for k in keys},
+          "unique_bytes": unique, "logical_bytes": plain["bytes"],
+          "workload": "C3: B=256 in 8 groups of 32 sharing 2048 tokens + tails U[16,2048], "
+                      "12/2 heads, D 128, fp16, block 16; GB/s over the unique bytes"}
+    c4 = BA.bench_c4(iters, 4)
+    torch.cuda.empty_cache()
+    c4["workload"] = ("C4: 4 prefill chunks of 256-512 tokens over 0-3072 cached + 48 decode "
+                      "rows L~U[256,4096], 12/2 heads, D 128, fp16, block 16")
+    c4["decode_pct_hbm_peak"] = round(100.0 * c4["decode_GB_s"] / HBM_PEAK_GBS, 1)
+    return c3, c4
 
 
 def main(argv=None) -> int:
@@ -317,7 +356,32 @@ def main(argv=None) -> int:
     ms_per_step = wall * 1e3 / steps
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (per_launch_ms * 1e-3) / 1e9
-    del cycle, rest, pools
+    del cycle, rest
+    # the other form of the launch (unplanned when the headline is planned), same method
+    other_us = None
+    if planned:
+        def step_unplanned(i: int) -> None:
+            kp, vp = pools[i % n_pool]
+            ops.paged_decode(d.q, kp, vp, d.block_tables, d.context_lens, k_new=d.k_new,
+                             v_new=d.v_new, out=out, workspace=ws,
+                             target_splits=args.target_splits)
+        for i in range(n_pool):
+            step_unplanned(i)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n_pool * 7):
+                step_unplanned(i)
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(2):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        other_us = e0.elapsed_time(e1) * 1e3 / (2 * n_pool * 7)
+        del g
+    del pools
     torch.cuda.empty_cache()
 
     traffic, traffic_src = None, None
@@ -332,6 +396,10 @@ def main(argv=None) -> int:
     _progress(f"C2: {per_launch_ms * 1e3:.2f} us per launch, {value:.0f} GB/s")
     micro = reference_microbench(dev)
     _progress(f"reference microbenchmark shape: {micro['ms_per_call']} ms/call")
+    c3, c4 = (None, None) if args.no_c3c4 else c3_c4(args.c3c4_iters)
+    if c3 is not None:
+        _progress(f"C3 plain {c3['plain']['us_per_call']} us, cascade {c3['cascade']['us_per_call']} us;"
+                  f" C4 prefill {c4['prefill_planned_us']} us planned, decode {c4['decode_us']} us")
     c5 = None if args.no_c5 else c5_decode(args.c5_steps)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 
@@ -374,12 +442,16 @@ def main(argv=None) -> int:
             "traffic_source": traffic_src,
             "kernel": (f"piece_decode_kernel<128, true, true, {elem}> (fe_paged_decode_planned"
                        f"{sfx}: page write + split-K attention + in-kernel LSE merge, one "
-                       "launch; achieved includes 1/28 of decode_plan_kernel per launch)")
+                       f"launch; achieved includes {-(-steps // LAYERS)} decode_plan_kernel "
+                       f"launch(es) over the {steps} launches)")
                       if planned else
                       f"piece_decode_kernel<128, true, false, {elem}> (fe_paged_decode{sfx}: "
                       "page write + split-K attention + in-kernel LSE merge, one launch)",
             "us_per_launch": round(per_launch_ms * 1e3, 3),
+            "us_per_launch_unplanned": None if other_us is None else round(other_us, 3),
         },
+        "c3": c3,
+        "c4": c4,
         "c5": c5,
         "reference_microbench": micro,
         "cpu_baseline": cpu,
