@@ -30,6 +30,10 @@ __device__ __forceinline__ int readlane_i(int v, int lane) {
   return __builtin_amdgcn_readlane(v, lane);
 }
 
+// the two 32-bit halves of an address (plan descriptors record their inputs' addresses)
+__device__ __forceinline__ int lo32(const void* p) { return (int)(uint32_t)(uintptr_t)p; }
+__device__ __forceinline__ int hi32(const void* p) { return (int)(uint32_t)((uintptr_t)p >> 32); }
+
 // Cross-lane integer reductions and scans on DPP row operations (VALU, a few
 // cycles each) instead of LDS-routed shuffles: within each row of 16 lanes,
 // then across the four rows with readlane.

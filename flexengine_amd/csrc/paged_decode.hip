@@ -94,14 +94,27 @@ struct DecodeArgs {
   int* plan;
 };
 
-// The decode plan of one step: items = target + 2 * batch (the grid of the
-// piece kernel over kv_heads), a header per item -- the Piece fields b, id,
-// split, nsplit, L, tok0, tok_begin, tok_end; b = -1 for an item without a
-// piece, whose id field is then the row it zero-fills when inactive -- and
-// the tile list of each of its four waves (lane k: pool row of tile k).
+// The decode plan of one step: a descriptor of kPlanDesc ints -- kPlanMagic,
+// then the sizes it was computed for (batch, kv_heads, table width, block
+// size, num_blocks, target) and an error word the planned decode sets -- then,
+// for items = target + 2 * batch (the grid of the piece kernel over kv_heads),
+// a descriptor of the sizes and tables it was computed for (kPlanDesc words:
+// magic, batch, kv heads, table stride, block size, pool blocks, target, the
+// block-table and context-length addresses, zero padding, and last the error
+// word the planned kernel sets: kPlanErrSizes, kPlanErrStale), a header per item -- the Piece fields b, id, split, nsplit, L, tok0,
+// tok_begin, tok_end; b = -1 for an item without a piece, whose id field is
+// then the row it zero-fills when inactive -- and the tile list of each of its
+// four waves (lane k: pool row of tile k).
+constexpr int kPlanDesc = 16;
+constexpr int kPlanCheck = 11;          // descriptor words a planned call compares
 constexpr int kPlanHdr = 8;
+constexpr int kPlanMagic = 0x46504450;  // "PDPF"
+constexpr int kPlanErrSizes = 1;        // error word: the call's sizes are not the plan's
+constexpr int kPlanErrStale = 2;        // error word: a row's context length is not the plan's
+static_assert((kPlanDesc - 1) * 4 == FE_DECODE_PLAN_ERROR_OFFSET &&
+              kPlanErrSizes == FE_PLAN_ERR_SIZES && kPlanErrStale == FE_PLAN_ERR_STALE);
 inline size_t plan_bytes(int items) {
-  return (size_t)items * (kPlanHdr + kWaves * kWave) * sizeof(int32_t);
+  return ((size_t)kPlanDesc + (size_t)items * (kPlanHdr + kWaves * kWave)) * sizeof(int32_t);
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -234,10 +247,18 @@ __device__ __forceinline__ int tile_list_row(const DecodeArgs& a, const Piece& p
 __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const DecodeArgs a) {
   const int item = blockIdx.x;
   const int items = a.target + 2 * a.B;
+  if (item == 0 && threadIdx.x < kPlanDesc) {
+    const int desc[kPlanCheck] = {kPlanMagic, a.B, a.Hkv, a.W, a.BS, a.NB, a.target,
+                                  lo32(a.tables), hi32(a.tables), lo32(a.ctx), hi32(a.ctx)};
+    int v = 0;  // padding and the error word
+#pragma unroll
+    for (int i = 0; i < kPlanCheck; ++i) v = (int)threadIdx.x == i ? desc[i] : v;
+    a.plan[threadIdx.x] = v;
+  }
   Piece pc;
   int total = 0;
   const bool found = find_piece(a.ctx, nullptr, a.B, a.max_len, a.target, item, pc, total);
-  int* hdr = a.plan + (int64_t)item * kPlanHdr;
+  int* hdr = a.plan + kPlanDesc + (int64_t)item * kPlanHdr;
   if (threadIdx.x == 0) {
     hdr[0] = found ? pc.b : -1;
     hdr[1] = found ? pc.id : item - total;
@@ -250,7 +271,7 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const DecodeArgs 
   }
   if (!found) return;
   const int w = threadIdx.x / kWave;
-  a.plan[(int64_t)items * kPlanHdr + ((int64_t)item * kWaves + w) * kWave + lane_id()] =
+  a.plan[kPlanDesc + (int64_t)items * kPlanHdr + ((int64_t)item * kWaves + w) * kWave + lane_id()] =
       tile_list_row(a, pc, w);
 }
 
@@ -269,18 +290,44 @@ void piece_decode_kernel(const DecodeArgs a) {
   bool found;
   int spare_row;
   if constexpr (PLANNED) {
-    // the header and this lane's tile row come from the plan, both loads in flight at once
-    const int* hdr = a.plan + (int64_t)item * kPlanHdr;
-    planned_row = a.plan[(int64_t)(a.target + 2 * a.B) * kPlanHdr +
-                         ((int64_t)item * kWaves + w) * kWave + lane_id()];
-    pc.b = __builtin_amdgcn_readfirstlane(hdr[0]);
-    pc.id = __builtin_amdgcn_readfirstlane(hdr[1]);
-    pc.split = __builtin_amdgcn_readfirstlane(hdr[2]);
-    pc.nsplit = __builtin_amdgcn_readfirstlane(hdr[3]);
-    pc.L = __builtin_amdgcn_readfirstlane(hdr[4]);
-    pc.tok0 = __builtin_amdgcn_readfirstlane(hdr[5]);
-    pc.tok_begin = __builtin_amdgcn_readfirstlane(hdr[6]);
-    pc.tok_end = __builtin_amdgcn_readfirstlane(hdr[7]);
+    // The descriptor, the header and this lane's tile row, all loads in flight at
+    // once (the host checked that the plan holds the call's items, so the header
+    // and row loads stay inside it whatever the plan is for).  A plan computed
+    // for other sizes or tables addresses other partial slots and rows, so none
+    // of it is used: every workgroup of the grid (items >= batch, so one per row
+    // and kv head) fills its row's heads with NaN, and the error word is set.
+    const int lane = lane_id();
+    const int dv = lane < kPlanDesc ? a.plan[lane] : 0;
+    const int* hdr = a.plan + kPlanDesc + (int64_t)item * kPlanHdr;
+    planned_row = a.plan[kPlanDesc + (int64_t)(a.target + 2 * a.B) * kPlanHdr +
+                         ((int64_t)item * kWaves + w) * kWave + lane];
+    const int h0 = hdr[0], h1 = hdr[1], h2 = hdr[2], h3 = hdr[3];
+    const int h4 = hdr[4], h5 = hdr[5], h6 = hdr[6], h7 = hdr[7];
+    {
+      const int want[kPlanCheck] = {kPlanMagic, a.B, a.Hkv, a.W, a.BS, a.NB, a.target,
+                                    lo32(a.tables), hi32(a.tables), lo32(a.ctx), hi32(a.ctx)};
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < kPlanCheck; ++i) ok = ok && readlane_i(dv, i) == want[i];
+      if (!ok) {
+        if (item < a.B) {
+          for (int e = threadIdx.x; e < a.G * D; e += kThreads)
+            a.out[((int64_t)item * a.Hq + h * a.G) * D + e] = to16<E>(__builtin_nanf(""));
+        }
+        if (item == 0 && h == 0 && threadIdx.x == 0)
+          __hip_atomic_store(a.plan + kPlanDesc - 1, kPlanErrSizes, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+    }
+    pc.b = __builtin_amdgcn_readfirstlane(h0);
+    pc.id = __builtin_amdgcn_readfirstlane(h1);
+    pc.split = __builtin_amdgcn_readfirstlane(h2);
+    pc.nsplit = __builtin_amdgcn_readfirstlane(h3);
+    pc.L = __builtin_amdgcn_readfirstlane(h4);
+    pc.tok0 = __builtin_amdgcn_readfirstlane(h5);
+    pc.tok_begin = __builtin_amdgcn_readfirstlane(h6);
+    pc.tok_end = __builtin_amdgcn_readfirstlane(h7);
     found = pc.b >= 0;
     spare_row = pc.id;
   } else {
@@ -304,6 +351,12 @@ void piece_decode_kernel(const DecodeArgs a) {
   const int n = lane & 15;
   const int G = a.G;
   const int b = pc.b;
+  // A plan of the same sizes computed for other context lengths would put the
+  // fused page write at a stale position: the row's live length is loaded here
+  // (its wait falls after the loop) and a piece whose length is not the plan's
+  // writes nothing to the pool and contributes NaN.
+  int live_len = pc.L;
+  if constexpr (PLANNED) live_len = seq_len(a.ctx, b, a.max_len);
   const int t_first = pc.tok_begin / kTile + w;
   const int t_end = (pc.tok_end + kTile - 1) / kTile;
 
@@ -361,7 +414,7 @@ void piece_decode_kernel(const DecodeArgs a) {
     for (int s = 0; s < C::NK; ++s) core.qv[s] = qv[s];
     core.init_acc();
     core.run();
-    core.store_new_row(a.k_pool, a.v_pool);
+    if (live_len == pc.L) core.store_new_row(a.k_pool, a.v_pool);
     m_run = core.m_run;
     l_tot = core.l_total();
 #pragma unroll
@@ -418,6 +471,13 @@ void piece_decode_kernel(const DecodeArgs a) {
       for (int v = 0; v < kWaves; ++v) acc += sc[v] * park[(v * C::NX + x) * kWave + lane];
       ox[xi] = acc * inv;
     }
+  }
+  if (PLANNED && live_len != pc.L) {
+#pragma unroll
+    for (int xi = 0; xi < XW; ++xi) ox[xi] = f32x4{1.f, 1.f, 1.f, 1.f} * __builtin_nanf("");
+    if (threadIdx.x == 0)
+      __hip_atomic_store(a.plan + kPlanDesc - 1, kPlanErrStale, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
   const int hq = h * G + (n < G ? n : G - 1);
   if (!split) {
@@ -1239,7 +1299,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
                 const int32_t* context_lens, void* workspace, size_t workspace_bytes, int batch,
                 int num_q_heads, int kv_heads, int head_dim, int block_size, float scale,
                 int target_splits, CascadePrefix* cascade, hipStream_t stream,
-                const void* plan = nullptr, size_t plan_len = 0, bool bf16 = false) {
+                void* plan = nullptr, size_t plan_len = 0, bool bf16 = false) {
   FE_CHECK_ARG(batch >= 0 && num_q_heads > 0 && kv_heads > 0 && num_blocks > 0 &&
                table_stride > 0 && target_splits >= 0);
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
@@ -1427,7 +1487,7 @@ extern "C" int fe_paged_decode_planned(const void* q, int64_t q_batch_stride, vo
                                        void* workspace, size_t workspace_bytes, int batch,
                                        int num_q_heads, int kv_heads, int head_dim,
                                        int block_size, float scale, int target_splits,
-                                       const void* plan, size_t plan_len, fe_stream_t stream) {
+                                       void* plan, size_t plan_len, fe_stream_t stream) {
   if (plan == nullptr) return FE_ERR_INVALID_ARGUMENT;
   return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
                      num_blocks, block_tables, table_stride, context_lens, workspace,
@@ -1457,7 +1517,7 @@ extern "C" int fe_paged_decode_planned_bf16(const void* q, int64_t q_batch_strid
                                             void* workspace, size_t workspace_bytes, int batch,
                                             int num_q_heads, int kv_heads, int head_dim,
                                             int block_size, float scale, int target_splits,
-                                            const void* plan, size_t plan_len,
+                                            void* plan, size_t plan_len,
                                             fe_stream_t stream) {
   if (plan == nullptr) return FE_ERR_INVALID_ARGUMENT;
   return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,

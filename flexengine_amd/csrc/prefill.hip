@@ -87,7 +87,7 @@ struct PrefillArgs {
   int* tickets;      // [row blocks * Hkv] (stream-K kernel: [nwg_max]), zero between calls
   // stream-K kernel: the step's plan (fe_prefill_plan), null to derive the
   // work split in the launch
-  const int* plan;
+  int* plan;
   int64_t q_stride;  // elements from one query row (token or sequence) to the next
   int W, S, total_q, Hq, Hkv, G, BS, bs_log2, NB, KS;
   int nwg_max;       // stream-K kernel: workgroups of the launch
@@ -1359,20 +1359,65 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
 // ranges and, per workgroup, its range and first unit -- and
 // fe_prefill_paged_planned reads it with one load instead of the scans of
 // stream_plan and stream_locate.  Layout (int32): a header of kPPlanInts
-// (nwg, T, q, r of the Ranges), then kPPlanInts per workgroup: x_begin,
-// x_end, has work, logical id, then the StreamPos s, h, rb, kb, q0, n,
-// cached, R, tb.
+// (nwg, T, q, r of the Ranges), a descriptor of kPPlanInts (what the plan was
+// computed for: magic, the sizes, the q_offsets and context_lens addresses, a
+// digest of their contents, and last an error word the planned kernel sets),
+// then kPPlanInts per workgroup: x_begin, x_end, has work, logical id, then the
+// StreamPos s, h, rb, kb, q0, n, cached, R, tb.
+//
+// A planned launch checks the descriptor before anything else: every unit after
+// a workgroup's first is located from the live q_offsets / context_lens, so a
+// plan of other contents would make workgroups disagree on a unit's size and
+// leave its ticket set for the next launch.  On a mismatch the launch writes
+// NaN to every output row, sets the error word and returns.
 constexpr int kPPlanInts = 16;
-inline size_t pplan_bytes() { return (size_t)(1 + kMaxStreamWgs) * kPPlanInts * sizeof(int32_t); }
+constexpr int kPPlanMagic = 0x46505046;  // "FPPF"
+constexpr int kPPlanCheck = 13;          // descriptor words a planned launch compares
+constexpr int kPPlanErrSizes = 1;        // error word: the call's sizes or tensors are not the plan's
+constexpr int kPPlanErrStale = 2;        // error word: q_offsets / context_lens changed since the plan
+static_assert((2 * kPPlanInts - 1) * 4 == FE_PREFILL_PLAN_ERROR_OFFSET &&
+              kPPlanErrSizes == FE_PLAN_ERR_SIZES && kPPlanErrStale == FE_PLAN_ERR_STALE);
+inline size_t pplan_bytes() { return (size_t)(2 + kMaxStreamWgs) * kPPlanInts * sizeof(int32_t); }
+
+// lowbias32 (C. Wellons' published 32-bit integer hash)
+__device__ __forceinline__ uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+// Digest of q_offsets[0..S] and context_lens[0..S), uniform over the wave.
+__device__ __forceinline__ int lens_digest(const PrefillArgs& a) {
+  const int lane = lane_id();
+  uint32_t d = lane == 0 ? mix32((uint32_t)a.q_off[a.S] ^ 0x5bd1e995u) : 0u;
+  for (int base = 0; base < a.S; base += kWave) {
+    const int s = base + lane;
+    if (s < a.S)
+      d += mix32((uint32_t)a.q_off[s] + 0x9e3779b9u * (uint32_t)(s + 1)) ^
+           mix32((uint32_t)a.ctx[s] + 0x85ebca6bu * (uint32_t)(s + 1));
+  }
+  return wave_sum_i((int)d);
+}
 
 // One wave per workgroup entry of the launch the plan is for (grid nwg_max).
 __global__ __launch_bounds__(kWave) void prefill_plan_kernel(const PrefillArgs a, int* plan) {
   const StreamPlan pl = stream_plan(a);
   const int nwg = pl.rg.nwg;
   const int lane = lane_id();
-  if (blockIdx.x == 0 && lane < kPPlanInts) {
+  if (blockIdx.x == 0) {
+    const int digest = lens_digest(a);
     const int hdr[4] = {nwg, pl.rg.T, pl.rg.q, pl.rg.r};
-    plan[lane] = lane < 4 ? hdr[lane] : 0;
+    const int desc[kPPlanCheck] = {kPPlanMagic, a.S, a.total_q, a.Hq, a.Hkv, a.W, a.BS,
+                                   a.nwg_max, lo32(a.q_off), hi32(a.q_off), lo32(a.ctx),
+                                   hi32(a.ctx), digest};
+    int v = 0;  // zero padding and the error word
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v = lane == i ? hdr[i] : v;
+#pragma unroll
+    for (int i = 0; i < kPPlanCheck; ++i) v = lane == kPPlanInts + i ? desc[i] : v;
+    if (lane < 2 * kPPlanInts) plan[lane] = v;
   }
   int e[13] = {};
   if ((int)blockIdx.x < nwg) {
@@ -1390,7 +1435,7 @@ __global__ __launch_bounds__(kWave) void prefill_plan_kernel(const PrefillArgs a
   int out = 0;
 #pragma unroll
   for (int i = 0; i < 13; ++i) out = lane == i ? e[i] : out;
-  if (lane < kPPlanInts) plan[kPPlanInts + (int)blockIdx.x * kPPlanInts + lane] = out;
+  if (lane < kPPlanInts) plan[2 * kPPlanInts + (int)blockIdx.x * kPPlanInts + lane] = out;
 }
 
 template <int D, int RT, class E = Fp16, bool PLANNED = false>
@@ -1418,12 +1463,35 @@ void prefill_dma_kernel(const PrefillArgs a) {
   StreamPos sp;
   int gid, x_begin, x_end;
   if constexpr (PLANNED) {
-    // the ranges and this workgroup's first unit from the plan: its header and
-    // entry in one round trip (lanes 0-15 the entry, 16-31 the header)
+    // the ranges and this workgroup's first unit from the plan: its entry,
+    // header and descriptor in one round trip (lanes 0-15 the entry, 16-31 the
+    // header, 32-47 the descriptor), the live lengths' loads beside them
     const int lane = lane_id();
-    const int v = lane < kPPlanInts
-                      ? a.plan[kPPlanInts + (int)blockIdx.x * kPPlanInts + lane]
-                      : (lane < 2 * kPPlanInts ? a.plan[lane - kPPlanInts] : 0);
+    const int v = lane < kPPlanInts ? a.plan[2 * kPPlanInts + (int)blockIdx.x * kPPlanInts + lane]
+                                    : (lane < 3 * kPPlanInts ? a.plan[lane - kPPlanInts] : 0);
+    const int digest = lens_digest(a);
+    {
+      const int want[kPPlanCheck] = {kPPlanMagic, a.S, a.total_q, a.Hq, a.Hkv, a.W, a.BS,
+                                     a.nwg_max, lo32(a.q_off), hi32(a.q_off), lo32(a.ctx),
+                                     hi32(a.ctx), digest};
+      int bad = 0;
+#pragma unroll
+      for (int i = 0; i < kPPlanCheck; ++i)
+        bad = bad ? bad : (readlane_i(v, 2 * kPPlanInts + i) == want[i]
+                               ? 0
+                               : (i + 1 == kPPlanCheck ? kPPlanErrStale : kPPlanErrSizes));
+      if (bad) {
+        const f16 nan = to16<E>(__builtin_nanf(""));
+        const int64_t n = (int64_t)a.total_q * a.Hq * D;
+        for (int64_t e = (int64_t)blockIdx.x * kDmaThreads + threadIdx.x; e < n;
+             e += (int64_t)gridDim.x * kDmaThreads)
+          a.out[e] = nan;
+        if (blockIdx.x == 0 && threadIdx.x == 0)
+          __hip_atomic_store(a.plan + 2 * kPPlanInts - 1, bad, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+    }
     pl.rg = Ranges{readlane_i(v, 16 + 1), readlane_i(v, 16 + 0), readlane_i(v, 16 + 2),
                    readlane_i(v, 16 + 3)};
     pl.w0 = SeqWork{};
@@ -1590,7 +1658,7 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
                  const int32_t* context_lens, int num_seqs, int total_q, int max_q_len,
                  int num_q_heads, int kv_heads, int head_dim, int block_size, float scale,
                  void* workspace, size_t workspace_bytes, fe_stream_t stream, bool bf16,
-                 const void* step_plan = nullptr, size_t plan_bytes = 0) {
+                 void* step_plan = nullptr, size_t plan_bytes = 0) {
   FE_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 &&
                kv_heads > 0 && num_blocks > 0 && table_stride > 0);
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
@@ -1650,7 +1718,7 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   a.pre_o = nullptr;
   a.pre_lse = nullptr;
   a.tok0 = nullptr;
-  a.plan = (const int*)step_plan;
+  a.plan = (int*)step_plan;
   hipStream_t s = (hipStream_t)stream;
   if (dma && bf16) {
     if (head_dim == 64) launch_prefill_dma<64, Bf16>(a, s); else launch_prefill_dma<128, Bf16>(a, s);
@@ -1743,7 +1811,7 @@ extern "C" int fe_prefill_paged_planned(const void* q, void* out, const void* k_
                                         const int32_t* q_offsets, const int32_t* context_lens,
                                         int num_seqs, int total_q, int max_q_len, int num_q_heads,
                                         int kv_heads, int head_dim, int block_size, float scale,
-                                        void* workspace, size_t workspace_bytes, const void* plan,
+                                        void* workspace, size_t workspace_bytes, void* plan,
                                         size_t plan_bytes, fe_stream_t stream) {
   FE_CHECK_ARG(plan != nullptr);
   return prefill_impl(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride, q_offsets,
@@ -1757,7 +1825,7 @@ extern "C" int fe_prefill_paged_planned_bf16(
     const int32_t* block_tables, int table_stride, const int32_t* q_offsets,
     const int32_t* context_lens, int num_seqs, int total_q, int max_q_len, int num_q_heads,
     int kv_heads, int head_dim, int block_size, float scale, void* workspace,
-    size_t workspace_bytes, const void* plan, size_t plan_bytes, fe_stream_t stream) {
+    size_t workspace_bytes, void* plan, size_t plan_bytes, fe_stream_t stream) {
   FE_CHECK_ARG(plan != nullptr);
   return prefill_impl(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride, q_offsets,
                       context_lens, num_seqs, total_q, max_q_len, num_q_heads, kv_heads, head_dim,

@@ -462,6 +462,20 @@ def prefill_paged_plan(q_offsets: torch.Tensor, context_lens: torch.Tensor, tota
     return PrefillPlan(buffer, q_offsets.data_ptr(), context_lens.data_ptr(), shape)
 
 
+# a planned launch's verdict on its plan (include/flexengine_amd.h FE_PLAN_ERR_*)
+PLAN_ERR_SIZES = 1   # other sizes or other block_tables / q_offsets / context_lens tensors
+PLAN_ERR_STALE = 2   # the lengths changed after the plan was computed
+_PLAN_ERROR_OFFSET = {"DecodePlan": 60, "PrefillPlan": 124}
+
+
+def plan_error(plan: DecodePlan | PrefillPlan) -> int:
+    """The plan's error word as the planned launches since the plan call left it:
+    0, PLAN_ERR_SIZES or PLAN_ERR_STALE (those launches wrote NaN instead of using
+    the plan).  Reads the word back from the device, after the stream's work."""
+    off = _PLAN_ERROR_OFFSET[type(plan).__name__]
+    return int(plan.buffer[off:off + 4].view(torch.int32).item())
+
+
 def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                   block_tables: torch.Tensor, q_offsets: torch.Tensor,
                   context_lens: torch.Tensor, max_q_len: int, *, scale: float | None = None,

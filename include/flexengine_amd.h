@@ -47,6 +47,19 @@ typedef struct ihipStream_t* fe_stream_t;
 /* Bytes of the static per-GPU scratch array of fe_paged_decode_noalloc. */
 #define FE_PAGED_DECODE_NOALLOC_SCRATCH_BYTES (16u << 20)
 
+/*
+ * A planned launch (fe_paged_decode_planned, fe_prefill_paged_planned and their
+ * bf16 forms) checks its plan before using it and reports a mismatch in the
+ * plan's error word: an int32 at these byte offsets of the plan buffer, zeroed
+ * by the plan call, set by the planned launch (the planned calls therefore take
+ * the plan as writable).  The launch itself has returned FE_OK: the check runs
+ * on the device, so the caller reads the word after the stream's work is done.
+ */
+#define FE_DECODE_PLAN_ERROR_OFFSET 60
+#define FE_PREFILL_PLAN_ERROR_OFFSET 124
+#define FE_PLAN_ERR_SIZES 1  /* other sizes, block_tables / q_offsets / context_lens tensors */
+#define FE_PLAN_ERR_STALE 2  /* the lengths changed since the plan was computed */
+
 /* Library version (major*10000 + minor*100 + patch). */
 int fe_version(void);
 
@@ -207,8 +220,13 @@ int fe_paged_decode_plan(const int32_t* block_tables, int table_stride,
  * (written by fe_paged_decode_plan on the same block_tables, table_stride,
  * context_lens, num_blocks, batch, kv_heads, block_size and target_splits,
  * earlier on the stream): same results, one dependent load fewer before the
- * first K/V loads.  A plan from other sizes or tables gives wrong results;
- * a plan_bytes below fe_paged_decode_plan_size returns FE_ERR_WORKSPACE.
+ * first K/V loads.  A plan_bytes below fe_paged_decode_plan_size returns
+ * FE_ERR_WORKSPACE.  A plan recorded for other sizes or other block_tables /
+ * context_lens addresses is not used: every output row is NaN and the error
+ * word is FE_PLAN_ERR_SIZES.  A row whose live context length is not the
+ * plan's (lengths changed after the plan call) writes nothing to the pools and
+ * gives NaN, and the error word is FE_PLAN_ERR_STALE; other rows are exact.
+ * Block-table contents are not checked: the plan's block rows are used.
  */
 int fe_paged_decode_planned(const void* q, int64_t q_batch_stride, void* out,
                             const void* k_new, const void* v_new, int64_t new_batch_stride,
@@ -218,7 +236,7 @@ int fe_paged_decode_planned(const void* q, int64_t q_batch_stride, void* out,
                             void* workspace, size_t workspace_bytes,
                             int batch, int num_q_heads, int kv_heads, int head_dim,
                             int block_size, float scale, int target_splits,
-                            const void* plan, size_t plan_bytes, fe_stream_t stream);
+                            void* plan, size_t plan_bytes, fe_stream_t stream);
 
 /*
  * bf16 forms of fe_paged_decode and fe_paged_decode_planned: the same
@@ -246,7 +264,7 @@ int fe_paged_decode_planned_bf16(const void* q, int64_t q_batch_stride, void* ou
                                  void* workspace, size_t workspace_bytes,
                                  int batch, int num_q_heads, int kv_heads, int head_dim,
                                  int block_size, float scale, int target_splits,
-                                 const void* plan, size_t plan_bytes, fe_stream_t stream);
+                                 void* plan, size_t plan_bytes, fe_stream_t stream);
 
 /*
  * fe_paged_decode without a workspace argument, for callers that cannot
@@ -403,7 +421,11 @@ int fe_prefill_paged_bf16(const void* q, void* out,
  * (and its bf16 form) is fe_prefill_paged reading the split from it, with the
  * same results.  The plan must come from the same q_offsets, context_lens,
  * table_stride, block_size and head counts, and be complete (stream order)
- * before the planned calls.  Sizes the stream-K kernel does not take (block
+ * before the planned calls.  A planned launch compares the plan's record of
+ * the sizes, of the q_offsets / context_lens addresses and of a digest of
+ * their contents with its own; on a mismatch every output row is NaN and the
+ * error word is FE_PLAN_ERR_SIZES (sizes, addresses) or FE_PLAN_ERR_STALE
+ * (contents).  Sizes the stream-K kernel does not take (block
  * sizes not a multiple of 16, or beyond its 32-bit work split) return
  * FE_ERR_UNSUPPORTED from fe_prefill_plan; such steps call fe_prefill_paged.
  * No counterpart in the reference: its prefill has no work split to plan; one
@@ -421,7 +443,7 @@ int fe_prefill_paged_planned(const void* q, void* out,
                              int num_q_heads, int kv_heads, int head_dim,
                              int block_size, float scale,
                              void* workspace, size_t workspace_bytes,
-                             const void* plan, size_t plan_bytes, fe_stream_t stream);
+                             void* plan, size_t plan_bytes, fe_stream_t stream);
 int fe_prefill_paged_planned_bf16(const void* q, void* out,
                                   const void* k_pool, const void* v_pool, int num_blocks,
                                   const int32_t* block_tables, int table_stride,
@@ -430,7 +452,7 @@ int fe_prefill_paged_planned_bf16(const void* q, void* out,
                                   int num_q_heads, int kv_heads, int head_dim,
                                   int block_size, float scale,
                                   void* workspace, size_t workspace_bytes,
-                                  const void* plan, size_t plan_bytes, fe_stream_t stream);
+                                  void* plan, size_t plan_bytes, fe_stream_t stream);
 
 /*
  * Bytes of device workspace fe_prefill_paged needs for these sizes (its key

@@ -149,3 +149,14 @@ def test_cpu_tensors_are_rejected_not_computed():
     t = torch.zeros(1, 1, dtype=torch.int32)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.paged_decode(q, pool, pool, t, torch.ones(1, dtype=torch.int32))
+
+
+def test_plan_error_word_constants_match_the_header():
+    """ops.plan_error reads the words the header places; the kernels static_assert the same."""
+    from flexengine_amd import ops
+    text = (Path(__file__).resolve().parents[1] / "include" / "flexengine_amd.h").read_text()
+    macros = dict(re.findall(r"#define\s+(FE_\w+)\s+(\d+)", text))
+    assert int(macros["FE_DECODE_PLAN_ERROR_OFFSET"]) == ops._PLAN_ERROR_OFFSET["DecodePlan"]
+    assert int(macros["FE_PREFILL_PLAN_ERROR_OFFSET"]) == ops._PLAN_ERROR_OFFSET["PrefillPlan"]
+    assert int(macros["FE_PLAN_ERR_SIZES"]) == ops.PLAN_ERR_SIZES
+    assert int(macros["FE_PLAN_ERR_STALE"]) == ops.PLAN_ERR_STALE

@@ -576,3 +576,71 @@ def test_planned_decode_rejects_a_foreign_plan():
                                   d.context_lens.data_ptr(), nb, d.q.shape[0], hkv, bs, 0,
                                   small.data_ptr(), small.numel(), None)
     assert rc == _lib.FE_ERR_WORKSPACE
+
+
+def _planned_call(d, out, plan, tables):
+    """fe_paged_decode_planned through the C ABI (ops refuses a plan for other tensors
+    before launching; the library's own check is what is tested here)."""
+    nb, bs, hkv, hd = d.k_pool.shape
+    need = ops.decode_workspace_bytes(d.q.shape[0], d.q.shape[1], hd, tables.shape[1] * bs)
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    rc = _lib.load().fe_paged_decode_planned(
+        d.q.data_ptr(), d.q.stride(0), out.data_ptr(), d.k_new.data_ptr(), d.v_new.data_ptr(),
+        d.k_new.stride(0), d.k_pool.data_ptr(), d.v_pool.data_ptr(), nb, tables.data_ptr(),
+        tables.shape[1], d.context_lens.data_ptr(), ws.data_ptr(), need, d.q.shape[0],
+        d.q.shape[1], hkv, hd, bs, 1.0 / math.sqrt(hd), 0, plan.buffer.data_ptr(),
+        plan.buffer.numel(), torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.FE_OK, _lib.error_string(rc)
+    torch.cuda.synchronize()
+
+
+def test_planned_decode_refuses_a_plan_recorded_for_other_tables():
+    """A plan whose record of the tables' address is not the call's: NaN in every row,
+    no page write, error word FE_PLAN_ERR_SIZES; the next plan call clears the word."""
+    w = _planned_cases()[1]
+    d = w.to(DEV)
+    nb, bs, hkv = d.k_pool.shape[0], d.k_pool.shape[1], d.k_pool.shape[2]
+    plan = ops.paged_decode_plan(d.block_tables, d.context_lens, nb, hkv, bs)
+    k0, v0 = d.k_pool.clone(), d.v_pool.clone()
+    out = torch.zeros_like(d.q)
+    _planned_call(d, out, plan, d.block_tables.clone())
+    assert torch.isnan(out).all(), "rows computed from a plan for other tables"
+    assert ops.plan_error(plan) == ops.PLAN_ERR_SIZES
+    assert torch.equal(d.k_pool, k0) and torch.equal(d.v_pool, v0), "page written"
+    ops.paged_decode_plan(d.block_tables, d.context_lens, nb, hkv, bs, out=plan)
+    assert ops.plan_error(plan) == 0
+    kp, vp = d.k_pool.clone(), d.v_pool.clone()
+    ref = ops.paged_decode(d.q, kp, vp, d.block_tables, d.context_lens, k_new=d.k_new,
+                           v_new=d.v_new)
+    _planned_call(d, out, plan, d.block_tables)
+    assert torch.equal(out, ref) and ops.plan_error(plan) == 0
+    assert torch.equal(d.k_pool, kp) and torch.equal(d.v_pool, vp)
+
+
+def test_stale_plan_rows_are_nan_and_write_no_page():
+    """Lengths changed in place after the plan call (a plan of the previous step):
+    those rows give NaN and write nothing to the pools, the error word is
+    FE_PLAN_ERR_STALE, and every other row is what an unplanned call gives."""
+    w = _planned_cases()[1]                  # lengths [0, 1, 15, 16, 17, 200, 0, 1023, 4096, 64]
+    d = w.to(DEV)
+    nb, bs, hkv = d.k_pool.shape[0], d.k_pool.shape[1], d.k_pool.shape[2]
+    plan = ops.paged_decode_plan(d.block_tables, d.context_lens, nb, hkv, bs)
+    stale = [2, 5]                           # 15 -> 16 and 200 -> 201: tile and piece edges
+    d.context_lens[stale] += 1
+    k0, v0 = d.k_pool.clone(), d.v_pool.clone()
+    got = ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens,
+                           k_new=d.k_new, v_new=d.v_new, plan=plan)
+    torch.cuda.synchronize()
+    assert ops.plan_error(plan) == ops.PLAN_ERR_STALE
+    assert torch.isnan(got[stale]).all()
+    keep = [b for b in range(w.batch) if b not in stale]
+    # the same call without the stale rows (inactive: no output, no page write)
+    lens = d.context_lens.clone()
+    lens[stale] = 0
+    kp, vp = k0.clone(), v0.clone()
+    ref = ops.paged_decode(d.q, kp, vp, d.block_tables, lens, k_new=d.k_new, v_new=d.v_new)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got[keep]).all()
+    diff = (got[keep].float() - ref[keep].float()).abs().max().item()
+    assert diff <= 2e-3, f"kept rows differ from the unplanned call by {diff}"
+    assert torch.equal(d.k_pool, kp) and torch.equal(d.v_pool, vp), "stale rows wrote a page"

@@ -238,3 +238,42 @@ def test_planned_prefill_bf16_and_refusals():
                                      q.shape[0], q.shape[1], kp.shape[2], tables.shape[1], bs,
                                      small.data_ptr(), small.numel(), None)
     assert rc == _lib.FE_ERR_WORKSPACE
+
+
+def test_planned_prefill_checks_its_plan_and_leaves_tickets_clean():
+    """A plan for other tensors (a clone of context_lens, same contents) and a stale plan
+    (a length changed in place after the plan call) are not used: every row NaN and the
+    error word set, before any split unit's ticket is taken -- so the unplanned and
+    freshly planned launches that follow are exact."""
+    q, offs, ctx, tables, kp, vp, bs = _planned_prefill_cases()["small"]  # lengths 130, 47, 1000
+    hq, hkv, d = q.shape[1], kp.shape[2], q.shape[2]
+    qd, kd, vd = q.to(DEV), kp.to(DEV), vp.to(DEV)
+    offs_d, ctx_d, tables_d = offs.to(DEV), ctx.to(DEV), tables.to(DEV)
+    max_q = int((offs[1:] - offs[:-1]).max())
+    plan = ops.prefill_paged_plan(offs_d, ctx_d, q.shape[0], hq, hkv, tables.shape[1], bs)
+    need = int(_lib.load().fe_prefill_workspace_size(ctx.shape[0], q.shape[0], hq, hkv, d))
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    out = torch.zeros_like(qd)
+    rc = _lib.load().fe_prefill_paged_planned(
+        qd.data_ptr(), out.data_ptr(), kd.data_ptr(), vd.data_ptr(), kp.shape[0],
+        tables_d.data_ptr(), tables.shape[1], offs_d.data_ptr(), ctx_d.clone().data_ptr(),
+        ctx.shape[0], q.shape[0], max_q, hq, hkv, d, bs, 1.0 / math.sqrt(d), ws.data_ptr(),
+        need, plan.buffer.data_ptr(), plan.buffer.numel(),
+        torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.FE_OK
+    torch.cuda.synchronize()
+    assert torch.isnan(out).all() and ops.plan_error(plan) == ops.PLAN_ERR_SIZES
+    ctx_d[1] += 1                                              # 47 -> 48, same page count
+    got = ops.prefill_paged(qd, kd, vd, tables_d, offs_d, ctx_d, max_q, plan=plan)
+    torch.cuda.synchronize()
+    assert torch.isnan(got).all() and ops.plan_error(plan) == ops.PLAN_ERR_STALE
+    ref = ops.prefill_paged(qd, kd, vd, tables_d, offs_d, ctx_d, max_q)
+    ops.prefill_paged_plan(offs_d, ctx_d, q.shape[0], hq, hkv, tables.shape[1], bs, out=plan)
+    got = ops.prefill_paged(qd, kd, vd, tables_d, offs_d, ctx_d, max_q, plan=plan)
+    torch.cuda.synchronize()
+    assert ops.plan_error(plan) == 0 and torch.equal(got, ref)
+    ctx2 = ctx.clone()
+    ctx2[1] += 1
+    exp = R.prefill_reference(q.numpy(), offs.numpy(), ctx2.numpy(), kp.numpy(), vp.numpy(),
+                              tables.numpy(), bs)
+    assert_attention_close(got.cpu().numpy(), exp, what="after a refused plan")
