@@ -54,6 +54,10 @@ constexpr int kPS = kBlockKeys / 32;    // 32-key PV steps per block
 // 55 us; 8: 61 us, 8 with loads only for the live splits: 57.5 us, 2: 63 us; the
 // C3 shared-prefix decode 81 us at 4 and 8, 91 us at 2).
 constexpr int kMaxSplits = 4;
+// Rows of the split merge whose partials are loaded in one round trip: the C3
+// shared-prefix pass took 24.15 us with 1 (a round trip per 8 rows), 23.79 with
+// 2, 23.06 with 4 and 23.14 with 8.
+constexpr int kMergeRows = 4;
 // Two 16-row tiles per wave (RT = 2) once the rows fill this many 128-row blocks;
 // below it the extra blocks of RT = 1 fill the CUs better (measured: 1377 new tokens
 // x 12 heads run slower with RT = 2).
@@ -478,43 +482,55 @@ void prefill_kernel(const PrefillArgs a) {
     __hip_atomic_store(a.tickets + item * a.Hkv + h, 0, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   // merge: thread -> (row of the block, 4 consecutive dims).  All KS LSEs and
-  // partial outputs of a row are loaded at once (indices past KS repeat the
-  // last split and get weight 0), so a row costs one round trip to memory.
+  // partial outputs of kMergeRows of the thread's rows are loaded at once
+  // (indices past KS repeat the last split and get weight 0; rows past the
+  // block repeat its last row and are not stored), so the block's rows cost
+  // ceil(rows / (RPS * kMergeRows)) round trips to memory.
   constexpr int TPR = D / 4;             // threads per row
   constexpr int RPS = kThreads / TPR;    // rows per pass
   const int d4 = (tid % TPR) * 4;
-  for (int row = r0 + tid / TPR; row <= r_last; row += RPS) {
-    const int64_t orow_idx = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
-    float lse[kMaxSplits];
-    f32x4 ov[kMaxSplits];
+  for (int row0 = r0 + tid / TPR; row0 <= r_last; row0 += RPS * kMergeRows) {
+    float lse[kMergeRows][kMaxSplits];
+    f32x4 ov[kMergeRows][kMaxSplits];
+    int64_t orow_idx[kMergeRows];
 #pragma unroll
-    for (int k = 0; k < kMaxSplits; ++k) {
-      const int kc = k < a.KS ? k : a.KS - 1;
-      const uint32_t prow = (uint32_t)(kc * split_stride + orow_idx);
-      lse[k] = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(rl, prow * (uint32_t)sizeof(float), 0, kSc1));
-      ov[k] = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                     ro, (prow * D + d4) * (uint32_t)sizeof(float), 0, kSc1));
+    for (int u = 0; u < kMergeRows; ++u) {
+      const int row = min(row0 + u * RPS, r_last);
+      orow_idx[u] = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
+#pragma unroll
+      for (int k = 0; k < kMaxSplits; ++k) {
+        const int kc = k < a.KS ? k : a.KS - 1;
+        const uint32_t prow = (uint32_t)(kc * split_stride + orow_idx[u]);
+        lse[u][k] = __builtin_bit_cast(
+            float,
+            __builtin_amdgcn_raw_buffer_load_b32(rl, prow * (uint32_t)sizeof(float), 0, kSc1));
+        ov[u][k] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       ro, (prow * D + d4) * (uint32_t)sizeof(float), 0, kSc1));
+      }
     }
-    float M = kNegInf;
 #pragma unroll
-    for (int k = 0; k < kMaxSplits; ++k)
-      if (k < a.KS) M = fmaxf(M, lse[k]);
-    f32x4 num = {0.f, 0.f, 0.f, 0.f};
-    float den = 0.f;
+    for (int u = 0; u < kMergeRows; ++u) {
+      if (row0 + u * RPS > r_last) break;
+      float M = kNegInf;
 #pragma unroll
-    for (int k = 0; k < kMaxSplits; ++k) {
-      const float wgt = k < a.KS && lse[k] != kNegInf ? exp2f(lse[k] - M) : 0.f;
-      num += wgt * ov[k];
-      den += wgt;
-    }
-    const float inv = den > 0.f ? 1.f / den : 0.f;
-    if constexpr (CASCADE) {
-      *reinterpret_cast<f32x4*>(a.pre_o + orow_idx * D + d4) = num * inv;
-      if (d4 == 0) a.pre_lse[orow_idx] = den > 0.f ? M + log2f(den) : kNegInf;
-    } else {
-      *reinterpret_cast<f16x4*>(a.out + orow_idx * D + d4) = to16x4<E>(num * inv);
+      for (int k = 0; k < kMaxSplits; ++k)
+        if (k < a.KS) M = fmaxf(M, lse[u][k]);
+      f32x4 num = {0.f, 0.f, 0.f, 0.f};
+      float den = 0.f;
+#pragma unroll
+      for (int k = 0; k < kMaxSplits; ++k) {
+        const float wgt = k < a.KS && lse[u][k] != kNegInf ? exp2f(lse[u][k] - M) : 0.f;
+        num += wgt * ov[u][k];
+        den += wgt;
+      }
+      const float inv = den > 0.f ? 1.f / den : 0.f;
+      if constexpr (CASCADE) {
+        *reinterpret_cast<f32x4*>(a.pre_o + orow_idx[u] * D + d4) = num * inv;
+        if (d4 == 0) a.pre_lse[orow_idx[u]] = den > 0.f ? M + log2f(den) : kNegInf;
+      } else {
+        *reinterpret_cast<f16x4*>(a.out + orow_idx[u] * D + d4) = to16x4<E>(num * inv);
+      }
     }
   }
 }
