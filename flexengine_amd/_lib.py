@@ -67,6 +67,10 @@ SIGNATURES["fe_prefill_paged_planned"] = (
 for _name in ("fe_paged_decode", "fe_paged_decode_planned", "fe_prefill_paged",
               "fe_prefill_paged_planned"):
     SIGNATURES[_name + "_bf16"] = SIGNATURES[_name]
+# and so do the fp32 forms
+for _name in ("fe_write_kv", "fe_write_kv_decode", "fe_write_kv_ragged", "fe_gather_kv",
+              "fe_paged_decode", "fe_prefill_paged"):
+    SIGNATURES[_name + "_f32"] = SIGNATURES[_name]
 SIGNATURES |= {
     # include/flexengine_amd_model.h
     "fe_rmsnorm": (_i, [_p, _i, _p, _p, _p, _p, _i, _i, _f, _p]),

@@ -232,6 +232,160 @@ struct TileCore {
   }
 };
 
+// fp32 tile engine (pools, q and output in fp32), in the 16-bit engines'
+// register layout, so the decode kernel around it -- the cross-wave combine,
+// the split-K partials and their merge -- is the same:
+//   S^T = K . Q^T on v_mfma_f32_16x16x4_f32: lane (g,n) loads dims 16c+4g .. +3
+//     of key n and of column n's query (one 16-byte load per chunk c); MFMA
+//     (c, j) contracts dim 16c + 4g + j in k-slot g.  -> lane (g,n) holds the
+//     scores of column n for keys 4g..4g+3.
+//   O^T += V^T . P^T, MFMA r taking keys 4g + r in k-slot g: A = V[key 4g+r]
+//     [dim 16x+n] (a dword per (r, x); the 16 lanes of a group read a 64-byte
+//     run of one row), B = the lane's probability of key 4g + r.  -> lane (g,n)
+//     accumulates O[col n][16x + 4g + i].
+// Probabilities stay fp32; the online softmax is the 16-bit engines' (base 2,
+// the same rescale slack).  Any block size (a table lookup per key row).
+// Column n accepts keys < limit (decode: tok_end; prefill: its position + 1).
+template <int D>
+struct F32Core {
+  static constexpr int NC = D / 16;  // 16-byte K and q chunks per lane
+  static constexpr int NX = D / 16;  // output tiles of 16 dims
+
+  const float* k_pool;
+  const float* v_pool;
+  const int32_t* trow;  // block-table row of the sequence
+  int64_t rs;           // elements per pool row (kv_heads * D)
+  int hoff;             // kv_head * D
+  int W, NB, BS, bs_log2;
+  int tok_end;          // keys >= tok_end are never read
+  int limit;            // this lane's column accepts keys < limit
+  float scale_log2;
+  // optional fused page write of the decode token (position new_pos)
+  const float* knew_row;
+  const float* vnew_row;
+  float* k_pool_w;
+  float* v_pool_w;
+  int new_pos;          // -1: none
+
+  f32x4 qv[NC];
+  float m_run;
+  float l_run;
+  f32x4 o[NX];
+
+  __device__ __forceinline__ int64_t pool_row(int tok) const {
+    int page = tok >> bs_log2;
+    page = page < W ? page : W - 1;
+    const int blk = clamp_block(trow[page], NB);
+    return (int64_t)blk * BS + (tok & (BS - 1));
+  }
+
+  __device__ __forceinline__ void init_acc() {
+    m_run = kNegInf;
+    l_run = 0.f;
+#pragma unroll
+    for (int x = 0; x < NX; ++x) o[x] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  __device__ __forceinline__ void load_tile(int t, f32x4 (&kk)[NC], float (&vv)[4][NX]) const {
+    const int lane = lane_id();
+    const int g = lane >> 4;
+    const int n = lane & 15;
+    const int t0 = t * kTile;
+    {
+      const int tk = t0 + n;
+      const int64_t off = pool_row(tk < tok_end ? tk : tok_end - 1) * rs + hoff + 4 * g;
+      if (tk == new_pos) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          kk[c] = *reinterpret_cast<const f32x4*>(knew_row + 16 * c + 4 * g);
+          *reinterpret_cast<f32x4*>(k_pool_w + off + 16 * c) = kk[c];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) kk[c] = *reinterpret_cast<const f32x4*>(k_pool + off + 16 * c);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tv = t0 + 4 * g + r;
+      const bool ok = tv < tok_end;
+      const int64_t off = pool_row(ok ? tv : tok_end - 1) * rs + hoff + n;
+      if (tv == new_pos) {
+#pragma unroll
+        for (int x = 0; x < NX; ++x) {
+          vv[r][x] = vnew_row[16 * x + n];
+          v_pool_w[off + 16 * x] = vv[r][x];
+        }
+      } else {
+#pragma unroll
+        for (int x = 0; x < NX; ++x) {
+          const float val = v_pool[off + 16 * x];
+          vv[r][x] = ok ? val : 0.f;
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void compute_tile(int t, const f32x4 (&kk)[NC],
+                                               const float (&vv)[4][NX]) {
+    const int lane = lane_id();
+    const int g = lane >> 4;
+    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sacc = mfma4_f32(kk[c][j], qv[c][j], sacc);
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = t * kTile + 4 * g + i;
+      sv[i] = tok < limit ? sacc[i] * scale_log2 : kNegInf;
+    }
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mx = fmaxf(mx, shfl_xor_f(mx, 16));
+    mx = fmaxf(mx, shfl_xor_f(mx, 32));
+    if (__ballot(mx > m_run + kRescaleSlack)) {  // wave-uniform
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int x = 0; x < NX; ++x) o[x] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == kNegInf ? 0.f : m_run;
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = exp2_fast(sv[i] - m_use);
+    l_run += (p[0] + p[1]) + (p[2] + p[3]);
+#pragma unroll
+    for (int x = 0; x < NX; ++x)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[x] = mfma4_f32(vv[r][x], p[r], o[x]);
+  }
+
+  // Tiles t_first, t_first + step, ... < t_end with one tile of prefetch.
+  __device__ __forceinline__ void run(int t_first, int step, int t_end) {
+    f32x4 ka[NC], kb[NC];
+    float va[4][NX], vb[4][NX];
+    int t = t_first;
+    if (t < t_end) load_tile(t, ka, va);
+    while (t < t_end) {
+      if (t + step < t_end) load_tile(t + step, kb, vb);
+      compute_tile(t, ka, va);
+      t += step;
+      if (t >= t_end) break;
+      if (t + step < t_end) load_tile(t + step, ka, va);
+      compute_tile(t, kb, vb);
+      t += step;
+    }
+  }
+
+  __device__ __forceinline__ float l_total() const {
+    float l = l_run + shfl_xor_f(l_run, 16);
+    return l + shfl_xor_f(l, 32);
+  }
+};
+
 // Fast path for block sizes that are multiples of 16: the 16 keys of a tile
 // share one physical block, so a tile is fully described by wave-uniform
 // values -- the pool row of its first key and its key count.  A wave's tiles

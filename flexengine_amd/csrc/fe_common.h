@@ -118,6 +118,16 @@ __device__ __forceinline__ f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
 // type.
 struct Fp16 {};
 struct Bf16 {};
+// fp32 pools, q and outputs (the decode's F32Core; products on
+// v_mfma_f32_16x16x4_f32, no rounding anywhere but the fp32 arithmetic's own)
+struct F32 {};
+template <class E>
+constexpr bool kIsF32 = __is_same(E, F32);
+// v_mfma_f32_16x16x4_f32: lane l (g = l/16, n = l%16) holds A[row n][k = g] and
+// B[k = g][col n]; C as for the 16-bit MFMAs (C[row 4g+i][col n]).
+__device__ __forceinline__ f32x4 mfma4_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
@@ -154,6 +164,23 @@ __device__ __forceinline__ f16x4 to16x4(float a, float b, float c, float d) {
 template <class E>
 __device__ __forceinline__ f16x4 to16x4(f32x4 v) {
   return to16x4<E>(v[0], v[1], v[2], v[3]);
+}
+// Outputs idx .. idx+3 of element type E from fp32: `out` is the kernels'
+// 16-bit-typed output pointer, which for F32 holds floats (idx counts elements)
+template <class E>
+__device__ __forceinline__ void store_out4(f16* out, int64_t idx, f32x4 v) {
+  if constexpr (kIsF32<E>)
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + idx) = v;
+  else
+    *reinterpret_cast<f16x4*>(out + idx) = to16x4<E>(v);
+}
+// One output element of type E set to x
+template <class E>
+__device__ __forceinline__ void store_out1(f16* out, int64_t idx, float x) {
+  if constexpr (kIsF32<E>)
+    reinterpret_cast<float*>(out)[idx] = x;
+  else
+    out[idx] = to16<E>(x);
 }
 
 __device__ __forceinline__ f16x4 lo4(f16x8 v) { return f16x4{v[0], v[1], v[2], v[3]}; }

@@ -273,3 +273,57 @@ extern "C" int fe_gather_kv(const void* k_pool, const void* v_pool, int num_bloc
                      (f16*)v_out, batch, total_tokens, kv_heads, head_dim, block_size, bs_log2);
   return FE_LAUNCH_STATUS();
 }
+
+// ---- fp32 pools -------------------------------------------------------------
+// The movers above copy 16-byte chunks and never look at the values, so an fp32
+// row of head_dim elements is a 16-bit row of 2 * head_dim: the fp32 forms call
+// them with the widths and strides (given in fp32 elements) doubled.
+
+extern "C" int fe_write_kv_f32(const void* k_new, const void* v_new, int64_t new_token_stride,
+                               void* k_pool, void* v_pool, int num_blocks,
+                               const int32_t* slot_block, const int32_t* slot_offset,
+                               int num_tokens, int kv_heads, int head_dim, int block_size,
+                               fe_stream_t stream) {
+  FE_CHECK_ARG(head_dim > 0 && head_dim % 4 == 0 && head_dim <= (1 << 28) &&
+               new_token_stride % 4 == 0 && new_token_stride >= 0);
+  return fe_write_kv(k_new, v_new, 2 * new_token_stride, k_pool, v_pool, num_blocks, slot_block,
+                     slot_offset, num_tokens, kv_heads, 2 * head_dim, block_size, stream);
+}
+
+extern "C" int fe_write_kv_decode_f32(const void* k_new, const void* v_new,
+                                      int64_t new_batch_stride, void* k_pool, void* v_pool,
+                                      int num_blocks, const int32_t* block_tables,
+                                      int table_stride, const int32_t* context_lens, int batch,
+                                      int kv_heads, int head_dim, int block_size,
+                                      fe_stream_t stream) {
+  FE_CHECK_ARG(head_dim > 0 && head_dim % 4 == 0 && head_dim <= (1 << 28) &&
+               new_batch_stride % 4 == 0 && new_batch_stride >= 0);
+  return fe_write_kv_decode(k_new, v_new, 2 * new_batch_stride, k_pool, v_pool, num_blocks,
+                            block_tables, table_stride, context_lens, batch, kv_heads,
+                            2 * head_dim, block_size, stream);
+}
+
+extern "C" int fe_write_kv_ragged_f32(const void* k_new, const void* v_new,
+                                      int64_t new_token_stride, void* k_pool, void* v_pool,
+                                      int num_blocks, const int32_t* block_tables,
+                                      int table_stride, const int32_t* q_offsets,
+                                      const int32_t* context_lens, int num_seqs,
+                                      int total_tokens, int kv_heads, int head_dim,
+                                      int block_size, fe_stream_t stream) {
+  FE_CHECK_ARG(head_dim > 0 && head_dim % 4 == 0 && head_dim <= (1 << 28) &&
+               new_token_stride % 4 == 0 && new_token_stride >= 0);
+  return fe_write_kv_ragged(k_new, v_new, 2 * new_token_stride, k_pool, v_pool, num_blocks,
+                            block_tables, table_stride, q_offsets, context_lens, num_seqs,
+                            total_tokens, kv_heads, 2 * head_dim, block_size, stream);
+}
+
+extern "C" int fe_gather_kv_f32(const void* k_pool, const void* v_pool, int num_blocks,
+                                const int32_t* block_tables, int table_stride,
+                                const int32_t* context_lens, const int32_t* out_offsets,
+                                void* k_out, void* v_out, int batch, int total_tokens,
+                                int kv_heads, int head_dim, int block_size, fe_stream_t stream) {
+  FE_CHECK_ARG(head_dim > 0 && head_dim % 4 == 0 && head_dim <= (1 << 28));
+  return fe_gather_kv(k_pool, v_pool, num_blocks, block_tables, table_stride, context_lens,
+                      out_offsets, k_out, v_out, batch, total_tokens, kv_heads, 2 * head_dim,
+                      block_size, stream);
+}

@@ -198,8 +198,7 @@ __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, 
       }
     }
     const float inv = 1.f / den;
-    *reinterpret_cast<f16x4*>(a.out + ((int64_t)b * a.Hq + h * G) * D + e4 * 4) =
-        to16x4<E>(num * inv);
+    store_out4<E>(a.out, ((int64_t)b * a.Hq + h * G) * D + e4 * 4, num * inv);
   }
 }
 
@@ -277,7 +276,7 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const DecodeArgs 
 
 template <int D, bool PAGE16, bool PLANNED = false, class E = Fp16>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(PAGE16 ? FE_DECODE_WAVES_PER_EU : 2, 8)))
+__attribute__((amdgpu_waves_per_eu(kIsF32<E> ? 1 : (PAGE16 ? FE_DECODE_WAVES_PER_EU : 2), 8)))
 void piece_decode_kernel(const DecodeArgs a) {
   using C = TileCfg<D>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -312,7 +311,7 @@ void piece_decode_kernel(const DecodeArgs a) {
       if (!ok) {
         if (item < a.B) {
           for (int e = threadIdx.x; e < a.G * D; e += kThreads)
-            a.out[((int64_t)item * a.Hq + h * a.G) * D + e] = to16<E>(__builtin_nanf(""));
+            store_out1<E>(a.out, ((int64_t)item * a.Hq + h * a.G) * D + e, __builtin_nanf(""));
         }
         if (item == 0 && h == 0 && threadIdx.x == 0)
           __hip_atomic_store(a.plan + kPlanDesc - 1, kPlanErrSizes, __ATOMIC_RELAXED,
@@ -340,7 +339,7 @@ void piece_decode_kernel(const DecodeArgs a) {
     const int b = spare_row;
     if (b < a.B && seq_len(a.ctx, b, a.max_len) == 0) {
       for (int e = threadIdx.x; e < a.G * D; e += kThreads)
-        a.out[((int64_t)b * a.Hq + h * a.G) * D + e] = (f16)0.f;
+        store_out1<E>(a.out, ((int64_t)b * a.Hq + h * a.G) * D + e, 0.f);
     }
     return;
   }
@@ -360,6 +359,51 @@ void piece_decode_kernel(const DecodeArgs a) {
   const int t_first = pc.tok_begin / kTile + w;
   const int t_end = (pc.tok_end + kTile - 1) / kTile;
 
+  float m_run, l_tot;
+  f32x4 o[C::NX];
+  if constexpr (kIsF32<E>) {
+    // fp32 pools: the fp32 engine over any block size (no tile lists, no plan)
+    F32Core<D> core;
+    core.k_pool = reinterpret_cast<const float*>(a.k_pool);
+    core.v_pool = reinterpret_cast<const float*>(a.v_pool);
+    core.k_pool_w = reinterpret_cast<float*>(a.k_pool);
+    core.v_pool_w = reinterpret_cast<float*>(a.v_pool);
+    core.trow = a.tables + (int64_t)b * a.W;
+    core.rs = a.Hkv * D;
+    core.hoff = h * D;
+    core.W = a.W;
+    core.NB = a.NB;
+    core.BS = a.BS;
+    core.bs_log2 = a.bs_log2;
+    core.tok_end = pc.tok_end;
+    core.limit = pc.tok_end;
+    core.scale_log2 = a.scale_log2;
+    core.new_pos = -1;
+    core.knew_row = nullptr;
+    core.vnew_row = nullptr;
+    if (a.k_new != nullptr) {
+      const int64_t nr = (int64_t)b * a.new_stride + (int64_t)h * D;
+      core.knew_row = reinterpret_cast<const float*>(a.k_new) + nr;
+      core.vnew_row = reinterpret_cast<const float*>(a.v_new) + nr;
+      core.new_pos = pc.L - 1;
+    }
+    {
+      const int hq = h * G + (n < G ? n : G - 1);
+      const float* qrow =
+          reinterpret_cast<const float*>(a.q) + (int64_t)b * a.q_stride + (int64_t)hq * D;
+#pragma unroll
+      for (int c = 0; c < F32Core<D>::NC; ++c) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(qrow + 16 * c + 4 * g);
+        core.qv[c] = n < G ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    core.init_acc();
+    core.run(t_first, kWaves, t_end);
+    m_run = core.m_run;
+    l_tot = core.l_total();
+#pragma unroll
+    for (int x = 0; x < C::NX; ++x) o[x] = core.o[x];
+  } else {
   f16x8 qv[C::NK];
   {
     const int hq = h * G + (n < G ? n : G - 1);
@@ -370,9 +414,6 @@ void piece_decode_kernel(const DecodeArgs a) {
       qv[s] = n < G ? v : f16x8{};
     }
   }
-
-  float m_run, l_tot;
-  f32x4 o[C::NX];
   if constexpr (PAGE16) {
     // the wave's tiles t_first, t_first + 4, ... of the piece as a tile list
     TileListCore<D, E> core;
@@ -433,6 +474,7 @@ void piece_decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int x = 0; x < C::NX; ++x) o[x] = core.o[x];
   }
+  }
 
   // a sequence with a shared prefix always merges (its prefix part is a partial)
   const bool split = pc.nsplit > 1 || pc.tok0 > 0;
@@ -482,10 +524,9 @@ void piece_decode_kernel(const DecodeArgs a) {
   const int hq = h * G + (n < G ? n : G - 1);
   if (!split) {
     if (n < G) {
-      f16* orow = a.out + ((int64_t)b * a.Hq + hq) * D + 4 * g;
+      const int64_t orow = ((int64_t)b * a.Hq + hq) * D + 4 * g;
 #pragma unroll
-      for (int xi = 0; xi < XW; ++xi)
-        *reinterpret_cast<f16x4*>(orow + 16 * (w * XW + xi)) = to16x4<E>(ox[xi]);
+      for (int xi = 0; xi < XW; ++xi) store_out4<E>(a.out, orow + 16 * (w * XW + xi), ox[xi]);
     }
     return;
   }
@@ -1257,21 +1298,24 @@ BalancedPlan plan_balanced(int batch, int hkv, int G, int block_size, int max_le
 
 template <int D, class E>
 int launch_decode(const DecodeArgs& a, hipStream_t stream) {
-  if (a.nwg > 0) {
-    hipLaunchKernelGGL((balanced_decode_kernel<D, E>), dim3(a.nwg), dim3(kBThreads),
-                       BLds<D>::bytes(a.B, a.G, a.states), stream, a);
-    return FE_LAUNCH_STATUS();
-  }
   const dim3 grid((a.target + 2 * a.B) * a.Hkv);
-  if (a.plan != nullptr)
-    hipLaunchKernelGGL((piece_decode_kernel<D, true, true, E>), grid, dim3(kThreads),
-                       PieceLds<D>::bytes, stream, a);
-  else if (a.BS % kTile == 0)
-    hipLaunchKernelGGL((piece_decode_kernel<D, true, false, E>), grid, dim3(kThreads),
-                       PieceLds<D>::bytes, stream, a);
-  else
+  if constexpr (kIsF32<E>) {
+    // fp32 pools: the fp32 engine, any block size, unplanned
     hipLaunchKernelGGL((piece_decode_kernel<D, false, false, E>), grid, dim3(kThreads),
                        PieceLds<D>::bytes, stream, a);
+  } else if (a.nwg > 0) {
+    hipLaunchKernelGGL((balanced_decode_kernel<D, E>), dim3(a.nwg), dim3(kBThreads),
+                       BLds<D>::bytes(a.B, a.G, a.states), stream, a);
+  } else if (a.plan != nullptr) {
+    hipLaunchKernelGGL((piece_decode_kernel<D, true, true, E>), grid, dim3(kThreads),
+                       PieceLds<D>::bytes, stream, a);
+  } else if (a.BS % kTile == 0) {
+    hipLaunchKernelGGL((piece_decode_kernel<D, true, false, E>), grid, dim3(kThreads),
+                       PieceLds<D>::bytes, stream, a);
+  } else {
+    hipLaunchKernelGGL((piece_decode_kernel<D, false, false, E>), grid, dim3(kThreads),
+                       PieceLds<D>::bytes, stream, a);
+  }
   return FE_LAUNCH_STATUS();
 }
 
@@ -1299,9 +1343,12 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
                 const int32_t* context_lens, void* workspace, size_t workspace_bytes, int batch,
                 int num_q_heads, int kv_heads, int head_dim, int block_size, float scale,
                 int target_splits, CascadePrefix* cascade, hipStream_t stream,
-                void* plan = nullptr, size_t plan_len = 0, bool bf16 = false) {
+                void* plan = nullptr, size_t plan_len = 0, bool bf16 = false,
+                bool f32 = false) {
   FE_CHECK_ARG(batch >= 0 && num_q_heads > 0 && kv_heads > 0 && num_blocks > 0 &&
                table_stride > 0 && target_splits >= 0);
+  // fp32 pools: the unplanned piece kernel only (no plan, no shared prefix)
+  if (f32 && (plan != nullptr || cascade != nullptr)) return FE_ERR_UNSUPPORTED;
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
   FE_CHECK_ARG(num_q_heads % kv_heads == 0);
   const int G = num_q_heads / kv_heads;
@@ -1421,6 +1468,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     a.pre_o = c.pre_o;
     a.pre_lse = c.pre_lse;
   }
+  if (f32) return head_dim == 64 ? launch_decode<64, F32>(a, s) : launch_decode<128, F32>(a, s);
   if (bf16) return head_dim == 64 ? launch_decode<64, Bf16>(a, s) : launch_decode<128, Bf16>(a, s);
   return head_dim == 64 ? launch_decode<64, Fp16>(a, s) : launch_decode<128, Fp16>(a, s);
 }
@@ -1507,6 +1555,20 @@ extern "C" int fe_paged_decode_bf16(const void* q, int64_t q_batch_stride, void*
                      num_blocks, block_tables, table_stride, context_lens, workspace,
                      workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
                      target_splits, nullptr, (hipStream_t)stream, nullptr, 0, true);
+}
+
+extern "C" int fe_paged_decode_f32(const void* q, int64_t q_batch_stride, void* out,
+                                   const void* k_new, const void* v_new,
+                                   int64_t new_batch_stride, void* k_pool, void* v_pool,
+                                   int num_blocks, const int32_t* block_tables, int table_stride,
+                                   const int32_t* context_lens, void* workspace,
+                                   size_t workspace_bytes, int batch, int num_q_heads,
+                                   int kv_heads, int head_dim, int block_size, float scale,
+                                   int target_splits, fe_stream_t stream) {
+  return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
+                     num_blocks, block_tables, table_stride, context_lens, workspace,
+                     workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
+                     target_splits, nullptr, (hipStream_t)stream, nullptr, 0, false, true);
 }
 
 extern "C" int fe_paged_decode_planned_bf16(const void* q, int64_t q_batch_stride, void* out,

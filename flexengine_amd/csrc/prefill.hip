@@ -536,6 +536,73 @@ void prefill_kernel(const PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// prefill_f32_kernel: fp32 pools (fe_prefill_paged_f32)
+// ---------------------------------------------------------------------------
+//
+// The rows of a sequence's KV-head group in the tile kernel's order (row r:
+// token r / G, query head hG + r % G), 16 per wave and 64 per workgroup.  Each
+// wave walks every key tile up to its last row's position on the fp32 engine
+// (F32Core: fp32 products on v_mfma_f32_16x16x4_f32, fp32 softmax), every
+// column masking the keys past its own position, then normalises and stores
+// its 16 rows: no LDS, no key splits.
+template <int D>
+__global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs a) {
+  constexpr int ROWS = kWaves * 16;
+  const int item = blockIdx.x / a.Hkv;
+  const int h = blockIdx.x - item * a.Hkv;
+  RowBlock rb;
+  if (!locate_rows<ROWS, false>(a, item, rb)) return;
+  const int G = a.G;
+  const int lane = lane_id();
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int total_rows = rb.n * G;
+  const int cached = rb.ctx >= rb.n ? rb.ctx - rb.n : 0;
+  const int wr0 = rb.rb * ROWS + 16 * w;
+  if (wr0 >= total_rows) return;
+  const int r_last = min(wr0 + 16, total_rows) - 1;
+  const int row = wr0 + n;
+  const bool valid = row < total_rows;
+  const int rc = valid ? row : r_last;
+
+  F32Core<D> core;
+  core.k_pool = reinterpret_cast<const float*>(a.k_pool);
+  core.v_pool = reinterpret_cast<const float*>(a.v_pool);
+  core.k_pool_w = nullptr;
+  core.v_pool_w = nullptr;
+  core.trow = a.tables + (int64_t)rb.s * a.W;
+  core.rs = a.Hkv * D;
+  core.hoff = h * D;
+  core.W = a.W;
+  core.NB = a.NB;
+  core.BS = a.BS;
+  core.bs_log2 = a.bs_log2;
+  core.tok_end = cached + r_last / G + 1;  // the wave's last row reads the most keys
+  core.limit = valid ? cached + rc / G + 1 : 0;
+  core.scale_log2 = a.scale_log2;
+  core.knew_row = nullptr;
+  core.vnew_row = nullptr;
+  core.new_pos = -1;
+  {
+    const float* qrow = reinterpret_cast<const float*>(a.q) +
+                        (int64_t)(rb.q0 + rc / G) * a.q_stride + (int64_t)(h * G + rc % G) * D;
+#pragma unroll
+    for (int c = 0; c < F32Core<D>::NC; ++c)
+      core.qv[c] = *reinterpret_cast<const f32x4*>(qrow + 16 * c + 4 * g);
+  }
+  core.init_acc();
+  core.run(0, 1, (core.tok_end + kTile - 1) / kTile);
+  const float l = core.l_total();
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (valid) {
+    const int64_t orow = ((int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G) * D + 4 * g;
+#pragma unroll
+    for (int x = 0; x < F32Core<D>::NX; ++x) store_out4<F32>(a.out, orow + 16 * x, core.o[x] * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // prefill_dma_kernel: 32 rows per wave, 64-key blocks staged by buffer->LDS DMA
 // ---------------------------------------------------------------------------
 //
@@ -1674,7 +1741,7 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
                  const int32_t* context_lens, int num_seqs, int total_q, int max_q_len,
                  int num_q_heads, int kv_heads, int head_dim, int block_size, float scale,
                  void* workspace, size_t workspace_bytes, fe_stream_t stream, bool bf16,
-                 void* step_plan = nullptr, size_t plan_bytes = 0) {
+                 void* step_plan = nullptr, size_t plan_bytes = 0, bool f32 = false) {
   FE_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 &&
                kv_heads > 0 && num_blocks > 0 && table_stride > 0);
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
@@ -1687,6 +1754,38 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   if (num_seqs == 0 || total_q == 0) return FE_OK;
   FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && q_offsets && context_lens);
   FE_CHECK_ARG(aligned16(q) && aligned16(out) && aligned16(k_pool) && aligned16(v_pool));
+  if (f32) {
+    // fp32 pools: prefill_f32_kernel, 64 rows per workgroup, no workspace
+    if (step_plan != nullptr) return FE_ERR_UNSUPPORTED;
+    PrefillArgs a{};
+    a.q = (const f16*)q;
+    a.out = (f16*)out;
+    a.k_pool = (const f16*)k_pool;
+    a.v_pool = (const f16*)v_pool;
+    a.tables = block_tables;
+    a.q_off = q_offsets;
+    a.ctx = context_lens;
+    a.q_stride = (int64_t)num_q_heads * head_dim;
+    a.W = table_stride;
+    a.S = num_seqs;
+    a.total_q = total_q;
+    a.Hq = num_q_heads;
+    a.Hkv = kv_heads;
+    a.G = num_q_heads / kv_heads;
+    a.BS = block_size;
+    a.bs_log2 = bs_log2;
+    a.NB = num_blocks;
+    a.KS = 1;
+    a.scale_log2 = scale * kLog2e;
+    const int64_t blocks = ((int64_t)total_q * a.G + kWaves * 16 - 1) / (kWaves * 16) + num_seqs;
+    if (blocks * kv_heads >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
+    const dim3 grid((unsigned)(blocks * kv_heads));
+    if (head_dim == 64)
+      hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    return FE_LAUNCH_STATUS();
+  }
   const int nwg = stream_wgs();
   const bool dma = stream_ok(block_size, table_stride, total_q, num_q_heads / kv_heads, num_seqs,
                              kv_heads, nwg);
@@ -1780,6 +1879,20 @@ extern "C" int fe_prefill_paged_bf16(const void* q, void* out, const void* k_poo
   return prefill_impl(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride, q_offsets,
                       context_lens, num_seqs, total_q, max_q_len, num_q_heads, kv_heads, head_dim,
                       block_size, scale, workspace, workspace_bytes, stream, true);
+}
+
+extern "C" int fe_prefill_paged_f32(const void* q, void* out, const void* k_pool,
+                                    const void* v_pool, int num_blocks,
+                                    const int32_t* block_tables, int table_stride,
+                                    const int32_t* q_offsets, const int32_t* context_lens,
+                                    int num_seqs, int total_q, int max_q_len, int num_q_heads,
+                                    int kv_heads, int head_dim, int block_size, float scale,
+                                    void* workspace, size_t workspace_bytes,
+                                    fe_stream_t stream) {
+  return prefill_impl(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride, q_offsets,
+                      context_lens, num_seqs, total_q, max_q_len, num_q_heads, kv_heads, head_dim,
+                      block_size, scale, workspace, workspace_bytes, stream, false, nullptr, 0,
+                      true);
 }
 
 extern "C" size_t fe_prefill_plan_size(int num_seqs, int total_q, int num_q_heads,

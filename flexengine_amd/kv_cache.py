@@ -31,6 +31,10 @@ The organisation underneath is this package's own:
   slot map computed by numpy from the table row; unlike the reference they
   never synchronise with the device.  The pools must live on a ROCm GPU for
   those two calls; all bookkeeping works anywhere.
+* Pools are float16, bfloat16 or float32 (the reference's own default,
+  allocator.py:26), each with its HIP kernels (the _bf16 / _f32 entry points).
+  The default here is float16 on "cuda:0", the dtype and place the decode path
+  is built around; callers that want the reference's float32 pass it.
 """
 from __future__ import annotations
 
@@ -250,8 +254,9 @@ class _DeviceTables:
 
 class PagedKVCache:
     def __init__(self, layout: CacheLayout, device="cuda:0", dtype=torch.float16, fill=None):
-        if dtype not in (torch.float16, torch.bfloat16):
-            raise ValueError(f"KV pools are float16 or bfloat16 on the HIP kernels; got {dtype}")
+        if dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError(f"KV pools are float16, bfloat16 or float32 on the HIP kernels; "
+                             f"got {dtype}")
         self.layout = layout
         self.device = torch.device(device)
         self.dtype = dtype

@@ -19,9 +19,15 @@ from flexengine_amd import _lib
 
 FP16 = torch.float16
 BF16 = torch.bfloat16
-# K/V element types of the attention entry points (the fe_*_bf16 forms take bf16);
-# the page writes and gathers copy 16-bit elements of either
-KV_DTYPES = (FP16, BF16)
+FP32 = torch.float32
+# K/V element types of the page movers, the decode and the prefill (the fe_*_bf16
+# forms take bf16, the fe_*_f32 forms float32)
+KV_DTYPES = (FP16, BF16, FP32)
+# 16-bit types only: plans, the shared-prefix decode and the LSE merge's output
+DTYPES_16 = (FP16, BF16)
+_SFX = {FP16: "", BF16: "_bf16", FP32: "_f32"}
+# the page movers copy bytes: one form for both 16-bit types, one for fp32
+_MOVER_SFX = {FP16: "", BF16: "", FP32: "_f32"}
 
 
 def _require_gpu(*tensors: torch.Tensor) -> torch.device:
@@ -96,7 +102,8 @@ def write_kv(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_p
     slot_block, slot_offset = _int32(slot_block, "slot_block"), _int32(slot_offset, "slot_offset")
     if slot_block.shape != (t,) or slot_offset.shape != (t,):
         raise ValueError("slot arrays must be [tokens]")
-    _lib.call("fe_write_kv", k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0),
+    _lib.call("fe_write_kv" + _MOVER_SFX[k_pool.dtype], k_new.data_ptr(), v_new.data_ptr(),
+              k_new.stride(0),
               k_pool.data_ptr(), v_pool.data_ptr(), nb, slot_block.data_ptr(),
               slot_offset.data_ptr(), t, hkv, d, bs, _stream(dev))
 
@@ -120,7 +127,8 @@ def write_kv_ragged(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tens
     s = context_lens.shape[0]
     if block_tables.ndim != 2 or block_tables.shape[0] != s or q_offsets.shape != (s + 1,):
         raise ValueError("block_tables must be [S, W], q_offsets [S+1], context_lens [S]")
-    _lib.call("fe_write_kv_ragged", k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0),
+    _lib.call("fe_write_kv_ragged" + _MOVER_SFX[k_pool.dtype], k_new.data_ptr(), v_new.data_ptr(),
+              k_new.stride(0),
               k_pool.data_ptr(), v_pool.data_ptr(), nb, block_tables.data_ptr(),
               block_tables.shape[1], q_offsets.data_ptr(), context_lens.data_ptr(), s,
               k_new.shape[0], hkv, d, bs, _stream(dev))
@@ -159,7 +167,8 @@ def write_kv_decode(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tens
     context_lens = _int32(context_lens, "context_lens")
     if block_tables.ndim != 2 or block_tables.shape[0] != batch or context_lens.shape != (batch,):
         raise ValueError("block_tables must be [batch, W] and context_lens [batch]")
-    _lib.call("fe_write_kv_decode", k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0),
+    _lib.call("fe_write_kv_decode" + _MOVER_SFX[k_pool.dtype], k_new.data_ptr(), v_new.data_ptr(),
+              k_new.stride(0),
               k_pool.data_ptr(), v_pool.data_ptr(), nb, block_tables.data_ptr(),
               block_tables.shape[1], context_lens.data_ptr(), batch, hkv, d, bs, _stream(dev))
 
@@ -178,7 +187,8 @@ def gather_kv(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Te
         raise ValueError("block_tables [batch, W], context_lens [batch], out_offsets [batch+1]")
     k_out = torch.empty((total_tokens, hkv, d), dtype=k_pool.dtype, device=dev)
     v_out = torch.empty_like(k_out)
-    _lib.call("fe_gather_kv", k_pool.data_ptr(), v_pool.data_ptr(), nb, block_tables.data_ptr(),
+    _lib.call("fe_gather_kv" + _MOVER_SFX[k_pool.dtype], k_pool.data_ptr(), v_pool.data_ptr(), nb,
+              block_tables.data_ptr(),
               block_tables.shape[1], context_lens.data_ptr(), out_offsets.data_ptr(),
               k_out.data_ptr(), v_out.data_ptr(), batch, total_tokens, hkv, d, bs, _stream(dev))
     return k_out, v_out
@@ -322,13 +332,13 @@ def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                  plan: DecodePlan | None = None) -> torch.Tensor:
     """Single-token paged decode attention over one layer's pools.
 
-    q [B, Hq, D] fp16 or bf16, the pools' dtype (rows may be strided, heads
-    contiguous); pools [NB, BS, Hkv, D]; block_tables int32 [B, W]; context_lens int32 [B]
-    (0 = inactive row -> zeros).  With k_new/v_new ([B, Hkv, D]) the new token's
-    K/V are written to the pool at position context_lens-1 in the same launch.
-    With `plan` (paged_decode_plan on these block_tables / context_lens) the
-    launch reads the partition and first block rows from it
-    (fe_paged_decode_planned); same results.
+    q [B, Hq, D] fp16, bf16 or float32, the pools' dtype (rows may be strided,
+    heads contiguous); pools [NB, BS, Hkv, D]; block_tables int32 [B, W];
+    context_lens int32 [B] (0 = inactive row -> zeros).  With k_new/v_new
+    ([B, Hkv, D]) the new token's K/V are written to the pool at position
+    context_lens-1 in the same launch.  With `plan` (paged_decode_plan on these
+    block_tables / context_lens; 16-bit pools) the launch reads the partition and
+    first block rows from it (fe_paged_decode_planned); same results.
     """
     (dev, nb, bs, hkv, d, batch, hq, block_tables, context_lens, new_stride, out,
      scale) = _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_new, out)
@@ -340,10 +350,12 @@ def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
             block_tables.shape[1], context_lens.data_ptr(), workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), batch, hq, hkv, d, bs, float(scale),
             int(target_splits))
-    sfx = "_bf16" if q.dtype == BF16 else ""
+    sfx = _SFX[q.dtype]
     if plan is None:
         _lib.call("fe_paged_decode" + sfx, *args, _stream(dev))
         return out
+    if q.dtype not in DTYPES_16:
+        raise ValueError("decode plans are for fp16 / bf16 pools (the fp32 decode has none)")
     shape = (batch, hkv, block_tables.shape[1], bs, nb, int(target_splits))
     if plan.shape != shape or plan.tables_ptr != block_tables.data_ptr() or \
             plan.lens_ptr != context_lens.data_ptr():
@@ -373,6 +385,8 @@ def paged_decode_shared_prefix(q: torch.Tensor, k_pool: torch.Tensor, v_pool: to
     """
     (dev, nb, bs, hkv, d, batch, hq, block_tables, context_lens, new_stride, out,
      scale) = _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_new, out)
+    if q.dtype not in DTYPES_16:
+        raise ValueError("the shared-prefix decode takes fp16 or bf16 pools")
     group_offsets = _int32(group_offsets, "group_offsets")
     group_prefix_lens = _int32(group_prefix_lens, "group_prefix_lens")
     if group_offsets.ndim != 1 or group_prefix_lens.ndim != 1 or \
@@ -401,7 +415,7 @@ def lse_merge(part_out: torch.Tensor, part_lse: torch.Tensor, with_lse: bool = F
               dtype: torch.dtype = FP16) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
     """Merges S split results: part_out fp32 [S, R, D], part_lse fp32 [S, R] (natural log);
     the output [R, D] in `dtype` (float16: fe_lse_merge, bfloat16: fe_lse_merge_bf16)."""
-    if dtype not in KV_DTYPES:
+    if dtype not in DTYPES_16:
         raise ValueError("the merged output is float16 or bfloat16")
     dev = _require_gpu(part_out, part_lse)
     if part_out.ndim != 3 or part_lse.shape != part_out.shape[:2]:
@@ -483,9 +497,9 @@ def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                   plan: PrefillPlan | None = None) -> torch.Tensor:
     """Ragged causal prefill: q [total_q, Hq, D]; sequence s owns rows
     q_offsets[s]:q_offsets[s+1] at positions context_lens[s]-n_s .. context_lens[s]-1.
-    fp16 or bf16 (q, out and the pools alike).  With `plan` (prefill_paged_plan on these q_offsets /
-    context_lens and sizes) the launch reads its work split from it
-    (fe_prefill_paged_planned); same results."""
+    fp16, bf16 or float32 (q, out and the pools alike).  With `plan`
+    (prefill_paged_plan on these q_offsets / context_lens and sizes; 16-bit pools)
+    the launch reads its work split from it (fe_prefill_paged_planned); same results."""
     dev = _require_gpu(q, k_pool, v_pool, block_tables, q_offsets, context_lens, out)
     nb, bs, hkv, d = _check_pool(k_pool, v_pool, KV_DTYPES)
     if q.ndim != 3 or q.shape[2] != d or q.dtype != k_pool.dtype or not q.is_contiguous():
@@ -511,10 +525,12 @@ def prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
             block_tables.data_ptr(), block_tables.shape[1], q_offsets.data_ptr(),
             context_lens.data_ptr(), num_seqs, total_q, int(max_q_len), hq, hkv, d, bs,
             float(scale), ws.data_ptr(), ws.numel())
-    sfx = "_bf16" if q.dtype == BF16 else ""
+    sfx = _SFX[q.dtype]
     if plan is None:
         _lib.call("fe_prefill_paged" + sfx, *args, _stream(dev))
         return out
+    if q.dtype not in DTYPES_16:
+        raise ValueError("prefill plans are for fp16 / bf16 pools (the fp32 prefill has none)")
     shape = (num_seqs, total_q, hq, hkv, block_tables.shape[1], bs)
     if plan.shape != shape or plan.q_offsets_ptr != q_offsets.data_ptr() or \
             plan.lens_ptr != context_lens.data_ptr():

@@ -24,6 +24,8 @@
  *
  * Supported shapes: head_dim in {64, 128}; num_q_heads a multiple of
  * kv_heads with a group size of at most 16; block_size a power of two.
+ * Element types: fp16 (the unsuffixed entry points), bfloat16 (_bf16) and
+ * fp32 (_f32: the KV movers, the decode and the prefill).
  */
 #ifndef FLEXENGINE_AMD_H
 #define FLEXENGINE_AMD_H
@@ -152,6 +154,37 @@ int fe_gather_kv(const void* k_pool, const void* v_pool, int num_blocks,
                  int kv_heads, int head_dim, int block_size, fe_stream_t stream);
 
 /*
+ * fp32 forms of the four KV movers above: the same arguments and byte-exact
+ * results for float32 pools and rows (strides in float32 elements; head_dim a
+ * multiple of 4).  The reference's PagedKVCache defaults to float32
+ * (src/flexengine/engine/kv_cache/allocator.py:26) and the engine builds the
+ * cache in the model's dtype, float32 among them (engine/runtime.py:37-40,
+ * inference/models/qwen2.py:54); its write and materialize
+ * (allocator.py:116-134) move those rows.
+ */
+int fe_write_kv_f32(const void* k_new, const void* v_new, int64_t new_token_stride,
+                    void* k_pool, void* v_pool, int num_blocks,
+                    const int32_t* slot_block, const int32_t* slot_offset,
+                    int num_tokens, int kv_heads, int head_dim, int block_size,
+                    fe_stream_t stream);
+int fe_write_kv_decode_f32(const void* k_new, const void* v_new, int64_t new_batch_stride,
+                           void* k_pool, void* v_pool, int num_blocks,
+                           const int32_t* block_tables, int table_stride,
+                           const int32_t* context_lens, int batch,
+                           int kv_heads, int head_dim, int block_size, fe_stream_t stream);
+int fe_write_kv_ragged_f32(const void* k_new, const void* v_new, int64_t new_token_stride,
+                           void* k_pool, void* v_pool, int num_blocks,
+                           const int32_t* block_tables, int table_stride,
+                           const int32_t* q_offsets, const int32_t* context_lens,
+                           int num_seqs, int total_tokens, int kv_heads, int head_dim,
+                           int block_size, fe_stream_t stream);
+int fe_gather_kv_f32(const void* k_pool, const void* v_pool, int num_blocks,
+                     const int32_t* block_tables, int table_stride,
+                     const int32_t* context_lens, const int32_t* out_offsets,
+                     void* k_out, void* v_out, int batch, int total_tokens,
+                     int kv_heads, int head_dim, int block_size, fe_stream_t stream);
+
+/*
  * Bytes of caller-owned workspace that fe_paged_decode needs for a given
  * batch / head configuration, table capacity (max_context = table_stride *
  * block_size) and split target (0 = library default).
@@ -265,6 +298,25 @@ int fe_paged_decode_planned_bf16(const void* q, int64_t q_batch_stride, void* ou
                                  int batch, int num_q_heads, int kv_heads, int head_dim,
                                  int block_size, float scale, int target_splits,
                                  void* plan, size_t plan_bytes, fe_stream_t stream);
+
+/*
+ * fp32 form of fe_paged_decode: the same arguments (strides in float32
+ * elements) and workspace, with q, out, k_new, v_new and the pools in float32,
+ * any power-of-two block size; fp32 products on v_mfma_f32_16x16x4_f32, fp32
+ * probabilities, softmax and merge -- no rounding below fp32.  Replaces the
+ * reference's Triton decode for the float32 caches it serves
+ * (src/flexengine/inference/kernels/paged_attention.py:99-155, which loads K,
+ * V and q as float32 at :116,126,134).  No plan and no shared-prefix form.
+ */
+int fe_paged_decode_f32(const void* q, int64_t q_batch_stride, void* out,
+                        const void* k_new, const void* v_new, int64_t new_batch_stride,
+                        void* k_pool, void* v_pool, int num_blocks,
+                        const int32_t* block_tables, int table_stride,
+                        const int32_t* context_lens,
+                        void* workspace, size_t workspace_bytes,
+                        int batch, int num_q_heads, int kv_heads, int head_dim,
+                        int block_size, float scale, int target_splits,
+                        fe_stream_t stream);
 
 /*
  * fe_paged_decode without a workspace argument, for callers that cannot
@@ -411,6 +463,25 @@ int fe_prefill_paged_bf16(const void* q, void* out,
                           int num_q_heads, int kv_heads, int head_dim,
                           int block_size, float scale,
                           void* workspace, size_t workspace_bytes, fe_stream_t stream);
+
+/*
+ * fp32 form of fe_prefill_paged: the same arguments and results with q, out
+ * and the pools in float32, any power-of-two block size; fp32 products on
+ * v_mfma_f32_16x16x4_f32 and an fp32 softmax, one wave per 16 (token, query
+ * head) rows over its whole causal key range (no key splits).  The workspace
+ * arguments are accepted and unused (null is allowed).  Replaces the
+ * reference's per-request prefill route on a float32 cache
+ * (src/flexengine/inference/attention/paged.py:27-36: materialize, then
+ * scaled_dot_product_attention in the cache's dtype).
+ */
+int fe_prefill_paged_f32(const void* q, void* out,
+                         const void* k_pool, const void* v_pool, int num_blocks,
+                         const int32_t* block_tables, int table_stride,
+                         const int32_t* q_offsets, const int32_t* context_lens,
+                         int num_seqs, int total_q, int max_q_len,
+                         int num_q_heads, int kv_heads, int head_dim,
+                         int block_size, float scale,
+                         void* workspace, size_t workspace_bytes, fe_stream_t stream);
 
 /*
  * Prefill plan of one model step: the stream-K work split of fe_prefill_paged

@@ -307,3 +307,36 @@ def test_planted_wrong_slot_map_is_caught(monkeypatch):
     R.write_kv(pool_k, pool_k.copy(), [0, 1], 0, a, a, 4)
     with pytest.raises(AssertionError):
         np.testing.assert_array_equal(pool_k[0], a[:4])
+
+
+def test_f32_tolerance_rejects_16_bit_rounding():
+    """The fp32 GPU tests' tolerance (max |err| <= 2e-5, mean <= 2e-6) pinned from both
+    sides on the oracle: a plain float32 evaluation of the same decode stays inside it,
+    while rounding q, K and V to fp16 or bf16 -- what a kernel computing in 16 bits
+    would do -- lands far outside it."""
+    rng = np.random.default_rng(77)
+    b, hq, hkv, d, bs = 3, 8, 2, 64, 16
+    lens = np.array([1000, 37, 4096])
+    width = 4096 // bs
+    tables = np.stack([rng.permutation(3 * width)[:width] for _ in range(b)]).astype(np.int32)
+    kp = rng.standard_normal((3 * width, bs, hkv, d)).astype(np.float32)
+    vp = rng.standard_normal((3 * width, bs, hkv, d)).astype(np.float32)
+    q = rng.standard_normal((b, hq, d)).astype(np.float32)
+    exact = R.decode_reference(q, kp, vp, tables, lens, bs)
+    # float32 arithmetic throughout (numpy float32 matmuls and softmax)
+    g = hq // hkv
+    f32 = np.zeros_like(q)
+    for i in range(b):
+        k = R.materialize(kp, tables[i], int(lens[i]), bs)
+        v = R.materialize(vp, tables[i], int(lens[i]), bs)
+        for h in range(hq):
+            s = (k[:, h // g] @ q[i, h]) * np.float32(1 / math.sqrt(d))
+            p = np.exp(s - s.max())
+            f32[i, h] = (p @ v[:, h // g]) / p.sum()
+    err = np.abs(f32 - exact)
+    assert err.max() <= 2e-5 and err.mean() <= 2e-6, (err.max(), err.mean())
+    for rnd in (lambda x: x.astype(np.float16).astype(np.float32),
+                lambda x: torch.from_numpy(x).to(torch.bfloat16).float().numpy()):
+        r = R.decode_reference(rnd(q), rnd(kp), rnd(vp), tables, lens, bs)
+        err = np.abs(r - exact)
+        assert err.max() > 10 * 2e-5 and err.mean() > 10 * 2e-6, (err.max(), err.mean())
