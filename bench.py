@@ -34,6 +34,9 @@ Also on the line:
 * c5: decode tok/s of the random-init Qwen2.5-1.5B (graph buckets 1, 2, 4 and 8,
   batch 64 eager and as a graph; contexts U{512..4096}), with the HBM bytes per
   step and their fraction of 8 TB/s;
+* f32: C2's decode and C4's prefill on float32 q / K / V (the _f32 entry points;
+  float32 is the reference's default cache dtype), in GB/s and TFLOP/s against
+  8 TB/s and the 157.3 TFLOP/s fp32 MFMA peak;
 * reference_microbench: the reference's kernel microbenchmark shape
   (src/flexengine/research/profiling/kernel.py:14-41: one request of 512 tokens,
   12/2 heads, D 128, per-request attention_for_request, 10 warm-up + 50 timed
@@ -85,6 +88,8 @@ def parse_args(argv=None):
     p.add_argument("--no-c5", action="store_true", help="skip the Qwen2.5-1.5B decode tok/s")
     p.add_argument("--no-c3c4", action="store_true", help="skip the C3 and C4 figures")
     p.add_argument("--c3c4-iters", type=int, default=112)
+    p.add_argument("--no-f32", action="store_true",
+                   help="skip the float32 figures (C2 decode, C4 prefill on the _f32 entry points)")
     p.add_argument("--c5-steps", type=int, default=16)
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                    help="only run a device-to-device copy of MB MiB --steps times (calibrates the "
@@ -277,6 +282,30 @@ def c3_c4(iters: int) -> tuple[dict, dict]:
     return c3, c4
 
 
+def f32_legs(iters: int) -> dict:
+    """C2's decode and C4's prefill on float32 pools (fe_paged_decode_f32,
+    fe_prefill_paged_f32; the reference's default cache dtype), timed as
+    flexengine_amd.bench_attention does.  Not the headline: C2 and C4 are quoted
+    in fp16."""
+    import torch
+
+    from flexengine_amd import bench_attention as BA
+    from flexengine_amd import workloads
+
+    dec = BA.bench_decode("C2", workloads.c2_workload(), iters, 4, dtype=torch.float32)
+    torch.cuda.empty_cache()
+    c4 = BA.bench_c4(iters, 4, torch.float32)
+    torch.cuda.empty_cache()
+    return {
+        "c2_decode": {k: dec[k] for k in ("us_per_call", "bytes", "GB_s", "pct_hbm_peak")},
+        "c4_prefill": {"us_per_call": c4["prefill_us"], "TFLOP_s": c4["prefill_TFLOP_s"],
+                       "pct_mfma_fp32_peak": c4["pct_mfma_fp32_peak"]},
+        "c4_decode_rows": {"us_per_call": c4["decode_us"], "GB_s": c4["decode_GB_s"]},
+        "workload": "C2 and C4 with float32 q / K / V / out (unplanned; 4 bytes per element; "
+                    "prefill against the 157.3 TFLOP/s fp32 MFMA peak)",
+    }
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -400,6 +429,10 @@ def main(argv=None) -> int:
     if c3 is not None:
         _progress(f"C3 plain {c3['plain']['us_per_call']} us, cascade {c3['cascade']['us_per_call']} us;"
                   f" C4 prefill {c4['prefill_planned_us']} us planned, decode {c4['decode_us']} us")
+    f32 = None if args.no_f32 else f32_legs(args.c3c4_iters)
+    if f32 is not None:
+        _progress(f"fp32: C2 decode {f32['c2_decode']['us_per_call']} us, "
+                  f"C4 prefill {f32['c4_prefill']['us_per_call']} us")
     c5 = None if args.no_c5 else c5_decode(args.c5_steps)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 
@@ -453,6 +486,7 @@ def main(argv=None) -> int:
         "c3": c3,
         "c4": c4,
         "c5": c5,
+        "f32": f32,
         "reference_microbench": micro,
         "cpu_baseline": cpu,
     }

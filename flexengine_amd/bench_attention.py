@@ -17,7 +17,10 @@ stream -- and prints one JSON line per config:
   the 48 decode rows in GB/s, and the whole step.
 
 Calls are replayed from a HIP graph, so each figure is GPU time per call.
-`--dtype bf16` runs the bf16 entry points on the same values rounded to bf16.
+`--dtype bf16` runs the bf16 entry points on the same values rounded to bf16;
+`--dtype f32` the fp32 entry points on the values widened to float32 (bytes at
+4 per element, the C4 prefill against the 157.3 TFLOP/s fp32 MFMA peak; no plan
+and no shared-prefix form).
 """
 from __future__ import annotations
 
@@ -32,6 +35,7 @@ from flexengine_amd import ops, workloads
 HBM_PEAK = 8.0e12
 LAYERS = 28  # Qwen2.5-1.5B: calls per model step that share one plan
 MFMA_FP16_PEAK = 2.5e15
+MFMA_FP32_PEAK = 157.3e12
 
 
 def _timed(fn, iters: int, variants: int) -> float:
@@ -95,7 +99,7 @@ def bench_decode(name: str, w, iters: int, copies: int, unique_bytes: int | None
             ops.paged_decode(d.q, kp, vp, d.block_tables, d.context_lens, out=out)
 
     sec = _timed(step, iters, len(pools))
-    logical = w.algorithmic_bytes(logical=True)
+    logical = d.algorithmic_bytes(logical=True)
     kernel = "fe_paged_decode_shared_prefix" if shared_prefix else "fe_paged_decode"
     res = {"config": name, "kernel": kernel, "us_per_call": round(sec * 1e6, 2),
            "batch": w.batch, "context_tokens": int(w.context_lens.sum()),
@@ -120,9 +124,12 @@ def bench_c4(iters: int, copies: int, dtype=torch.float16) -> dict:
         ops.prefill_paged(d.q, kp, vp, d.block_tables, d.q_offsets, d.context_lens, max_q, out=out)
 
     # one plan per model step of 28 layers (fe_prefill_plan), charged 1/28 per call
+    # (16-bit pools: the fp32 prefill has no plan)
     hq, hkv = d.q.shape[1], d.k_pool.shape[2]
-    plan = ops.prefill_paged_plan(d.q_offsets, d.context_lens, d.q.shape[0], hq, hkv,
-                                  d.block_tables.shape[1], d.k_pool.shape[1])
+    plan = None
+    if dtype != torch.float32:
+        plan = ops.prefill_paged_plan(d.q_offsets, d.context_lens, d.q.shape[0], hq, hkv,
+                                      d.block_tables.shape[1], d.k_pool.shape[1])
 
     def prefill_planned(i):
         kp, vp = pools[i % len(pools)]
@@ -162,13 +169,16 @@ def bench_c4(iters: int, copies: int, dtype=torch.float16) -> dict:
     t_all = _timed(both, iters, len(pools))
     t_ovl = _timed(both_overlapped, iters, len(pools))
     flops = w.flops()
-    dbytes = w.decode.algorithmic_bytes()
+    dbytes = d.decode.algorithmic_bytes()
+    # the MFMA peak of the arithmetic type: fp16 / bf16 (same dense rate) or fp32
+    f32 = dtype == torch.float32
+    peak, tag = (MFMA_FP32_PEAK, "fp32") if f32 else (MFMA_FP16_PEAK, "fp16")
     return {"config": "C4", "prefill_us": round(t_pre * 1e6, 2), "prefill_flops": flops,
             "prefill_TFLOP_s": round(flops / t_pre / 1e12, 1),
-            "pct_mfma_fp16_peak": round(100 * flops / t_pre / MFMA_FP16_PEAK, 2),
+            f"pct_mfma_{tag}_peak": round(100 * flops / t_pre / peak, 2),
             "prefill_planned_us": None if t_plan is None else round(t_plan * 1e6, 2),
-            "pct_mfma_fp16_peak_planned":
-                None if t_plan is None else round(100 * flops / t_plan / MFMA_FP16_PEAK, 2),
+            f"pct_mfma_{tag}_peak_planned":
+                None if t_plan is None else round(100 * flops / t_plan / peak, 2),
             "decode_us": round(t_dec * 1e6, 2), "decode_bytes": dbytes,
             "decode_GB_s": round(dbytes / t_dec / 1e9, 1), "step_us": round(t_all * 1e6, 2),
             "step_overlap_us": round(t_ovl * 1e6, 2),
@@ -180,9 +190,9 @@ def main(argv=None) -> int:
     p.add_argument("--iters", type=int, default=200)
     p.add_argument("--copies", type=int, default=4, help="rotating KV pool copies")
     p.add_argument("--configs", default="c1,c3,c4")
-    p.add_argument("--dtype", choices=("f16", "bf16"), default="f16")
+    p.add_argument("--dtype", choices=("f16", "bf16", "f32"), default="f16")
     args = p.parse_args(argv)
-    dt = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    dt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[args.dtype]
     if not torch.cuda.is_available():
         print("bench_attention needs a ROCm GPU", file=sys.stderr)
         return 2
@@ -194,12 +204,14 @@ def main(argv=None) -> int:
         w = workloads.c3_workload()
         hkv, d = w.k_pool.shape[2], w.k_pool.shape[3]
         # compulsory bytes: every distinct K/V row once, plus q and out
-        unique = w.unique_tokens * 2 * hkv * d * 2 + 2 * w.q.numel() * 2
+        size = torch.tensor([], dtype=dt).element_size()
+        unique = w.unique_tokens * 2 * hkv * d * size + 2 * w.q.numel() * size
         print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique, dtype=dt)
                          | {"dtype": args.dtype}), flush=True)
-        print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique,
-                                      shared_prefix=True, dtype=dt) | {"dtype": args.dtype}),
-              flush=True)
+        if dt != torch.float32:  # the shared-prefix decode takes 16-bit pools
+            print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique,
+                                          shared_prefix=True, dtype=dt) | {"dtype": args.dtype}),
+                  flush=True)
     if "c4" in cfgs:
         print(json.dumps(bench_c4(args.iters, args.copies, dt) | {"dtype": args.dtype}),
               flush=True)

@@ -244,9 +244,11 @@ struct TileCore {
 //     run of one row), B = the lane's probability of key 4g + r.  -> lane (g,n)
 //     accumulates O[col n][16x + 4g + i].
 // Probabilities stay fp32; the online softmax is the 16-bit engines' (base 2,
-// the same rescale slack).  Any block size (a table lookup per key row).
-// Column n accepts keys < limit (decode: tok_end; prefill: its position + 1).
-template <int D>
+// the same rescale slack).  Any block size: a table lookup per key row, or
+// (LIST, block sizes that are multiples of 16) the wave's tile rows held one
+// per lane.  Column n accepts keys < limit (decode: tok_end; prefill: its
+// position + 1).
+template <int D, bool LIST = false>
 struct F32Core {
   static constexpr int NC = D / 16;  // 16-byte K and q chunks per lane
   static constexpr int NX = D / 16;  // output tiles of 16 dims
@@ -266,6 +268,12 @@ struct F32Core {
   float* k_pool_w;
   float* v_pool_w;
   int new_pos;          // -1: none
+  // the wave's tiles: t_first, t_first + step, ... (LIST: block sizes that are
+  // multiples of 16, so a tile's 16 keys are consecutive rows of one block;
+  // lane j of row_vec holds the pool row of the first key of tile list_base + j,
+  // refilled every 64 tiles, so no table load sits between two tiles' loads)
+  int t_first, step;
+  int row_vec, list_base;
 
   f32x4 qv[NC];
   float m_run;
@@ -278,6 +286,19 @@ struct F32Core {
     const int blk = clamp_block(trow[page], NB);
     return (int64_t)blk * BS + (tok & (BS - 1));
   }
+  // LIST: the pool rows of tiles k0 .. k0 + 63 of the wave's list
+  __device__ __forceinline__ void fill_list(int k0) {
+    list_base = k0;
+    row_vec = (int)pool_row((t_first + (k0 + lane_id()) * step) * kTile);
+  }
+  // Pool row of key t0 + r of the wave's k-th tile (key clamped below tok_end).
+  __device__ __forceinline__ int64_t key_row(int k, int t0, int r) const {
+    const int tok = t0 + r < tok_end ? t0 + r : tok_end - 1;
+    if constexpr (LIST)
+      return (int64_t)__builtin_amdgcn_readlane(row_vec, k - list_base) + (tok - t0);
+    else
+      return pool_row(tok);
+  }
 
   __device__ __forceinline__ void init_acc() {
     m_run = kNegInf;
@@ -286,14 +307,17 @@ struct F32Core {
     for (int x = 0; x < NX; ++x) o[x] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  __device__ __forceinline__ void load_tile(int t, f32x4 (&kk)[NC], float (&vv)[4][NX]) const {
+  __device__ __forceinline__ void load_tile(int k, f32x4 (&kk)[NC], float (&vv)[4][NX]) {
     const int lane = lane_id();
     const int g = lane >> 4;
     const int n = lane & 15;
-    const int t0 = t * kTile;
+    if constexpr (LIST) {
+      if (k - list_base >= kWave) fill_list(k);  // wave-uniform
+    }
+    const int t0 = (t_first + k * step) * kTile;
     {
       const int tk = t0 + n;
-      const int64_t off = pool_row(tk < tok_end ? tk : tok_end - 1) * rs + hoff + 4 * g;
+      const int64_t off = key_row(k, t0, n) * rs + hoff + 4 * g;
       if (tk == new_pos) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -309,7 +333,7 @@ struct F32Core {
     for (int r = 0; r < 4; ++r) {
       const int tv = t0 + 4 * g + r;
       const bool ok = tv < tok_end;
-      const int64_t off = pool_row(ok ? tv : tok_end - 1) * rs + hoff + n;
+      const int64_t off = key_row(k, t0, 4 * g + r) * rs + hoff + n;
       if (tv == new_pos) {
 #pragma unroll
         for (int x = 0; x < NX; ++x) {
@@ -326,10 +350,11 @@ struct F32Core {
     }
   }
 
-  __device__ __forceinline__ void compute_tile(int t, const f32x4 (&kk)[NC],
+  __device__ __forceinline__ void compute_tile(int k, const f32x4 (&kk)[NC],
                                                const float (&vv)[4][NX]) {
     const int lane = lane_id();
     const int g = lane >> 4;
+    const int t0 = (t_first + k * step) * kTile;
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NC; ++c)
@@ -338,7 +363,7 @@ struct F32Core {
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int tok = t * kTile + 4 * g + i;
+      const int tok = t0 + 4 * g + i;
       sv[i] = tok < limit ? sacc[i] * scale_log2 : kNegInf;
     }
     float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
@@ -363,20 +388,24 @@ struct F32Core {
       for (int r = 0; r < 4; ++r) o[x] = mfma4_f32(vv[r][x], p[r], o[x]);
   }
 
-  // Tiles t_first, t_first + step, ... < t_end with one tile of prefetch.
-  __device__ __forceinline__ void run(int t_first, int step, int t_end) {
+  // The wave's tiles t_first, t_first + step, ... below t_end, one tile of
+  // prefetch: while tile k is computed, the loads of tile k + 1 are in flight.
+  __device__ __forceinline__ void run(int first, int stride, int t_end) {
+    t_first = first;
+    step = stride;
+    const int ntiles = first < t_end ? (t_end - first + stride - 1) / stride : 0;
+    if (ntiles == 0) return;
+    if constexpr (LIST) fill_list(0);
     f32x4 ka[NC], kb[NC];
     float va[4][NX], vb[4][NX];
-    int t = t_first;
-    if (t < t_end) load_tile(t, ka, va);
-    while (t < t_end) {
-      if (t + step < t_end) load_tile(t + step, kb, vb);
-      compute_tile(t, ka, va);
-      t += step;
-      if (t >= t_end) break;
-      if (t + step < t_end) load_tile(t + step, ka, va);
-      compute_tile(t, kb, vb);
-      t += step;
+    load_tile(0, ka, va);
+    for (int k = 0;; k += 2) {
+      if (k + 1 < ntiles) load_tile(k + 1, kb, vb);
+      compute_tile(k, ka, va);
+      if (k + 1 >= ntiles) break;
+      if (k + 2 < ntiles) load_tile(k + 2, ka, va);
+      compute_tile(k + 1, kb, vb);
+      if (k + 2 >= ntiles) break;
     }
   }
 

@@ -362,8 +362,9 @@ void piece_decode_kernel(const DecodeArgs a) {
   float m_run, l_tot;
   f32x4 o[C::NX];
   if constexpr (kIsF32<E>) {
-    // fp32 pools: the fp32 engine over any block size (no tile lists, no plan)
-    F32Core<D> core;
+    // fp32 pools: the fp32 engine (tile lists for block sizes that are multiples
+    // of 16, a table lookup per key row otherwise; no plan)
+    F32Core<D, PAGE16> core;
     core.k_pool = reinterpret_cast<const float*>(a.k_pool);
     core.v_pool = reinterpret_cast<const float*>(a.v_pool);
     core.k_pool_w = reinterpret_cast<float*>(a.k_pool);
@@ -392,7 +393,7 @@ void piece_decode_kernel(const DecodeArgs a) {
       const float* qrow =
           reinterpret_cast<const float*>(a.q) + (int64_t)b * a.q_stride + (int64_t)hq * D;
 #pragma unroll
-      for (int c = 0; c < F32Core<D>::NC; ++c) {
+      for (int c = 0; c < F32Core<D, PAGE16>::NC; ++c) {
         const f32x4 v = *reinterpret_cast<const f32x4*>(qrow + 16 * c + 4 * g);
         core.qv[c] = n < G ? v : f32x4{0.f, 0.f, 0.f, 0.f};
       }
@@ -1300,9 +1301,13 @@ template <int D, class E>
 int launch_decode(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid((a.target + 2 * a.B) * a.Hkv);
   if constexpr (kIsF32<E>) {
-    // fp32 pools: the fp32 engine, any block size, unplanned
-    hipLaunchKernelGGL((piece_decode_kernel<D, false, false, E>), grid, dim3(kThreads),
-                       PieceLds<D>::bytes, stream, a);
+    // fp32 pools: the fp32 engine, unplanned
+    if (a.BS % kTile == 0)
+      hipLaunchKernelGGL((piece_decode_kernel<D, true, false, E>), grid, dim3(kThreads),
+                         PieceLds<D>::bytes, stream, a);
+    else
+      hipLaunchKernelGGL((piece_decode_kernel<D, false, false, E>), grid, dim3(kThreads),
+                         PieceLds<D>::bytes, stream, a);
   } else if (a.nwg > 0) {
     hipLaunchKernelGGL((balanced_decode_kernel<D, E>), dim3(a.nwg), dim3(kBThreads),
                        BLds<D>::bytes(a.B, a.G, a.states), stream, a);

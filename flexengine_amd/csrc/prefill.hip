@@ -545,7 +545,7 @@ void prefill_kernel(const PrefillArgs a) {
 // (F32Core: fp32 products on v_mfma_f32_16x16x4_f32, fp32 softmax), every
 // column masking the keys past its own position, then normalises and stores
 // its 16 rows: no LDS, no key splits.
-template <int D>
+template <int D, bool LIST>
 __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs a) {
   constexpr int ROWS = kWaves * 16;
   const int item = blockIdx.x / a.Hkv;
@@ -566,7 +566,7 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs
   const bool valid = row < total_rows;
   const int rc = valid ? row : r_last;
 
-  F32Core<D> core;
+  F32Core<D, LIST> core;
   core.k_pool = reinterpret_cast<const float*>(a.k_pool);
   core.v_pool = reinterpret_cast<const float*>(a.v_pool);
   core.k_pool_w = nullptr;
@@ -588,7 +588,7 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs
     const float* qrow = reinterpret_cast<const float*>(a.q) +
                         (int64_t)(rb.q0 + rc / G) * a.q_stride + (int64_t)(h * G + rc % G) * D;
 #pragma unroll
-    for (int c = 0; c < F32Core<D>::NC; ++c)
+    for (int c = 0; c < F32Core<D, LIST>::NC; ++c)
       core.qv[c] = *reinterpret_cast<const f32x4*>(qrow + 16 * c + 4 * g);
   }
   core.init_acc();
@@ -598,7 +598,8 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs
   if (valid) {
     const int64_t orow = ((int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G) * D + 4 * g;
 #pragma unroll
-    for (int x = 0; x < F32Core<D>::NX; ++x) store_out4<F32>(a.out, orow + 16 * x, core.o[x] * inv);
+    for (int x = 0; x < F32Core<D, LIST>::NX; ++x)
+      store_out4<F32>(a.out, orow + 16 * x, core.o[x] * inv);
   }
 }
 
@@ -1780,10 +1781,16 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
     const int64_t blocks = ((int64_t)total_q * a.G + kWaves * 16 - 1) / (kWaves * 16) + num_seqs;
     if (blocks * kv_heads >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
     const dim3 grid((unsigned)(blocks * kv_heads));
-    if (head_dim == 64)
-      hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    const hipStream_t s = (hipStream_t)stream;
+    const bool list = block_size % kTile == 0;  // tile rows held per lane
+    if (head_dim == 64 && list)
+      hipLaunchKernelGGL((prefill_f32_kernel<64, true>), grid, dim3(kThreads), 0, s, a);
+    else if (head_dim == 64)
+      hipLaunchKernelGGL((prefill_f32_kernel<64, false>), grid, dim3(kThreads), 0, s, a);
+    else if (list)
+      hipLaunchKernelGGL((prefill_f32_kernel<128, true>), grid, dim3(kThreads), 0, s, a);
     else
-      hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+      hipLaunchKernelGGL((prefill_f32_kernel<128, false>), grid, dim3(kThreads), 0, s, a);
     return FE_LAUNCH_STATUS();
   }
   const int nwg = stream_wgs();

@@ -47,9 +47,9 @@ class DecodeWorkload:
                               mv(self.v_new), self.unique_tokens, dict(self.meta))
 
     def kv_row_bytes(self) -> int:
-        """Bytes of K plus V for one token of one layer (2 * Hkv * D * 2)."""
+        """Bytes of K plus V for one token of one layer (2 * Hkv * D * element size)."""
         _, _, hkv, d = self.k_pool.shape
-        return 2 * hkv * d * 2
+        return 2 * hkv * d * self.k_pool.element_size()
 
     def algorithmic_bytes(self, logical: bool = False) -> int:
         """Compulsory HBM bytes of one decode call.
@@ -63,7 +63,7 @@ class DecodeWorkload:
         tokens = int(ctx.sum()) if (logical or not self.unique_tokens) else self.unique_tokens
         b, hq, d = self.q.shape
         nbytes = tokens * self.kv_row_bytes()
-        nbytes += 2 * b * hq * d * 2                      # q in, out
+        nbytes += 2 * b * hq * d * self.q.element_size()  # q in, out
         pages = int(((ctx + self.block_size - 1) // self.block_size).sum())
         nbytes += 4 * pages + 4 * b                         # table entries + lengths
         if self.k_new is not None:
