@@ -5,6 +5,11 @@ Usage: python -m flexengine_amd.build   (or flexengine_amd.build.build())
 Each csrc/*.hip file is compiled to an object with hipcc, in parallel, then
 linked into flexengine_amd/libfe_paged.so.  The library is always rebuilt:
 this is the "does it build" check as well as the build.
+
+`python -m flexengine_amd.build --timeline` builds the diagnostic variant
+libfe_paged_timeline.so instead (FE_TIMELINE: per-workgroup phase stamps of the
+decode kernel, read by flexengine_amd/timeline_c2.py); the product library is
+not touched.
 """
 from __future__ import annotations
 
@@ -43,8 +48,12 @@ def hipcc() -> str:
     return exe
 
 
-def _compile(src: Path, obj: Path, verbose: bool) -> None:
-    cmd = [hipcc(), *HIP_FLAGS, "-I", str(INCLUDE_DIR), "-I", str(CSRC_DIR), "-c", str(src), "-o", str(obj)]
+TIMELINE_LIB_PATH = PKG_DIR / "libfe_paged_timeline.so"
+
+
+def _compile(src: Path, obj: Path, verbose: bool, defines: tuple = ()) -> None:
+    cmd = [hipcc(), *HIP_FLAGS, *defines, "-I", str(INCLUDE_DIR), "-I", str(CSRC_DIR), "-c",
+           str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -56,24 +65,26 @@ def _compile(src: Path, obj: Path, verbose: bool) -> None:
         print(msg, file=sys.stderr)
 
 
-def build(verbose: bool = False) -> Path:
+def build(verbose: bool = False, timeline: bool = False) -> Path:
     sources = sorted(CSRC_DIR.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+    target = TIMELINE_LIB_PATH if timeline else LIB_PATH
+    defines = ("-DFE_TIMELINE",) if timeline else ()
     with tempfile.TemporaryDirectory(prefix="fe_build_") as tmp:
         objs = [Path(tmp) / (s.stem + ".o") for s in sources]
         workers = min(len(sources), max(1, (os.cpu_count() or 2) // 2), 8)
         with ThreadPoolExecutor(max_workers=workers) as pool:
-            list(pool.map(lambda so: _compile(so[0], so[1], verbose), zip(sources, objs)))
-        tmp_lib = PKG_DIR / (LIB_NAME + ".tmp")
+            list(pool.map(lambda so: _compile(so[0], so[1], verbose, defines), zip(sources, objs)))
+        tmp_lib = PKG_DIR / (target.name + ".tmp")
         cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp_lib)]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
-            raise RuntimeError(f"link of {LIB_NAME} failed:\n{res.stderr}")
-        os.replace(tmp_lib, LIB_PATH)
-    return LIB_PATH
+            raise RuntimeError(f"link of {target.name} failed:\n{res.stderr}")
+        os.replace(tmp_lib, target)
+    return target
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build(verbose="-v" in sys.argv, timeline="--timeline" in sys.argv)
     print(path)

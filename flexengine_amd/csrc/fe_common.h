@@ -30,6 +30,21 @@ __device__ __forceinline__ int readlane_i(int v, int lane) {
   return __builtin_amdgcn_readlane(v, lane);
 }
 
+// splitmix64's finaliser (S. Vigna, public domain); the host folds the fields a
+// step plan is tied to through it, so a planned launch checks its plan with one
+// two-word compare (plan_key)
+inline uint64_t mix64(uint64_t z) {
+  z += 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+inline uint64_t plan_key(const uint64_t* f, int n) {
+  uint64_t h = 0;
+  for (int i = 0; i < n; ++i) h = mix64(h ^ f[i]);
+  return h;
+}
+
 // the two 32-bit halves of an address (plan descriptors record their inputs' addresses)
 __device__ __forceinline__ int lo32(const void* p) { return (int)(uint32_t)(uintptr_t)p; }
 __device__ __forceinline__ int hi32(const void* p) { return (int)(uint32_t)((uintptr_t)p >> 32); }

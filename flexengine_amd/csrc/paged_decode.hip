@@ -32,6 +32,30 @@
 
 #include "attn_core.h"
 
+// Diagnostic build only (python -m flexengine_amd.build --timeline, which
+// defines FE_TIMELINE and writes libfe_paged_timeline.so): thread 0 of every
+// piece_decode_kernel workgroup records s_memrealtime stamps (100 MHz) of its
+// phases into fe_tl_stamps, read back by flexengine_amd/timeline_c2.py.  The
+// product library compiles the marks to nothing.
+#ifdef FE_TIMELINE
+constexpr int kTlWgs = 4096;
+constexpr int kTlSlots = 16;
+__device__ unsigned long long fe_tl_stamps[kTlWgs * kTlSlots];
+#define FE_TL_SET(slot, v)                                                     \
+  do {                                                                         \
+    if (threadIdx.x == 0 && blockIdx.x < kTlWgs)                               \
+      fe_tl_stamps[blockIdx.x * kTlSlots + (slot)] = (unsigned long long)(v);  \
+  } while (0)
+#define FE_TL_MARK(slot) FE_TL_SET(slot, __builtin_amdgcn_s_memrealtime())
+#else
+#define FE_TL_SET(slot, v) \
+  do {                     \
+  } while (0)
+#define FE_TL_MARK(slot) \
+  do {                   \
+  } while (0)
+#endif
+
 using namespace fe;
 
 namespace {
@@ -92,21 +116,23 @@ struct DecodeArgs {
   // [kPlanHdr ints], then per item, wave and lane the pool row of the lane's
   // tile; null for the unplanned decode
   int* plan;
+  uint32_t plan_key_lo, plan_key_hi;  // plan_key() of the call's sizes and tensors
 };
 
-// The decode plan of one step: a descriptor of kPlanDesc ints -- kPlanMagic,
-// then the sizes it was computed for (batch, kv_heads, table width, block
-// size, num_blocks, target) and an error word the planned decode sets -- then,
-// for items = target + 2 * batch (the grid of the piece kernel over kv_heads),
-// a descriptor of the sizes and tables it was computed for (kPlanDesc words:
-// magic, batch, kv heads, table stride, block size, pool blocks, target, the
-// block-table and context-length addresses, zero padding, and last the error
-// word the planned kernel sets: kPlanErrSizes, kPlanErrStale), a header per item -- the Piece fields b, id, split, nsplit, L, tok0,
-// tok_begin, tok_end; b = -1 for an item without a piece, whose id field is
-// then the row it zero-fills when inactive -- and the tile list of each of its
-// four waves (lane k: pool row of tile k).
+// The decode plan of one step, for items = target + 2 * batch (the grid of the
+// piece kernel over kv_heads):
+// * a descriptor of kPlanDesc ints: the 64-bit plan_key() of the sizes and
+//   tensors it was computed for (the word pair a planned call compares), the
+//   same fields in the clear for inspection (magic, batch, kv heads, table
+//   stride, block size, pool blocks, target, the block-table and
+//   context-length addresses), zero padding, and last the error word the
+//   planned kernel sets (kPlanErrSizes, kPlanErrStale);
+// * a header per item -- the Piece fields b, id, split, nsplit, L, tok0,
+//   tok_begin, tok_end; b = -1 for an item without a piece, whose id field is
+//   then the row it zero-fills when inactive;
+// * the tile list of each item's four waves (lane k: pool row of tile k).
 constexpr int kPlanDesc = 16;
-constexpr int kPlanCheck = 11;          // descriptor words a planned call compares
+constexpr int kPlanFields = 13;         // key (2 words) + the fields in the clear
 constexpr int kPlanHdr = 8;
 constexpr int kPlanMagic = 0x46504450;  // "PDPF"
 constexpr int kPlanErrSizes = 1;        // error word: the call's sizes are not the plan's
@@ -115,6 +141,15 @@ static_assert((kPlanDesc - 1) * 4 == FE_DECODE_PLAN_ERROR_OFFSET &&
               kPlanErrSizes == FE_PLAN_ERR_SIZES && kPlanErrStale == FE_PLAN_ERR_STALE);
 inline size_t plan_bytes(int items) {
   return ((size_t)kPlanDesc + (size_t)items * (kPlanHdr + kWaves * kWave)) * sizeof(int32_t);
+}
+// The key of the fields a plan is tied to (computed on the host).
+inline void set_plan_key(DecodeArgs& a) {
+  const uint64_t f[] = {(uint64_t)kPlanMagic, (uint64_t)a.B, (uint64_t)a.Hkv, (uint64_t)a.W,
+                        (uint64_t)a.BS, (uint64_t)a.NB, (uint64_t)a.target,
+                        (uint64_t)(uintptr_t)a.tables, (uint64_t)(uintptr_t)a.ctx};
+  const uint64_t h = plan_key(f, (int)(sizeof(f) / sizeof(f[0])));
+  a.plan_key_lo = (uint32_t)h;
+  a.plan_key_hi = (uint32_t)(h >> 32);
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -247,11 +282,12 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const DecodeArgs 
   const int item = blockIdx.x;
   const int items = a.target + 2 * a.B;
   if (item == 0 && threadIdx.x < kPlanDesc) {
-    const int desc[kPlanCheck] = {kPlanMagic, a.B, a.Hkv, a.W, a.BS, a.NB, a.target,
-                                  lo32(a.tables), hi32(a.tables), lo32(a.ctx), hi32(a.ctx)};
+    const int desc[kPlanFields] = {(int)a.plan_key_lo, (int)a.plan_key_hi, kPlanMagic, a.B,
+                                   a.Hkv, a.W, a.BS, a.NB, a.target, lo32(a.tables),
+                                   hi32(a.tables), lo32(a.ctx), hi32(a.ctx)};
     int v = 0;  // padding and the error word
 #pragma unroll
-    for (int i = 0; i < kPlanCheck; ++i) v = (int)threadIdx.x == i ? desc[i] : v;
+    for (int i = 0; i < kPlanFields; ++i) v = (int)threadIdx.x == i ? desc[i] : v;
     a.plan[threadIdx.x] = v;
   }
   Piece pc;
@@ -281,6 +317,7 @@ void piece_decode_kernel(const DecodeArgs a) {
   using C = TileCfg<D>;
   extern __shared__ __align__(16) unsigned char smem[];
 
+  FE_TL_MARK(0);  // start
   const int h = blockIdx.x % a.Hkv;
   const int item = blockIdx.x / a.Hkv;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -288,37 +325,23 @@ void piece_decode_kernel(const DecodeArgs a) {
   int planned_row = 0;
   bool found;
   int spare_row;
+  bool plan_ok = true;
   if constexpr (PLANNED) {
-    // The descriptor, the header and this lane's tile row, all loads in flight at
-    // once (the host checked that the plan holds the call's items, so the header
-    // and row loads stay inside it whatever the plan is for).  A plan computed
-    // for other sizes or tables addresses other partial slots and rows, so none
-    // of it is used: every workgroup of the grid (items >= batch, so one per row
-    // and kv head) fills its row's heads with NaN, and the error word is set.
+    // The plan's key, the header and this lane's tile row, all loads in flight
+    // at once (the host checked that the plan holds the call's items, so the
+    // header and row loads stay inside it whatever the plan is for).  The key's
+    // verdict joins `found` instead of branching here: a branch on it would let
+    // the compiler sink the header and row loads behind the key's round trip.
+    // A plan computed for other sizes or tables addresses other partial slots
+    // and rows, so none of it is used (see the spare-workgroup branch).
     const int lane = lane_id();
-    const int dv = lane < kPlanDesc ? a.plan[lane] : 0;
+    const uint32_t key_lo = (uint32_t)a.plan[0], key_hi = (uint32_t)a.plan[1];
     const int* hdr = a.plan + kPlanDesc + (int64_t)item * kPlanHdr;
     planned_row = a.plan[kPlanDesc + (int64_t)(a.target + 2 * a.B) * kPlanHdr +
                          ((int64_t)item * kWaves + w) * kWave + lane];
     const int h0 = hdr[0], h1 = hdr[1], h2 = hdr[2], h3 = hdr[3];
     const int h4 = hdr[4], h5 = hdr[5], h6 = hdr[6], h7 = hdr[7];
-    {
-      const int want[kPlanCheck] = {kPlanMagic, a.B, a.Hkv, a.W, a.BS, a.NB, a.target,
-                                    lo32(a.tables), hi32(a.tables), lo32(a.ctx), hi32(a.ctx)};
-      bool ok = true;
-#pragma unroll
-      for (int i = 0; i < kPlanCheck; ++i) ok = ok && readlane_i(dv, i) == want[i];
-      if (!ok) {
-        if (item < a.B) {
-          for (int e = threadIdx.x; e < a.G * D; e += kThreads)
-            store_out1<E>(a.out, ((int64_t)item * a.Hq + h * a.G) * D + e, __builtin_nanf(""));
-        }
-        if (item == 0 && h == 0 && threadIdx.x == 0)
-          __hip_atomic_store(a.plan + kPlanDesc - 1, kPlanErrSizes, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        return;
-      }
-    }
+    plan_ok = ((key_lo ^ a.plan_key_lo) | (key_hi ^ a.plan_key_hi)) == 0;
     pc.b = __builtin_amdgcn_readfirstlane(h0);
     pc.id = __builtin_amdgcn_readfirstlane(h1);
     pc.split = __builtin_amdgcn_readfirstlane(h2);
@@ -327,14 +350,30 @@ void piece_decode_kernel(const DecodeArgs a) {
     pc.tok0 = __builtin_amdgcn_readfirstlane(h5);
     pc.tok_begin = __builtin_amdgcn_readfirstlane(h6);
     pc.tok_end = __builtin_amdgcn_readfirstlane(h7);
-    found = pc.b >= 0;
+    // (the row is consumed here -- the plan kernel never writes a negative row --
+    // so that its load is issued beside the header's rather than sunk behind them)
+    found = plan_ok & (pc.b >= 0) & (__builtin_amdgcn_readfirstlane(planned_row) >= 0);
     spare_row = pc.id;
   } else {
     int total = 0;
     found = find_piece(a.ctx, a.tok0, a.B, a.max_len, a.target, item, pc, total);
     spare_row = item - total;
   }
+  FE_TL_MARK(1);  // the piece is known (plan header, or the partition scan)
+  FE_TL_SET(6, found ? 1 : 0);
   if (!found) {
+    if (PLANNED && !plan_ok) {
+      // not this call's plan: every workgroup of the grid (items >= batch, so one
+      // per row and kv head) fills its row's heads with NaN; the error word is set
+      if (item < a.B) {
+        for (int e = threadIdx.x; e < a.G * D; e += kThreads)
+          store_out1<E>(a.out, ((int64_t)item * a.Hq + h * a.G) * D + e, __builtin_nanf(""));
+      }
+      if (item == 0 && h == 0 && threadIdx.x == 0)
+        __hip_atomic_store(a.plan + kPlanDesc - 1, kPlanErrSizes, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
     // spare workgroup: zero rows of inactive sequences
     const int b = spare_row;
     if (b < a.B && seq_len(a.ctx, b, a.max_len) == 0) {
@@ -476,6 +515,10 @@ void piece_decode_kernel(const DecodeArgs a) {
     for (int x = 0; x < C::NX; ++x) o[x] = core.o[x];
   }
   }
+  FE_TL_MARK(2);  // wave 0's tile loop has ended
+  FE_TL_SET(7, pc.tok_end - pc.tok_begin);
+  FE_TL_SET(8, pc.b);
+  FE_TL_SET(9, pc.nsplit);
 
   // a sequence with a shared prefix always merges (its prefix part is a partial)
   const bool split = pc.nsplit > 1 || pc.tok0 > 0;
@@ -522,6 +565,7 @@ void piece_decode_kernel(const DecodeArgs a) {
       __hip_atomic_store(a.plan + kPlanDesc - 1, kPlanErrStale, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
+  FE_TL_MARK(3);  // the four waves are combined
   const int hq = h * G + (n < G ? n : G - 1);
   if (!split) {
     if (n < G) {
@@ -529,6 +573,7 @@ void piece_decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int xi = 0; xi < XW; ++xi) store_out4<E>(a.out, orow + 16 * (w * XW + xi), ox[xi]);
     }
+    FE_TL_MARK(4);  // output stores issued
     return;
   }
   // device-coherent (sc1) 16-byte stores of this piece's partial output and LSE
@@ -554,9 +599,12 @@ void piece_decode_kernel(const DecodeArgs a) {
     *flag = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
             pc.nsplit - 1;
   __syncthreads();
+  FE_TL_MARK(4);  // partial stored, ticket drawn
+  FE_TL_SET(6, *flag ? 7 : 3);
   if (!*flag) return;
   if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   merge_pieces<D, E>(a, b, h, pc.id - pc.split, pc.nsplit, pc.tok0 > 0);
+  FE_TL_MARK(5);  // merge stores issued
 }
 
 // ---- balanced decode (block sizes that are multiples of 16) ----------------------
@@ -1430,6 +1478,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     if (cascade || block_size % kTile != 0) return FE_ERR_UNSUPPORTED;
     if (plan_len < plan_bytes(target + 2 * batch) || !aligned16(plan)) return FE_ERR_WORKSPACE;
     a.plan = (int*)plan;
+    set_plan_key(a);
   }
   if (cascade) {
     const BalancedPlan bp =
@@ -1527,6 +1576,7 @@ extern "C" int fe_paged_decode_plan(const int32_t* block_tables, int table_strid
   a.target = target;
   a.max_len = max_len;
   a.plan = (int*)plan;
+  set_plan_key(a);
   hipLaunchKernelGGL(decode_plan_kernel, dim3(target + 2 * batch), dim3(kThreads), 0,
                      (hipStream_t)stream, a);
   return FE_LAUNCH_STATUS();
@@ -1780,3 +1830,17 @@ extern "C" int fe_lse_merge_bf16(const float* part_out, const float* part_lse, i
   return lse_merge_impl<Bf16>(part_out, part_lse, num_splits, rows, head_dim, out, out_lse,
                               stream);
 }
+
+#ifdef FE_TIMELINE
+// Diagnostic build only (not declared in include/): the stamps of the last
+// launches, and their reset.
+extern "C" int fe_timeline_read(void* host, int wgs) {
+  if (wgs < 0 || wgs > kTlWgs) return FE_ERR_INVALID_ARGUMENT;
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(fe_tl_stamps),
+                                  (size_t)wgs * kTlSlots * sizeof(unsigned long long));
+}
+extern "C" int fe_timeline_clear() {
+  static unsigned long long zeros[kTlWgs * kTlSlots];
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(fe_tl_stamps), zeros, sizeof(zeros));
+}
+#endif

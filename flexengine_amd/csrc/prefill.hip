@@ -90,8 +90,9 @@ struct PrefillArgs {
   float* part_lse;   // [KS][total_q * Hq] base-2 LSE of each partial
   int* tickets;      // [row blocks * Hkv] (stream-K kernel: [nwg_max]), zero between calls
   // stream-K kernel: the step's plan (fe_prefill_plan), null to derive the
-  // work split in the launch
+  // work split in the launch, and the key of the call's sizes and tensors
   int* plan;
+  uint32_t plan_key_lo, plan_key_hi;
   int64_t q_stride;  // elements from one query row (token or sequence) to the next
   int W, S, total_q, Hq, Hkv, G, BS, bs_log2, NB, KS;
   int nwg_max;       // stream-K kernel: workgroups of the launch
@@ -1027,20 +1028,85 @@ __device__ __forceinline__ void merge_split_rows(const PrefillArgs& a, __amdgpu_
 constexpr int kHalfWaves = kDmaRows / 32;
 constexpr int kDmaThreads = 2 * kHalfWaves * kWave;
 
+constexpr int kPPlanInts = 16;
+constexpr int kPPlanMagic = 0x46505046;  // "FPPF"
+constexpr int kPPlanFields = 15;         // descriptor words: key (2), fields in the clear, digest
+constexpr int kPPlanDigest = 14;         // descriptor word of the digest
+constexpr int kPPlanErrSizes = 1;        // error word: the call's sizes or tensors are not the plan's
+constexpr int kPPlanErrStale = 2;        // error word: q_offsets / context_lens changed since the plan
+static_assert((2 * kPPlanInts - 1) * 4 == FE_PREFILL_PLAN_ERROR_OFFSET &&
+              kPPlanErrSizes == FE_PLAN_ERR_SIZES && kPPlanErrStale == FE_PLAN_ERR_STALE);
+inline size_t pplan_bytes() { return (size_t)(2 + kMaxStreamWgs) * kPPlanInts * sizeof(int32_t); }
+inline void set_pplan_key(PrefillArgs& a) {
+  const uint64_t f[] = {(uint64_t)kPPlanMagic, (uint64_t)a.S, (uint64_t)a.total_q,
+                        (uint64_t)a.Hq, (uint64_t)a.Hkv, (uint64_t)a.W, (uint64_t)a.BS,
+                        (uint64_t)a.nwg_max, (uint64_t)(uintptr_t)a.q_off,
+                        (uint64_t)(uintptr_t)a.ctx};
+  const uint64_t h = plan_key(f, (int)(sizeof(f) / sizeof(f[0])));
+  a.plan_key_lo = (uint32_t)h;
+  a.plan_key_hi = (uint32_t)(h >> 32);
+}
+
+// lowbias32 (C. Wellons' published 32-bit integer hash)
+__device__ __forceinline__ uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+// Digest of q_offsets[0..S] and context_lens[0..S), uniform over the wave: lane
+// s of a pass loads q_offsets[s] (s <= S) and context_lens[s] (s < S), both
+// loads unconditional (indices clamped, results selected), so for up to 63
+// sequences all of it is one round trip.  S >= 1 (the callers return earlier
+// for an empty batch).
+__device__ __forceinline__ int lens_digest(const PrefillArgs& a) {
+  const int lane = lane_id();
+  uint32_t d = 0;
+  for (int base = 0; base <= a.S; base += kWave) {
+    const int s = base + lane;
+    const uint32_t qo = (uint32_t)a.q_off[min(s, a.S)];
+    const uint32_t cx = (uint32_t)a.ctx[min(s, a.S - 1)];
+    const uint32_t mq = mix32(qo + 0x9e3779b9u * (uint32_t)(s + 1));
+    const uint32_t mc = mix32(cx + 0x85ebca6bu * (uint32_t)(s + 1));
+    d += s <= a.S ? (s < a.S ? mq ^ mc : mq) : 0u;
+  }
+  return wave_sum_i((int)d);
+}
+
+// A planned launch whose plan is not for the call: every workgroup of the grid
+// writes NaN to its grid-stride share of the output (so the whole of it is
+// NaN), and workgroup 0 sets the plan's error word.
+template <int D, class E>
+__device__ __forceinline__ void refuse_plan(const PrefillArgs& a, int err) {
+  const f16 nan = to16<E>(__builtin_nanf(""));
+  const int64_t n = (int64_t)a.total_q * a.Hq * D;
+  for (int64_t e = (int64_t)blockIdx.x * kDmaThreads + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * kDmaThreads)
+    a.out[e] = nan;
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(a.plan + 2 * kPPlanInts - 1, err, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The units of workgroup gid's range [x_begin, x_end) for the waves of half H
 // (wave r of the half); k0 .. v1 are the half's stage objects, pk1 / pv1 the
 // partner half's stage-1 objects, xml the exchange of row maxima and sums and
 // last the workgroup's ticket result.  Units follow each other without a
 // pipeline bubble: after a unit's last step the next unit's block ids, queries
 // and first block (into stage 0) are loaded while the halves exchange their
-// states (in the stage-1 objects) and store.
-template <int D, int RT, int H, class E>
+// states (in the stage-1 objects) and store.  PLANNED: the live lengths'
+// digest is checked against the plan's (plan_digest) while the first unit's
+// loads are in flight -- they stay in bounds for a stale plan of the call's
+// sizes -- and before anything is stored or any ticket drawn.
+template <int D, int RT, int H, class E, bool PLANNED = false>
 __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan& pl, int gid,
                                           int x_begin, int x_end, StreamPos sp, int r,
                                           unsigned char* k0, unsigned char* v0,
                                           unsigned char* k1, unsigned char* v1,
                                           const unsigned char* pk1, const unsigned char* pv1,
-                                          float* xml, int* last) {
+                                          float* xml, int* last, int plan_digest = 0) {
   using P = DCfg<D>;
   static_assert(RT == 2, "each half's wave exchanges one of its two row tiles");
   static_assert(2 * P::NX * kWave * 16 <= P::MAT, "two waves' tiles per stage object");
@@ -1140,8 +1206,21 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
   bool pend = false;
 
   open_unit();
+  if constexpr (PLANNED) {
+    // one wave reads the lengths and posts the verdict for the barrier below
+    if (H == 0 && r == 0) {
+      const int stale = lens_digest(a) != plan_digest;
+      if (lane == 0) last[9] = stale;
+    }
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  if constexpr (PLANNED) {
+    if (last[9]) {  // workgroup-uniform; nothing stored yet, no ticket drawn
+      refuse_plan<D, E>(a, kPPlanErrStale);
+      return;
+    }
+  }
   while (true) {
     float m_run[RT];
     f32x4 o[RT][P::NX];
@@ -1444,47 +1523,17 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
 // fe_prefill_paged_planned reads it with one load instead of the scans of
 // stream_plan and stream_locate.  Layout (int32): a header of kPPlanInts
 // (nwg, T, q, r of the Ranges), a descriptor of kPPlanInts (what the plan was
-// computed for: magic, the sizes, the q_offsets and context_lens addresses, a
-// digest of their contents, and last an error word the planned kernel sets),
-// then kPPlanInts per workgroup: x_begin, x_end, has work, logical id, then the
-// StreamPos s, h, rb, kb, q0, n, cached, R, tb.
+// computed for: the 64-bit key of the sizes and tensors, the same fields in
+// the clear -- magic, the sizes, the q_offsets and context_lens addresses --,
+// a digest of their contents, and last an error word the planned kernel
+// sets), then kPPlanInts per workgroup: x_begin, x_end, has work, logical id,
+// then the StreamPos s, h, rb, kb, q0, n, cached, R, tb.
 //
 // A planned launch checks the descriptor before anything else: every unit after
 // a workgroup's first is located from the live q_offsets / context_lens, so a
 // plan of other contents would make workgroups disagree on a unit's size and
 // leave its ticket set for the next launch.  On a mismatch the launch writes
 // NaN to every output row, sets the error word and returns.
-constexpr int kPPlanInts = 16;
-constexpr int kPPlanMagic = 0x46505046;  // "FPPF"
-constexpr int kPPlanCheck = 13;          // descriptor words a planned launch compares
-constexpr int kPPlanErrSizes = 1;        // error word: the call's sizes or tensors are not the plan's
-constexpr int kPPlanErrStale = 2;        // error word: q_offsets / context_lens changed since the plan
-static_assert((2 * kPPlanInts - 1) * 4 == FE_PREFILL_PLAN_ERROR_OFFSET &&
-              kPPlanErrSizes == FE_PLAN_ERR_SIZES && kPPlanErrStale == FE_PLAN_ERR_STALE);
-inline size_t pplan_bytes() { return (size_t)(2 + kMaxStreamWgs) * kPPlanInts * sizeof(int32_t); }
-
-// lowbias32 (C. Wellons' published 32-bit integer hash)
-__device__ __forceinline__ uint32_t mix32(uint32_t x) {
-  x ^= x >> 16;
-  x *= 0x7feb352du;
-  x ^= x >> 15;
-  x *= 0x846ca68bu;
-  x ^= x >> 16;
-  return x;
-}
-// Digest of q_offsets[0..S] and context_lens[0..S), uniform over the wave.
-__device__ __forceinline__ int lens_digest(const PrefillArgs& a) {
-  const int lane = lane_id();
-  uint32_t d = lane == 0 ? mix32((uint32_t)a.q_off[a.S] ^ 0x5bd1e995u) : 0u;
-  for (int base = 0; base < a.S; base += kWave) {
-    const int s = base + lane;
-    if (s < a.S)
-      d += mix32((uint32_t)a.q_off[s] + 0x9e3779b9u * (uint32_t)(s + 1)) ^
-           mix32((uint32_t)a.ctx[s] + 0x85ebca6bu * (uint32_t)(s + 1));
-  }
-  return wave_sum_i((int)d);
-}
-
 // One wave per workgroup entry of the launch the plan is for (grid nwg_max).
 __global__ __launch_bounds__(kWave) void prefill_plan_kernel(const PrefillArgs a, int* plan) {
   const StreamPlan pl = stream_plan(a);
@@ -1493,14 +1542,16 @@ __global__ __launch_bounds__(kWave) void prefill_plan_kernel(const PrefillArgs a
   if (blockIdx.x == 0) {
     const int digest = lens_digest(a);
     const int hdr[4] = {nwg, pl.rg.T, pl.rg.q, pl.rg.r};
-    const int desc[kPPlanCheck] = {kPPlanMagic, a.S, a.total_q, a.Hq, a.Hkv, a.W, a.BS,
-                                   a.nwg_max, lo32(a.q_off), hi32(a.q_off), lo32(a.ctx),
-                                   hi32(a.ctx), digest};
+    const int desc[kPPlanFields] = {(int)a.plan_key_lo, (int)a.plan_key_hi, kPPlanMagic, a.S,
+                                    a.total_q, a.Hq, a.Hkv, a.W, a.BS, a.nwg_max,
+                                    lo32(a.q_off), hi32(a.q_off), lo32(a.ctx), hi32(a.ctx),
+                                    digest};
+    static_assert(kPPlanDigest == kPPlanFields - 1, "the digest closes the descriptor");
     int v = 0;  // zero padding and the error word
 #pragma unroll
     for (int i = 0; i < 4; ++i) v = lane == i ? hdr[i] : v;
 #pragma unroll
-    for (int i = 0; i < kPPlanCheck; ++i) v = lane == kPPlanInts + i ? desc[i] : v;
+    for (int i = 0; i < kPPlanFields; ++i) v = lane == kPPlanInts + i ? desc[i] : v;
     if (lane < 2 * kPPlanInts) plan[lane] = v;
   }
   int e[13] = {};
@@ -1540,46 +1591,36 @@ void prefill_dma_kernel(const PrefillArgs a) {
   __shared__ float xml[2 * kHalfWaves * 2 * kWave];  // row maxima and sums exchanged at unit ends
   // whether this workgroup drew the last ticket of its range's last unit [0]
   // and of its first unit [1], when split; [2..8]: the first unit's merge
-  // parameters
-  __shared__ int last[9];
+  // parameters; [9]: a planned launch's verdict on the lengths (stale plan)
+  __shared__ int last[10];
 
   StreamPlan pl;
   StreamPos sp;
   int gid, x_begin, x_end;
+  int plan_digest = 0;
   if constexpr (PLANNED) {
     // the ranges and this workgroup's first unit from the plan: its entry,
     // header and descriptor in one round trip (lanes 0-15 the entry, 16-31 the
-    // header, 32-47 the descriptor), the live lengths' loads beside them
+    // header, 32-47 the descriptor).  The key of the sizes and tensors is
+    // checked here; the digest of the lengths while the first unit's loads
+    // are in flight (run_units), or here by workgroups without work.
     const int lane = lane_id();
     const int v = lane < kPPlanInts ? a.plan[2 * kPPlanInts + (int)blockIdx.x * kPPlanInts + lane]
                                     : (lane < 3 * kPPlanInts ? a.plan[lane - kPPlanInts] : 0);
-    const int digest = lens_digest(a);
-    {
-      const int want[kPPlanCheck] = {kPPlanMagic, a.S, a.total_q, a.Hq, a.Hkv, a.W, a.BS,
-                                     a.nwg_max, lo32(a.q_off), hi32(a.q_off), lo32(a.ctx),
-                                     hi32(a.ctx), digest};
-      int bad = 0;
-#pragma unroll
-      for (int i = 0; i < kPPlanCheck; ++i)
-        bad = bad ? bad : (readlane_i(v, 2 * kPPlanInts + i) == want[i]
-                               ? 0
-                               : (i + 1 == kPPlanCheck ? kPPlanErrStale : kPPlanErrSizes));
-      if (bad) {
-        const f16 nan = to16<E>(__builtin_nanf(""));
-        const int64_t n = (int64_t)a.total_q * a.Hq * D;
-        for (int64_t e = (int64_t)blockIdx.x * kDmaThreads + threadIdx.x; e < n;
-             e += (int64_t)gridDim.x * kDmaThreads)
-          a.out[e] = nan;
-        if (blockIdx.x == 0 && threadIdx.x == 0)
-          __hip_atomic_store(a.plan + 2 * kPPlanInts - 1, bad, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        return;
-      }
+    const uint32_t diff_key = ((uint32_t)readlane_i(v, 2 * kPPlanInts) ^ a.plan_key_lo) |
+                              ((uint32_t)readlane_i(v, 2 * kPPlanInts + 1) ^ a.plan_key_hi);
+    if (diff_key) {
+      refuse_plan<D, E>(a, kPPlanErrSizes);
+      return;
     }
+    plan_digest = readlane_i(v, 2 * kPPlanInts + kPPlanDigest);
     pl.rg = Ranges{readlane_i(v, 16 + 1), readlane_i(v, 16 + 0), readlane_i(v, 16 + 2),
                    readlane_i(v, 16 + 3)};
     pl.w0 = SeqWork{};
-    if ((int)blockIdx.x >= pl.rg.nwg || readlane_i(v, 2) == 0) return;
+    if ((int)blockIdx.x >= pl.rg.nwg || readlane_i(v, 2) == 0) {
+      if (lens_digest(a) != plan_digest) refuse_plan<D, E>(a, kPPlanErrStale);
+      return;
+    }
     x_begin = readlane_i(v, 0);
     x_end = readlane_i(v, 1);
     gid = readlane_i(v, 3);
@@ -1605,11 +1646,11 @@ void prefill_dma_kernel(const PrefillArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = w % kHalfWaves;
   if (w < kHalfWaves)
-    run_units<D, RT, 0, E>(a, pl, gid, x_begin, x_end, sp, r, k00, v00, k01, v01, k11, v11, xml,
-                           last);
+    run_units<D, RT, 0, E, PLANNED>(a, pl, gid, x_begin, x_end, sp, r, k00, v00, k01, v01, k11,
+                                    v11, xml, last, plan_digest);
   else
-    run_units<D, RT, 1, E>(a, pl, gid, x_begin, x_end, sp, r, k10, v10, k11, v11, k01, v01, xml,
-                           last);
+    run_units<D, RT, 1, E, PLANNED>(a, pl, gid, x_begin, x_end, sp, r, k10, v10, k11, v11, k01,
+                                    v01, xml, last, plan_digest);
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1841,6 +1882,7 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   a.pre_lse = nullptr;
   a.tok0 = nullptr;
   a.plan = (int*)step_plan;
+  if (a.plan != nullptr) set_pplan_key(a);
   hipStream_t s = (hipStream_t)stream;
   if (dma && bf16) {
     if (head_dim == 64) launch_prefill_dma<64, Bf16>(a, s); else launch_prefill_dma<128, Bf16>(a, s);
@@ -1936,6 +1978,7 @@ extern "C" int fe_prefill_plan(const int32_t* q_offsets, const int32_t* context_
   a.BS = block_size;
   a.bs_log2 = bs_log2;
   a.nwg_max = nwg;
+  set_pplan_key(a);
   hipLaunchKernelGGL(prefill_plan_kernel, dim3(nwg), dim3(kWave), 0, (hipStream_t)stream, a,
                      (int*)plan);
   return FE_LAUNCH_STATUS();
