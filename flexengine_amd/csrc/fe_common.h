@@ -382,6 +382,8 @@ __device__ __forceinline__ bool find_piece(const int32_t* ctx, const int32_t* to
 // the attention over the shared keys as fp32 (normalised) plus its base-2
 // LSE, and tok0[b] for every row: the first key its own decode attends (the
 // prefix end, or 0 when the row does not share a prefix). ----
+// Most slots of a shared-prefix result (CascadePrefix::splits).
+constexpr int kMaxPrefixSlots = 4;
 struct CascadePrefix {
   const void* q;
   int64_t q_stride;
@@ -395,17 +397,24 @@ struct CascadePrefix {
   const int32_t* prefix_len;
   int num_groups, batch, hq, hkv, d, bs;
   float scale;
-  int* tickets;      // zero between calls (shared with the decode launch)
   float* pre_o;      // [batch * hq][d]
   float* pre_lse;    // [batch * hq]
   int32_t* tok0;     // [batch]
   void* scratch;     // key-split partials, cascade_prefix_scratch_bytes
   bool bf16;         // q and the pools are bfloat16 (fp16 otherwise)
+  // set by cascade_prefix_launch: the prefix result the decode launch folds
+  // into every row with a shared prefix -- `splits` slots per query-head row
+  // r (row-major: the slots of a row are adjacent), slot s a normalised
+  // output at out_o + (r * splits + s) * d and its base-2 LSE at
+  // out_lse[r * splits + s]
+  float* out_o;
+  float* out_lse;
+  int splits;
 };
 __attribute__((visibility("hidden"))) size_t cascade_prefix_scratch_bytes(int num_groups,
                                                                           int batch, int hq,
                                                                           int hkv, int d);
-__attribute__((visibility("hidden"))) int cascade_prefix_launch(const CascadePrefix& c,
+__attribute__((visibility("hidden"))) int cascade_prefix_launch(CascadePrefix& c,
                                                                 hipStream_t stream);
 
 }  // namespace fe

@@ -100,11 +100,13 @@ struct DecodeArgs {
   float* ws_lse;     // [pieces, Hq]  (base 2)
   int* tickets;      // [B, Hkv], zero between calls
   // shared-prefix decode: sequence b attends only keys tok0[b].. here and
-  // merges the prefix attention (pre_o [B*Hq][D], base-2 pre_lse [B*Hq]) in;
-  // all three null otherwise
+  // merges the prefix attention in -- pre_splits slots per query-head row r of
+  // normalised outputs (slot s at pre_o + (r*pre_splits + s)*D) and base-2
+  // LSEs (pre_lse[r*pre_splits + s]); null and 0 otherwise
   const int32_t* tok0;
   const float* pre_o;
   const float* pre_lse;
+  int pre_splits;
   int64_t q_stride;
   int64_t new_stride;
   int W, B, Hq, Hkv, G, BS, bs_log2, NB, target;
@@ -172,6 +174,46 @@ __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)
 // common case (ns <= kMergeBatch) is one round trip to memory and no barrier.
 constexpr int kMergeBatch = 16;
 
+// Folds the shared-prefix result of query-head row r (dims d0 .. d0 + 3; every
+// slot the prefix launch wrote, loaded in one round trip: a row's slots are
+// adjacent) into an online merge state: running maximum M (base 2),
+// denominator den and numerator num.  Called for rows with a shared prefix,
+// so pre_splits >= 1.
+template <int D>
+__device__ __forceinline__ void fold_prefix(const DecodeArgs& a, int64_t r, int d0, float& M,
+                                            float& den, f32x4& num) {
+  const int64_t r0 = r * a.pre_splits;
+  float lv[kMaxPrefixSlots];
+  f32x4 ov[kMaxPrefixSlots];
+  // every load unconditional (slots past the last repeat it and get weight 0):
+  // guarded loads were issued one branch at a time, a round trip each
+#pragma unroll
+  for (int s = 0; s < kMaxPrefixSlots; ++s) {
+    const int sc = s < a.pre_splits ? s : a.pre_splits - 1;
+    lv[s] = a.pre_lse[r0 + sc];
+    ov[s] = *reinterpret_cast<const f32x4*>(a.pre_o + (r0 + sc) * D + d0);
+  }
+#pragma unroll
+  for (int s = 0; s < kMaxPrefixSlots; ++s)
+    if (s >= a.pre_splits) lv[s] = kNegInf;
+  // no early exit when every slot is -inf (the loads above would sink below
+  // it): newM is then M, and alpha 1 (or 0 for a state that is still empty)
+  float bm = kNegInf;
+#pragma unroll
+  for (int s = 0; s < kMaxPrefixSlots; ++s) bm = fmaxf(bm, lv[s]);
+  const float newM = fmaxf(M, bm);
+  const float alpha = M == kNegInf ? 0.f : exp2f(M - newM);
+  num *= alpha;
+  den *= alpha;
+#pragma unroll
+  for (int s = 0; s < kMaxPrefixSlots; ++s) {
+    const float wv = lv[s] == kNegInf ? 0.f : exp2f(lv[s] - newM);
+    num += wv * ov[s];
+    den += wv;
+  }
+  M = newM;
+}
+
 template <int D, class E = Fp16>
 __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, int first,
                                              int ns, bool pre = false) {
@@ -219,19 +261,8 @@ __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, 
       }
       M = newM;
     }
-    if (pre) {
-      // the shared-prefix part, written by the launch before this one
-      const int64_t r = (int64_t)b * a.Hq + h * G;
-      const float lv = a.pre_lse[r + hh];
-      const f32x4 ov = *reinterpret_cast<const f32x4*>(a.pre_o + r * D + e4 * 4);
-      if (lv != kNegInf) {
-        const float newM = fmaxf(M, lv);
-        const float alpha = M == kNegInf ? 0.f : exp2f(M - newM);
-        num = num * alpha + exp2f(lv - newM) * ov;
-        den = den * alpha + exp2f(lv - newM);
-        M = newM;
-      }
-    }
+    // the shared-prefix part, written by the launch before this one
+    if (pre) fold_prefix<D>(a, (int64_t)b * a.Hq + h * G + hh, (e4 * 4) % D, M, den, num);
     const float inv = 1.f / den;
     store_out4<E>(a.out, ((int64_t)b * a.Hq + h * G) * D + e4 * 4, num * inv);
   }
@@ -1005,14 +1036,10 @@ __global__ __launch_bounds__(kBThreads) void balanced_decode_kernel(const Decode
       const int d0 = (xg >> 2) * 16 + (xg & 3) * 4;
       const int start = seg_start(sg);
       if (start >= lo && start + seg_tiles(sg) <= hi) {
-        if (S0[b] > 0) {  // fold in the shared-prefix partial of the launch before
-          const float lp = a.pre_lse[r];
-          if (lp != kNegInf) {
-            const f32x4 op = *reinterpret_cast<const f32x4*>(a.pre_o + r * D + d0);
-            const float mx = fmaxf(lse, lp);
-            const float w1 = exp2f(lse - mx), w2 = exp2f(lp - mx);
-            acc = (w1 * acc + w2 * op) * (1.f / (w1 + w2));
-          }
+        if (S0[b] > 0) {  // fold in the shared-prefix result of the launch before
+          float M = lse, dsum = 1.f;
+          fold_prefix<D>(a, r, d0, M, dsum, acc);
+          if (dsum > 0.f) acc *= 1.f / dsum;
         }
         *reinterpret_cast<f16x4*>(a.out + r * D + d0) = to16x4<E>(acc);
       } else {
@@ -1200,16 +1227,7 @@ __global__ __launch_bounds__(kBThreads) void balanced_decode_kernel(const Decode
       M = newM;
     }
     const int64_t r = (int64_t)b * a.Hq + h * G;
-    if (S0[b] > 0) {  // the shared-prefix part
-      const float lp = a.pre_lse[r + hh];
-      if (lp != kNegInf) {
-        const f32x4 op = *reinterpret_cast<const f32x4*>(a.pre_o + r * D + e4 * 4);
-        const float newM = fmaxf(M, lp);
-        const float alpha = M == kNegInf ? 0.f : exp2f(M - newM);
-        num = num * alpha + exp2f(lp - newM) * op;
-        den = den * alpha + exp2f(lp - newM);
-      }
-    }
+    if (S0[b] > 0) fold_prefix<D>(a, r + hh, (e4 * 4) % D, M, den, num);  // the shared prefix
     const float inv = 1.f / den;
     *reinterpret_cast<f16x4*>(a.out + r * D + e4 * 4) = to16x4<E>(num * inv);
   }
@@ -1455,6 +1473,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   a.tok0 = nullptr;
   a.pre_o = nullptr;
   a.pre_lse = nullptr;
+  a.pre_splits = 0;
   a.q_stride = q_batch_stride;
   a.new_stride = new_batch_stride;
   a.W = table_stride;
@@ -1507,7 +1526,6 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     c.d = head_dim;
     c.bs = block_size;
     c.scale = scale;
-    c.tickets = a.tickets;  // each launch leaves the tickets it used at zero
     c.bf16 = bf16;
     c.tok0 = (int32_t*)cw;
     cw += align256((size_t)batch * sizeof(int32_t));
@@ -1519,8 +1537,9 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     const int rc = cascade_prefix_launch(c, s);
     if (rc != FE_OK) return rc;
     a.tok0 = c.tok0;
-    a.pre_o = c.pre_o;
-    a.pre_lse = c.pre_lse;
+    a.pre_o = c.out_o;
+    a.pre_lse = c.out_lse;
+    a.pre_splits = c.splits;
   }
   if (f32) return head_dim == 64 ? launch_decode<64, F32>(a, s) : launch_decode<128, F32>(a, s);
   if (bf16) return head_dim == 64 ? launch_decode<64, Bf16>(a, s) : launch_decode<128, Bf16>(a, s);

@@ -54,6 +54,7 @@ constexpr int kPS = kBlockKeys / 32;    // 32-key PV steps per block
 // 55 us; 8: 61 us, 8 with loads only for the live splits: 57.5 us, 2: 63 us; the
 // C3 shared-prefix decode 81 us at 4 and 8, 91 us at 2).
 constexpr int kMaxSplits = 4;
+static_assert(kMaxSplits <= kMaxPrefixSlots, "the cascade prefix writes one slot per key split");
 // Rows of the split merge whose partials are loaded in one round trip: the C3
 // shared-prefix pass took 24.15 us with 1 (a round trip per 8 rows), 23.79 with
 // 2, 23.06 with 4 and 23.14 with 8.
@@ -139,13 +140,16 @@ __device__ __forceinline__ bool locate_rows(const PrefillArgs& a, int item, RowB
   int carry = 0;
   for (int base = 0; base < a.S; base += kWave) {
     const int s = base + lane;
-    int q0 = 0, n = 0;
+    int q0 = 0, n = 0, cx = 0;
     if (s < a.S) {
       // rows outside [0, total_q) are dropped: every row the kernel touches
       // (q, out, the context and table of a decode row) stays in its array
       q0 = min(max(a.q_off[s], 0), a.total_q);
       n = min(a.q_off[s + 1], a.total_q) - q0;
       n = n > 0 ? n : 0;
+      // the context length (group prefix) loaded with the offsets: the hit
+      // lane's is read below without another round trip
+      cx = CASCADE ? group_prefix(a, s) : clamp_len(a.ctx[s]);
     }
     const int nb = (n * a.G + ROWS - 1) / ROWS;
     const int incl = wave_scan_incl_i(nb) + carry;
@@ -157,8 +161,7 @@ __device__ __forceinline__ bool locate_rows(const PrefillArgs& a, int item, RowB
       rb.rb = item - readlane_i(excl, src);
       rb.n = readlane_i(n, src);
       rb.q0 = readlane_i(q0, src);
-      rb.ctx = __builtin_amdgcn_readfirstlane(CASCADE ? group_prefix(a, rb.s)
-                                                      : clamp_len(a.ctx[rb.s]));
+      rb.ctx = readlane_i(cx, src);
       return true;
     }
     carry = readlane_i(incl, kWave - 1);
@@ -168,16 +171,18 @@ __device__ __forceinline__ bool locate_rows(const PrefillArgs& a, int item, RowB
 
 // Cascade mode: the decode row b shares group s's prefix when its context
 // reaches past it; its own decode then starts at the prefix end.  Written by
-// the first workgroup for every decode row (0 = no shared prefix).
-__device__ void write_suffix_starts(const PrefillArgs& a) {
-  for (int b = threadIdx.x; b < a.total_q; b += kThreads) {
+// one workgroup for every decode row (0 = no shared prefix).  offs: the group
+// offsets q_off[0 .. S], in global memory or a copy in LDS.
+template <class Offs>
+__device__ void write_suffix_starts(const PrefillArgs& a, Offs offs) {
+  for (int b = threadIdx.x; b < a.total_q; b += blockDim.x) {
     int lo = 0, hi = a.S;  // last group s with q_off[s] <= b
     while (hi - lo > 1) {
       const int mid = (lo + hi) / 2;
-      if (a.q_off[mid] <= b) lo = mid; else hi = mid;
+      if (offs[mid] <= b) lo = mid; else hi = mid;
     }
     int t = 0;
-    if (a.S > 0 && a.q_off[lo] <= b && b < a.q_off[lo + 1]) {
+    if (a.S > 0 && offs[lo] <= b && b < offs[lo + 1]) {
       const int pl = group_prefix(a, lo);
       t = member_len(a, b) > pl ? pl : 0;
     }
@@ -185,15 +190,122 @@ __device__ void write_suffix_starts(const PrefillArgs& a) {
   }
 }
 
-template <int D, int RT, bool CASCADE, class E = Fp16>
+// The end of a key split of the tile kernel.  Lane (g, n) holds
+// O[row n][dims 16x + 4g + i] of its RT row tiles, the row's running maximum
+// m_run (base 2) and its sum l.  One split: normalise and store.  Several:
+// write this split's partial (device-coherent stores), draw the row block's
+// ticket; the last split merges all of them.
+template <int D, int RT, class E>
+__device__ __forceinline__ void finish_split(const PrefillArgs& a, const RowBlock& rb, int item,
+                                             int h, int ks, int wr0, int r0, int r_last,
+                                             const bool (&valid)[RT], const float (&m_run)[RT],
+                                             const float (&l)[RT], const f32x4 (&o)[RT][D / 16],
+                                             int* last) {
+  constexpr int NX = D / 16;
+  const int G = a.G;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const bool split = a.KS > 1;
+  const int64_t split_stride = (int64_t)a.total_q * a.Hq;  // rows per split
+  // (only used when split; the host keeps KS * rows * D floats under 2 GiB)
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      a.part_o, 0, split ? (int)(a.KS * split_stride * D * 4) : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
+      a.part_lse, 0, split ? (int)(a.KS * split_stride * 4) : 0, 0x00020000);
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    if (!valid[rt]) continue;
+    const int row = wr0 + 16 * rt + n;
+    const int64_t orow_idx = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
+    const float inv = l[rt] > 0.f ? 1.f / l[rt] : 0.f;
+    if (!split) {
+      f16* orow = a.out + orow_idx * D + 4 * g;
+#pragma unroll
+      for (int x = 0; x < NX; ++x)
+        *reinterpret_cast<f16x4*>(orow + 16 * x) = to16x4<E>(o[rt][x] * inv);
+    } else {
+      // device-coherent stores through one wave-uniform descriptor per array
+      // (the host keeps the partial arrays under 2 GiB)
+      const uint32_t prow = (uint32_t)((int64_t)ks * a.total_q * a.Hq + orow_idx);
+#pragma unroll
+      for (int x = 0; x < NX; ++x)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[rt][x] * inv), ro,
+                                               (prow * D + 16 * x + 4 * g) * (uint32_t)sizeof(float),
+                                               0, kSc1);
+      if (g == 0)
+        __builtin_amdgcn_raw_buffer_store_b32(
+            __builtin_bit_cast(uint32_t, l[rt] > 0.f ? m_run[rt] + log2f(l[rt]) : kNegInf), rl,
+            prow * (uint32_t)sizeof(float), 0, kSc1);
+    }
+  }
+  if (!split) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials are complete
+  __syncthreads();
+  if (tid == 0)
+    *last = __hip_atomic_fetch_add(a.tickets + item * a.Hkv + h, 1, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) == a.KS - 1;
+  __syncthreads();
+  if (!*last) return;
+  if (tid == 0)
+    __hip_atomic_store(a.tickets + item * a.Hkv + h, 0, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  // merge: thread -> (row of the block, 4 consecutive dims).  All KS LSEs and
+  // partial outputs of kMergeRows of the thread's rows are loaded at once
+  // (indices past KS repeat the last split and get weight 0; rows past the
+  // block repeat its last row and are not stored), so the block's rows cost
+  // ceil(rows / (RPS * kMergeRows)) round trips to memory.
+  constexpr int TPR = D / 4;             // threads per row
+  constexpr int RPS = kThreads / TPR;    // rows per pass
+  const int d4 = (tid % TPR) * 4;
+  for (int row0 = r0 + tid / TPR; row0 <= r_last; row0 += RPS * kMergeRows) {
+    float lse[kMergeRows][kMaxSplits];
+    f32x4 ov[kMergeRows][kMaxSplits];
+    int64_t orow_idx[kMergeRows];
+#pragma unroll
+    for (int u = 0; u < kMergeRows; ++u) {
+      const int row = min(row0 + u * RPS, r_last);
+      orow_idx[u] = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
+#pragma unroll
+      for (int k = 0; k < kMaxSplits; ++k) {
+        const int kc = k < a.KS ? k : a.KS - 1;
+        const uint32_t prow = (uint32_t)(kc * split_stride + orow_idx[u]);
+        lse[u][k] = __builtin_bit_cast(
+            float,
+            __builtin_amdgcn_raw_buffer_load_b32(rl, prow * (uint32_t)sizeof(float), 0, kSc1));
+        ov[u][k] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       ro, (prow * D + d4) * (uint32_t)sizeof(float), 0, kSc1));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeRows; ++u) {
+      if (row0 + u * RPS > r_last) break;
+      float M = kNegInf;
+#pragma unroll
+      for (int k = 0; k < kMaxSplits; ++k)
+        if (k < a.KS) M = fmaxf(M, lse[u][k]);
+      f32x4 num = {0.f, 0.f, 0.f, 0.f};
+      float den = 0.f;
+#pragma unroll
+      for (int k = 0; k < kMaxSplits; ++k) {
+        const float wgt = k < a.KS && lse[u][k] != kNegInf ? exp2f(lse[u][k] - M) : 0.f;
+        num += wgt * ov[u][k];
+        den += wgt;
+      }
+      const float inv = den > 0.f ? 1.f / den : 0.f;
+      *reinterpret_cast<f16x4*>(a.out + orow_idx[u] * D + d4) = to16x4<E>(num * inv);
+    }
+  }
+}
+
+template <int D, int RT, class E = Fp16>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void prefill_kernel(const PrefillArgs a) {
   using P = PCfg<D, RT>;
   extern __shared__ __align__(16) unsigned char smem[];
 
-  if constexpr (CASCADE) {
-    if (blockIdx.x == 0) write_suffix_starts(a);
-  }
   // workgroup i: (KV head, key split) pair i % P, row block i / P (P = Hkv * KS);
   // the hardware places workgroup i on XCD i % 8, so when P divides 8 or is a
   // multiple of it every XCD serves fixed pairs -- one KV head and one key
@@ -202,7 +314,7 @@ void prefill_kernel(const PrefillArgs a) {
   const int item = blockIdx.x / npair;
   const int pair = blockIdx.x - item * npair;
   RowBlock rb;
-  if (!locate_rows<P::ROWS, CASCADE>(a, item, rb)) return;
+  if (!locate_rows<P::ROWS, false>(a, item, rb)) return;
   const int h = pair % a.Hkv;
   const int G = a.G;
   const int tid = threadIdx.x;
@@ -212,11 +324,11 @@ void prefill_kernel(const PrefillArgs a) {
   const int n = lane & 15;
 
   const int total_rows = rb.n * G;
-  const int cached = CASCADE ? 0 : (rb.ctx >= rb.n ? rb.ctx - rb.n : 0);
+  const int cached = rb.ctx >= rb.n ? rb.ctx - rb.n : 0;
   const int r0 = rb.rb * P::ROWS;
   const int r_last = min(r0 + P::ROWS, total_rows) - 1;
-  // keys the row block reads: causal up to its last position, or the prefix
-  const int key_end = CASCADE ? rb.ctx : cached + r_last / G + 1;
+  // keys the row block reads: causal up to its last position
+  const int key_end = cached + r_last / G + 1;
   // split ks of KS takes an equal share of the row block's key blocks
   const int ks = pair / a.Hkv;
   const int nblocks_all = (key_end + kBlockKeys - 1) / kBlockKeys;
@@ -226,24 +338,16 @@ void prefill_kernel(const PrefillArgs a) {
   const int wr0 = r0 + w * 16 * RT;                               // first row of this wave
 
   // ---- this lane's rows: query vectors (B operand), last key each may see
-  //      (its position; in cascade mode the prefix end, or -1 for a row whose
-  //      context does not reach past the prefix) ----
+  //      (its position) ----
   f16x8 qv[RT][P::NC];
   int pos[RT];
   bool valid[RT];
-  int pos_lo = 0x7fffffff;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int row = wr0 + 16 * rt + n;
     valid[rt] = row < total_rows;
     const int rc = valid[rt] ? row : r_last;
-    if constexpr (CASCADE) {
-      const int L = member_len(a, rb.q0 + rc / G);
-      pos[rt] = valid[rt] && L > rb.ctx ? rb.ctx - 1 : -1;
-    } else {
-      pos[rt] = valid[rt] ? cached + rc / G : -1;
-    }
-    if (valid[rt]) pos_lo = min(pos_lo, pos[rt]);
+    pos[rt] = valid[rt] ? cached + rc / G : -1;
     const f16* qrow = a.q + (int64_t)(rb.q0 + rc / G) * a.q_stride + (h * G + rc % G) * D + 8 * g;
 #pragma unroll
     for (int c = 0; c < P::NC; ++c) {
@@ -253,13 +357,7 @@ void prefill_kernel(const PrefillArgs a) {
   }
 
   // blocks whose last key is <= every row's position need no mask
-  int unmasked_blocks;
-  if constexpr (CASCADE) {
-    pos_lo = -wave_max_i(-min(pos_lo, rb.ctx));
-    unmasked_blocks = __builtin_amdgcn_readfirstlane((pos_lo + 1) / kBlockKeys);
-  } else {
-    unmasked_blocks = (cached + min(wr0, r_last) / G + 1) / kBlockKeys;
-  }
+  const int unmasked_blocks = (cached + min(wr0, r_last) / G + 1) / kBlockKeys;
 
   float m_run[RT], l_run[RT];
   f32x4 o[RT][P::NX];
@@ -275,7 +373,7 @@ void prefill_kernel(const PrefillArgs a) {
   //      t / CPR + KPL * i (keys at or past key_end repeat key_end - 1).  The
   //      block ids a block needs are fetched one iteration before its K/V
   //      loads, so no table access sits in front of a K/V load. ----
-  const int32_t* trow = a.tables + (int64_t)(CASCADE ? rb.q0 : rb.s) * a.W;
+  const int32_t* trow = a.tables + (int64_t)rb.s * a.W;
   const int chunk = tid % P::CPR;
   const int krow = tid / P::CPR;
   f16x8 kst[P::LOADS], vst[P::LOADS];
@@ -427,113 +525,15 @@ void prefill_kernel(const PrefillArgs a) {
     __syncthreads();
   }
 
-  // ---- normalise; one split: store.  Several: write this split's partial
-  //      (device-coherent stores), draw a ticket; the last split of the row
-  //      block merges all of them.  Lane (g,n) holds O[row n][dims 16x+4g+i]. ----
-  const bool split = a.KS > 1;
-  const int64_t split_stride = (int64_t)a.total_q * a.Hq;  // rows per split
-  // (only used when split; the host keeps KS * rows * D floats under 2 GiB)
-  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-      a.part_o, 0, split ? (int)(a.KS * split_stride * D * 4) : 0, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
-      a.part_lse, 0, split ? (int)(a.KS * split_stride * 4) : 0, 0x00020000);
+  // ---- normalise and store, or the split's partial and the merge ----
+  float lt[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    float l = l_run[rt] + shfl_xor_f(l_run[rt], 16);
-    l += shfl_xor_f(l, 32);
-    if (!valid[rt]) continue;
-    const int row = wr0 + 16 * rt + n;
-    const int64_t orow_idx = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    if (CASCADE && !split) {
-      float* orow = a.pre_o + orow_idx * D + 4 * g;
-#pragma unroll
-      for (int x = 0; x < P::NX; ++x) *reinterpret_cast<f32x4*>(orow + 16 * x) = o[rt][x] * inv;
-      if (g == 0) a.pre_lse[orow_idx] = l > 0.f ? m_run[rt] + log2f(l) : kNegInf;
-    } else if (!split) {
-      f16* orow = a.out + orow_idx * D + 4 * g;
-#pragma unroll
-      for (int x = 0; x < P::NX; ++x)
-        *reinterpret_cast<f16x4*>(orow + 16 * x) = to16x4<E>(o[rt][x] * inv);
-    } else {
-      // device-coherent stores through one wave-uniform descriptor per array
-      // (the host keeps the partial arrays under 2 GiB)
-      const uint32_t prow = (uint32_t)((int64_t)ks * a.total_q * a.Hq + orow_idx);
-#pragma unroll
-      for (int x = 0; x < P::NX; ++x)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[rt][x] * inv), ro,
-                                               (prow * D + 16 * x + 4 * g) * (uint32_t)sizeof(float),
-                                               0, kSc1);
-      if (g == 0)
-        __builtin_amdgcn_raw_buffer_store_b32(
-            __builtin_bit_cast(uint32_t, l > 0.f ? m_run[rt] + log2f(l) : kNegInf), rl,
-            prow * (uint32_t)sizeof(float), 0, kSc1);
-    }
+    lt[rt] = l_run[rt] + shfl_xor_f(l_run[rt], 16);
+    lt[rt] += shfl_xor_f(lt[rt], 32);
   }
-  if (!split) return;
   __shared__ int last;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials are complete
-  __syncthreads();
-  if (tid == 0)
-    last = __hip_atomic_fetch_add(a.tickets + item * a.Hkv + h, 1, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT) == a.KS - 1;
-  __syncthreads();
-  if (!last) return;
-  if (tid == 0)
-    __hip_atomic_store(a.tickets + item * a.Hkv + h, 0, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  // merge: thread -> (row of the block, 4 consecutive dims).  All KS LSEs and
-  // partial outputs of kMergeRows of the thread's rows are loaded at once
-  // (indices past KS repeat the last split and get weight 0; rows past the
-  // block repeat its last row and are not stored), so the block's rows cost
-  // ceil(rows / (RPS * kMergeRows)) round trips to memory.
-  constexpr int TPR = D / 4;             // threads per row
-  constexpr int RPS = kThreads / TPR;    // rows per pass
-  const int d4 = (tid % TPR) * 4;
-  for (int row0 = r0 + tid / TPR; row0 <= r_last; row0 += RPS * kMergeRows) {
-    float lse[kMergeRows][kMaxSplits];
-    f32x4 ov[kMergeRows][kMaxSplits];
-    int64_t orow_idx[kMergeRows];
-#pragma unroll
-    for (int u = 0; u < kMergeRows; ++u) {
-      const int row = min(row0 + u * RPS, r_last);
-      orow_idx[u] = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
-#pragma unroll
-      for (int k = 0; k < kMaxSplits; ++k) {
-        const int kc = k < a.KS ? k : a.KS - 1;
-        const uint32_t prow = (uint32_t)(kc * split_stride + orow_idx[u]);
-        lse[u][k] = __builtin_bit_cast(
-            float,
-            __builtin_amdgcn_raw_buffer_load_b32(rl, prow * (uint32_t)sizeof(float), 0, kSc1));
-        ov[u][k] = __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       ro, (prow * D + d4) * (uint32_t)sizeof(float), 0, kSc1));
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kMergeRows; ++u) {
-      if (row0 + u * RPS > r_last) break;
-      float M = kNegInf;
-#pragma unroll
-      for (int k = 0; k < kMaxSplits; ++k)
-        if (k < a.KS) M = fmaxf(M, lse[u][k]);
-      f32x4 num = {0.f, 0.f, 0.f, 0.f};
-      float den = 0.f;
-#pragma unroll
-      for (int k = 0; k < kMaxSplits; ++k) {
-        const float wgt = k < a.KS && lse[u][k] != kNegInf ? exp2f(lse[u][k] - M) : 0.f;
-        num += wgt * ov[u][k];
-        den += wgt;
-      }
-      const float inv = den > 0.f ? 1.f / den : 0.f;
-      if constexpr (CASCADE) {
-        *reinterpret_cast<f32x4*>(a.pre_o + orow_idx[u] * D + d4) = num * inv;
-        if (d4 == 0) a.pre_lse[orow_idx[u]] = den > 0.f ? M + log2f(den) : kNegInf;
-      } else {
-        *reinterpret_cast<f16x4*>(a.out + orow_idx[u] * D + d4) = to16x4<E>(num * inv);
-      }
-    }
-  }
+  finish_split<D, RT, E>(a, rb, item, h, ks, wr0, r0, r_last, valid, m_run, lt, o, &last);
 }
 
 // ---------------------------------------------------------------------------
@@ -659,23 +659,20 @@ __device__ __forceinline__ int swz_k(int r) { return D == 128 ? (r & 15) : ((r >
 template <int D>
 __device__ __forceinline__ int swz_v(int r) { return D == 128 ? ((r & 7) << 1) : (((r >> 1) & 3) << 1); }
 
-// Row maxima of scores (finite or -inf, never NaN): v_max3_f32 straight from the
-// MFMA results (fmaxf would first canonicalise every operand, one v_max_f32
-// x, x, x each, under the IEEE mode), and the cross-lane steps with gfx950's
-// permlane swaps (VALU, no LDS round trip).  Each swap returns both halves and
-// both are used: permlane32_swap(x, x) gives lane l the values of lanes l % 32
-// and l % 32 + 32, permlane16_swap(x, x) those of the two 16-lane rows l / 16
-// pairs with.
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-__device__ __forceinline__ float vmax2(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
+// Row maxima of scores (finite or -inf, never NaN): IEEE maximum, which gfx950
+// computes three operands at a time (v_maximum3_f32) straight from the MFMA
+// results -- fmaxf would first canonicalise every operand, one v_max_f32
+// x, x, x each, under the IEEE mode.  Written as the compiler's own operation,
+// not inline asm: an MFMA result read by a VALU instruction needs wait states
+// that the compiler inserts only for instructions it can see (an inline-asm
+// max read a score tile two instructions after its MFMA, before the MFMA had
+// written every lane, and overwrote a register that MFMA was still reading).
+// The cross-lane steps use gfx950's permlane swaps (VALU, no LDS round trip).
+// Each swap returns both halves and both are used: permlane32_swap(x, x) gives
+// lane l the values of lanes l % 32 and l % 32 + 32, permlane16_swap(x, x)
+// those of the two 16-lane rows l / 16 pairs with.
+__device__ __forceinline__ float vmax2(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float vmax3(float a, float b, float c) { return vmax2(vmax2(a, b), c); }
 __device__ __forceinline__ float max_over_lane_rows(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = vmax2(__uint_as_float(a[0]), __uint_as_float(a[1]));
@@ -692,6 +689,13 @@ __device__ __forceinline__ float max16(const float (&v)[4][4]) {
   return vmax2(vmax3(a, b, c), vmax3(d, e, v[3][3]));
 }
 
+// max of the 8 values sv[0..1][4]
+__device__ __forceinline__ float max8(const float (&v)[4][4]) {
+  const float a = vmax3(v[0][0], v[0][1], v[0][2]);
+  const float b = vmax3(v[0][3], v[1][0], v[1][1]);
+  return vmax3(a, b, vmax2(v[1][2], v[1][3]));
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(4))) const int32_t const_i32;
@@ -705,30 +709,152 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t run_rsrc(const f16* base, uint
                                            0x00020000);
 }
 
-// DMA of one wave's 16-key run of block kb (first key t0) into the K and V
-// stages: one buffer descriptor per matrix whose range ends at the run's last
-// key before key_end (later rows arrive as zeros).
-template <int D>
+// DMA of one wave's RUN-key run of block kb (first key t0, RUN dividing 16, so
+// the run lies in one page) into rows RUN * w .. of the K and V stages: one
+// buffer descriptor per matrix whose range ends at the run's last key before
+// key_end (later rows arrive as zeros).
+template <int D, int RUN = 16>
 __device__ __forceinline__ void dma_run(const PrefillArgs& a, int h, int w, int t0, int key_end,
                                         int id, const uint32_t* voff_k, const uint32_t* voff_v,
-                                        unsigned char* kst, unsigned char* vst) {
+                                        unsigned char* kst, unsigned char* vst, int wv = -1) {
   using P = DCfg<D>;
+  static_assert(16 % RUN == 0 && RUN % P::RPI == 0, "whole DMA instructions within a page");
   const int rs = a.Hkv * D * 2;
   int nv = key_end - t0;
-  nv = nv < 0 ? 0 : (nv > 16 ? 16 : nv);
+  nv = nv < 0 ? 0 : (nv > RUN ? RUN : nv);
   const uint32_t nrec = nv > 0 ? (uint32_t)((nv - 1) * rs + D * 2) : 0u;
   const int64_t row0 = (int64_t)id * a.BS + (t0 & (a.BS - 1));
   const int64_t off = row0 * a.Hkv * D + h * D;
   const __amdgpu_buffer_rsrc_t rk = run_rsrc(a.k_pool + off, nrec);
   const __amdgpu_buffer_rsrc_t rv = run_rsrc(a.v_pool + off, nrec);
-  unsigned char* kl = kst + 16 * w * P::ROWB;
-  unsigned char* vl = vst + 16 * w * P::ROWB;
+  unsigned char* kl = kst + RUN * w * P::ROWB;
+  unsigned char* vl = vst + RUN * (wv < 0 ? w : wv) * P::ROWB;  // V rows: run wv, if given
 #pragma unroll
-  for (int i = 0; i < P::NI; ++i) {
+  for (int i = 0; i < RUN / P::RPI; ++i) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(kl + i * P::RPI * P::ROWB), 16,
                                              voff_k[i], 0, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(vl + i * P::RPI * P::ROWB), 16,
                                              voff_v[i], 0, 0, 0);
+  }
+}
+
+// NKT 16-key tiles of a staged 64-key block for a wave's RT 16-row tiles (the
+// stream-K kernel's step: the whole block; the cascade prefix kernel's: one
+// half, NKT = 2, kbase and koff moved to key 32 for the second, vbase at
+// that half's V rows):
+// S^T = K.Q^T with v_mfma_f32_16x16x32, base-2 online softmax with the lazy
+// rescale (the causal mask only on blocks at or past unmasked_blocks: key
+// kb * 64 + koff + j is masked past the row's pos), P as fp16 / bf16,
+// O^T += V^T.P^T, and the row sums from a tile of ones (every element of
+// lsum[rt] is the row's sum of P).  A move by 32 keys keeps the chunk
+// swizzles (they depend on the key row mod 16, or mod 32 halved).
+template <int D, int RT, class E, int NKT = 4>
+__device__ __forceinline__ void dma_block(int kb, const unsigned char* kbase,
+                                          const unsigned char* vbase, int unmasked_blocks,
+                                          float scale_log2, const f16x8 (&qv)[RT][DCfg<D>::NC],
+                                          const int (&pos)[RT], float (&m_run)[RT],
+                                          f32x4 (&lsum)[RT], f32x4 (&o)[RT][DCfg<D>::NX],
+                                          int koff = 0) {
+  static_assert(NKT == 4 || NKT == 2, "a whole block or one half");
+  constexpr int NPS = NKT / 2;  // 32-key PV steps
+  using P = DCfg<D>;
+  const int lane = lane_id();
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const f16 one = to16<E>(1.f);
+  const f16x8 ones = {one, one, one, one, one, one, one, one};
+  // K fragments (16 keys x 32 dims, A operand): all reads issued ahead of
+  // the MFMAs that use them
+  f16x8 kf[NKT][P::NC];
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+    for (int c = 0; c < P::NC; ++c)
+      kf[kt][c] = *reinterpret_cast<const f16x8*>(
+          kbase + (16 * kt + n) * P::ROWB + (((4 * c + g) ^ swz_k<D>(16 * kt + n)) * 16));
+  // one row tile: the scheduler would otherwise interleave the reads with the
+  // MFMAs to save registers, and each MFMA would wait for its read
+  if constexpr (RT == 1) __builtin_amdgcn_sched_barrier(0);
+  f32x4 st[RT][NKT];
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) st[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+    for (int c = 0; c < P::NC; ++c)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) st[rt][kt] = mma32<E>(kf[kt][c], qv[rt][c], st[rt][kt]);
+  // V fragments (transposing reads): lane (g, n) of a read addresses V[key
+  // 32ps + 4g + n/4][dims 16x + 4(n%4) .. +3] (and the same 16 keys further
+  // for the second half of the k = 32 operand; 32ps and 16 keep the row's
+  // swizzle).  The first 32 keys' fragments are read before the softmax,
+  // whose VALU work hides their latency.
+  const int vrow = 4 * g + (n >> 2);
+  const int vswz = swz_v<D>(vrow);
+  auto vfrag = [&](int ps, int x) __attribute__((always_inline)) {
+    const unsigned char* vb = vbase + (32 * ps + vrow) * P::ROWB + (n & 1) * 8;
+    const unsigned char* vh = vbase + (32 * ps + 16 + vrow) * P::ROWB + (n & 1) * 8;
+    const int slot = (2 * x + ((n & 3) >> 1)) ^ vswz;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + slot * 16));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vh + slot * 16));
+    const f16x4 l4 = __builtin_bit_cast(f16x4, lo), h4 = __builtin_bit_cast(f16x4, hi);
+    return f16x8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+  };
+  f16x8 vf[P::NX];
+#pragma unroll
+  for (int x = 0; x < P::NX; ++x) vf[x] = vfrag(0, x);
+
+  const bool need_mask = kb >= unmasked_blocks;  // wave-uniform
+  f16x8 pb[RT][NPS];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    float sv[4][4];
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[kt][i] = st[rt][kt][i];
+    if (need_mask) {
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (kb * kDmaKeys + koff + 16 * kt + 4 * g + i > pos[rt]) sv[kt][i] = kNegInf;
+    }
+    const float mx = max_over_lane_rows(NKT == 4 ? max16(sv) : max8(sv)) * scale_log2;
+    if (__ballot(mx > m_run[rt] + kRescaleSlack)) {  // wave-uniform
+      const float m_new = fmaxf(m_run[rt], mx);
+      const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run[rt] - m_new);
+      lsum[rt] *= alpha;
+#pragma unroll
+      for (int x = 0; x < P::NX; ++x) o[rt][x] *= alpha;
+      m_run[rt] = m_new;
+    }
+    const float neg_m = m_run[rt] == kNegInf ? 0.f : -m_run[rt];
+#pragma unroll
+    for (int ps = 0; ps < NPS; ++ps) {
+      f16x8 p;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          p[4 * kt + i] =
+              to16<E>(exp2_fast(__builtin_fmaf(sv[2 * ps + kt][i], scale_log2, neg_m)));
+      pb[rt][ps] = p;
+    }
+  }
+#pragma unroll
+  for (int ps = 0; ps < NPS; ++ps) {
+#pragma unroll
+    for (int x = 0; x < P::NX; ++x) {
+      const f16x8 va = vf[x];
+      if (ps + 1 < NPS) vf[x] = vfrag(ps + 1, x);  // the next 32 keys' fragment, in flight meanwhile
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) o[rt][x] = mma32<E>(va, pb[rt][ps], o[rt][x]);
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) lsum[rt] = mma32<E>(ones, pb[rt][ps], lsum[rt]);
   }
 }
 
@@ -1234,100 +1360,9 @@ __device__ __forceinline__ void run_units(const PrefillArgs& a, const StreamPlan
     }
 
     // ---- one block: S^T = K.Q^T, online softmax, O^T += V^T.P^T ----
-    const f16 one = to16<E>(1.f);
-    const f16x8 ones = {one, one, one, one, one, one, one, one};
     auto compute = [&](int kb, const unsigned char* kbase,
                        const unsigned char* vbase) __attribute__((always_inline)) {
-      // K fragments (16 keys x 32 dims, A operand): all reads issued ahead of
-      // the MFMAs that use them
-      f16x8 kf[4][P::NC];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int c = 0; c < P::NC; ++c)
-          kf[kt][c] = *reinterpret_cast<const f16x8*>(
-              kbase + (16 * kt + n) * P::ROWB + (((4 * c + g) ^ swz_k<D>(16 * kt + n)) * 16));
-      f32x4 st[RT][4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) st[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int c = 0; c < P::NC; ++c)
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) st[rt][kt] = mma32<E>(kf[kt][c], qv[rt][c], st[rt][kt]);
-      // V fragments (transposing reads): lane (g, n) of a read addresses V[key
-      // 32ps + 4g + n/4][dims 16x + 4(n%4) .. +3] (and the same 16 keys further
-      // for the second half of the k = 32 operand; 32ps and 16 keep the row's
-      // swizzle).  The first 32 keys' fragments are read before the softmax,
-      // whose VALU work hides their latency.
-      const int vrow = 4 * g + (n >> 2);
-      const int vswz = swz_v<D>(vrow);
-      auto vfrag = [&](int ps, int x) __attribute__((always_inline)) {
-        const unsigned char* vb = vbase + (32 * ps + vrow) * P::ROWB + (n & 1) * 8;
-        const unsigned char* vh = vbase + (32 * ps + 16 + vrow) * P::ROWB + (n & 1) * 8;
-        const int slot = (2 * x + ((n & 3) >> 1)) ^ vswz;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + slot * 16));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vh + slot * 16));
-        const f16x4 l4 = __builtin_bit_cast(f16x4, lo), h4 = __builtin_bit_cast(f16x4, hi);
-        return f16x8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
-      };
-      f16x8 vf[P::NX];
-#pragma unroll
-      for (int x = 0; x < P::NX; ++x) vf[x] = vfrag(0, x);
-
-      const bool need_mask = kb >= unmasked_blocks;  // wave-uniform
-      f16x8 pb[RT][2];
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        float sv[4][4];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sv[kt][i] = st[rt][kt][i];
-        if (need_mask) {
-#pragma unroll
-          for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (kb * kDmaKeys + 16 * kt + 4 * g + i > pos[rt]) sv[kt][i] = kNegInf;
-        }
-        const float mx = max_over_lane_rows(max16(sv)) * a.scale_log2;
-        if (__ballot(mx > m_run[rt] + kRescaleSlack)) {  // wave-uniform
-          const float m_new = fmaxf(m_run[rt], mx);
-          const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run[rt] - m_new);
-          lsum[rt] *= alpha;
-#pragma unroll
-          for (int x = 0; x < P::NX; ++x) o[rt][x] *= alpha;
-          m_run[rt] = m_new;
-        }
-        const float neg_m = m_run[rt] == kNegInf ? 0.f : -m_run[rt];
-#pragma unroll
-        for (int ps = 0; ps < 2; ++ps) {
-          f16x8 p;
-#pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              p[4 * kt + i] =
-                  to16<E>(exp2_fast(__builtin_fmaf(sv[2 * ps + kt][i], a.scale_log2, neg_m)));
-          pb[rt][ps] = p;
-        }
-      }
-#pragma unroll
-      for (int ps = 0; ps < 2; ++ps) {
-#pragma unroll
-        for (int x = 0; x < P::NX; ++x) {
-          const f16x8 va = vf[x];
-          if (ps == 0) vf[x] = vfrag(1, x);  // the next 32 keys' fragment, in flight meanwhile
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) o[rt][x] = mma32<E>(va, pb[rt][ps], o[rt][x]);
-        }
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) lsum[rt] = mma32<E>(ones, pb[rt][ps], lsum[rt]);
-      }
+      dma_block<D, RT, E>(kb, kbase, vbase, unmasked_blocks, a.scale_log2, qv, pos, m_run, lsum, o);
     };
 
     // ---- pipeline: the DMA of the half's next block (kb + 2) runs while block
@@ -1653,6 +1688,260 @@ void prefill_dma_kernel(const PrefillArgs a) {
                                     v01, xml, last, plan_digest);
 }
 
+// ---------------------------------------------------------------------------
+// prefix_dma_kernel: the cascade prefix pass on LDS DMA (block sizes that are
+// multiples of 16)
+// ---------------------------------------------------------------------------
+//
+// The tile kernel's cascade work split -- workgroup i: (KV head, key split)
+// pair i % P, 64-row block i / P of a group -- with the stream-K kernel's key
+// staging and block step.  The group's prefix arrives in 64-key blocks (each
+// wave brings an 8-key run by LDS DMA) in a ring of kPfxStages stages, so three
+// blocks are in flight while one is computed.  Eight waves, two per SIMD: wave
+// r of half H computes rows 16r .. 16r + 15 over keys 32H .. 32H + 31 of every
+// block (dma_block on half a block), so the two waves of a SIMD share its
+// MFMA and VALU time and hide each other's latencies; at the end the halves'
+// states of the same rows meet in LDS.  Each key split writes its normalised
+// output and base-2 LSE into its own slot of the prefix result (slot ks of
+// query-head row r at r * KS + ks): the decode launch after it folds a row's
+// adjacent slots into its own-key attention, so no split merge runs here.
+//
+// Measured at C3 against a first form with four waves (one per SIMD, whole
+// blocks): 20.2 us, of which 8.8 us in the eight-block loop -- per block a
+// wave spent ~0.78 us computing (0.23 us of it MFMA) and ~0.17 us issuing its
+// DMA, with no second wave to cover either -- and ~4 us of split merge in the
+// 48 merging workgroups.
+constexpr int kPfxStages = 4;
+constexpr int kPfxThreads = 2 * kThreads;  // two halves of four waves
+constexpr int kPfxRun = 8;                 // keys of a block each wave brings in
+
+// s_waitcnt operand that waits until at most n vector-memory operations of
+// the wave are in flight (they complete in issue order); expcnt and lgkmcnt at
+// their maxima, i.e. not waited for.  Issued through the builtin, the compiler
+// sees the wait: it knows the LDS DMA of a stage being read has completed and
+// adds no wait of its own before the reads.
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(vm_wait(N));
+}
+constexpr int kWaitVm0 = vm_wait(0);
+
+template <int D, class E>
+__global__ __launch_bounds__(kPfxThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefix_dma_kernel(const PrefillArgs a) {
+  using P = DCfg<D>;
+  constexpr int RT = 1;
+  constexpr int ROWS = kWaves * 16;                    // 64 rows: wave r of each half owns 16
+  constexpr int VM_BLOCK = 2 * kPfxRun / P::RPI;       // DMA instructions of one wave per block
+  static_assert(kPfxStages == 4, "the step sequence below names four stages");
+  static_assert(2 * kWaves * kPfxRun == kDmaKeys, "the eight runs cover a block");
+  static_assert(2 * P::NX * kWave * 16 <= P::MAT && 2 * kWaves * kWave * 4 <= P::MAT / 2,
+                "two waves' tiles per K stage object; the maxima and sums in a V one");
+  // one LDS object per stage and matrix, V split by half (keys 0-31 and
+  // 32-63): the compiler's wait for an LDS DMA before an LDS read is then
+  // limited to reads of the object it fills (half 1's V reads at an offset
+  // of 32 rows in a whole-block object were not told apart from the DMA into
+  // the other stages, and waited for all of it)
+  __shared__ __align__(16) unsigned char k0[P::MAT];
+  __shared__ __align__(16) unsigned char k1[P::MAT];
+  __shared__ __align__(16) unsigned char k2[P::MAT];
+  __shared__ __align__(16) unsigned char k3[P::MAT];
+  __shared__ __align__(16) unsigned char vl0[P::MAT / 2];
+  __shared__ __align__(16) unsigned char vh0[P::MAT / 2];
+  __shared__ __align__(16) unsigned char vl1[P::MAT / 2];
+  __shared__ __align__(16) unsigned char vh1[P::MAT / 2];
+  __shared__ __align__(16) unsigned char vl2[P::MAT / 2];
+  __shared__ __align__(16) unsigned char vh2[P::MAT / 2];
+  __shared__ __align__(16) unsigned char vl3[P::MAT / 2];
+  __shared__ __align__(16) unsigned char vh3[P::MAT / 2];
+
+  // the last workgroup of the grid writes the suffix starts (read by the
+  // decode launch after this one), beside the others' work
+  if (blockIdx.x == gridDim.x - 1) {
+    typedef __attribute__((address_space(3))) int32_t lds_i32;
+    if (a.S + 1 <= (int)(P::MAT / sizeof(int32_t))) {
+      // the offsets staged in a stage buffer (one round trip), searched there
+      lds_i32* offs = (lds_i32*)(int32_t*)k0;
+      for (int i = threadIdx.x; i <= a.S; i += blockDim.x) offs[i] = a.q_off[i];
+      __syncthreads();
+      write_suffix_starts(a, offs);
+    } else {
+      write_suffix_starts(a, a.q_off);
+    }
+    return;
+  }
+  const int npair = a.Hkv * a.KS;
+  const int item = blockIdx.x / npair;
+  const int pair = blockIdx.x - item * npair;
+  RowBlock rb;
+  if (!locate_rows<ROWS, true>(a, item, rb)) return;
+  const int h = pair % a.Hkv;
+  const int ks = pair / a.Hkv;
+  const int G = a.G;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int H = w / kWaves;  // half: keys 32H .. 32H + 31 of each block
+  const int r = w % kWaves;  // row tile
+  const int lane = lane_id();
+  const int g = lane >> 4;
+  const int n = lane & 15;
+
+  const int total_rows = rb.n * G;
+  const int r0 = rb.rb * ROWS;
+  const int r_last = min(r0 + ROWS, total_rows) - 1;
+  const int key_end = rb.ctx;  // the group's prefix (whole blocks)
+  const int nblocks_all = (key_end + kDmaKeys - 1) / kDmaKeys;
+  const int per_split = (nblocks_all + a.KS - 1) / a.KS;
+  const int kb_lo = min(ks * per_split, nblocks_all);
+  const int nb = min(kb_lo + per_split, nblocks_all) - kb_lo;  // this split's blocks
+  const int wr0 = r0 + r * 16;
+  const bool has_rows = wr0 <= r_last;
+  const int32_t* trow = a.tables + (int64_t)rb.q0 * a.W;  // the group's first row
+
+  // pool block of this wave's run of blocks base .. base + 63 (lane j: block
+  // base + j; pages past the table repeat its last entry, unused)
+  auto load_ids = [&](int base) __attribute__((always_inline)) {
+    int page = ((base + lane) * kDmaKeys + kPfxRun * w) >> a.bs_log2;
+    page = page < a.W ? page : a.W - 1;
+    return trow[page];
+  };
+  int kb_base = kb_lo;
+  int idv = load_ids(kb_lo);
+
+  // this lane's row: query vector (B operand) and last key it may see (the
+  // prefix end, or -1 for a row whose context does not pass the prefix)
+  f16x8 qv[RT][P::NC];
+  int pos[RT];
+  bool valid[RT];
+  {
+    const int row = wr0 + n;
+    valid[0] = row < total_rows;
+    const int rc = valid[0] ? row : r_last;
+    const int L = member_len(a, rb.q0 + rc / G);
+    pos[0] = valid[0] && L > rb.ctx ? rb.ctx - 1 : -1;
+    const f16* qrow = a.q + (int64_t)(rb.q0 + rc / G) * a.q_stride + (h * G + rc % G) * D + 8 * g;
+#pragma unroll
+    for (int c = 0; c < P::NC; ++c) {
+      const f16x8 v = ld16(qrow + 32 * c);
+      qv[0][c] = valid[0] ? v : f16x8{};
+    }
+  }
+  // blocks whose last key is <= every row's position of the wave need no mask
+  const int pos_lo = -wave_max_i(-(valid[0] ? min(pos[0], rb.ctx) : rb.ctx));
+  const int unmasked_blocks = __builtin_amdgcn_readfirstlane((pos_lo + 1) / kDmaKeys);
+
+  float m_run[RT] = {kNegInf};
+  f32x4 lsum[RT] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+  f32x4 o[RT][P::NX];
+#pragma unroll
+  for (int x = 0; x < P::NX; ++x) o[0][x] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int rs = a.Hkv * D * 2;  // pool bytes from one key row to the next
+  // loop-invariant DMA lane offsets: key rr of the wave's run lands on K row
+  // 8w + rr and on V row 8r + rr of the half's object; the chunk swizzles
+  // take those rows
+  uint32_t voff_k[P::NI], voff_v[P::NI];
+#pragma unroll
+  for (int i = 0; i < P::NI; ++i) {
+    const int rr = P::RPI * i + lane / P::CPR;
+    const int sl = lane % P::CPR;
+    voff_k[i] = (uint32_t)(rr * rs + (sl ^ swz_k<D>(kPfxRun * w + rr)) * 16);
+    voff_v[i] = (uint32_t)(rr * rs + (sl ^ swz_v<D>(kPfxRun * r + rr)) * 16);
+  }
+  // wave w brings keys 8w .. 8w + 7 of block kb: K rows 8w of the stage, V
+  // rows 8r of the half's V object
+  auto issue = [&](int kb, unsigned char* kst, unsigned char* vlo,
+                   unsigned char* vhi) __attribute__((always_inline)) {
+    const int id = clamp_block(__builtin_amdgcn_readlane(idv, kb - kb_base), a.NB);
+    dma_run<D, kPfxRun>(a, h, w, kb * kDmaKeys + kPfxRun * w, key_end, id, voff_k, voff_v, kst,
+                        H == 0 ? vlo : vhi, r);
+  };
+
+  // the ids, the row's context length and the queries in one round trip;
+  // then the first kPfxStages - 1 blocks
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  if (nb > 0) issue(kb_lo, k0, vl0, vh0);
+  if (nb > 1) issue(kb_lo + 1, k1, vl1, vh1);
+  if (nb > 2) issue(kb_lo + 2, k2, vl2, vh2);
+
+  // step j: block kb_lo + j sits in stage j % 4; once every wave's run of it
+  // has landed and every wave is done with block j - 1, block j + 3 goes into
+  // the stage block j - 1 used
+  auto step = [&](int j, const unsigned char* kc, const unsigned char* vlc,
+                  const unsigned char* vhc, unsigned char* kn, unsigned char* vln,
+                  unsigned char* vhn) __attribute__((always_inline)) {
+    if (j + 2 < nb) wait_vm<2 * VM_BLOCK>();  // blocks j + 1 and j + 2 stay in flight
+    else if (j + 1 < nb) wait_vm<VM_BLOCK>();
+    else wait_vm<0>();
+    // a bare barrier: __syncthreads()'s release fence would also wait for the
+    // DMA of blocks j + 1 and j + 2.  The wait above has put this wave's run
+    // of block j in LDS; LDS operations of a wave complete in order, and the
+    // compiler fences keep every LDS access on its side of the barrier.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (j + 3 < nb) {
+      if (j + 3 - (kb_base - kb_lo) >= kWave) {
+        // the next 64 blocks' ids (splits past 61 blocks only): the wait is
+        // an s_waitcnt the compiler sees, so no path that skips this load
+        // carries a pending load into the readlane below
+        kb_base = kb_lo + j + 3;
+        idv = load_ids(kb_base);
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      }
+      issue(kb_lo + j + 3, kn, vln, vhn);
+    }
+    // the half's keys: K at a constant offset of the stage object, V in the
+    // half's own object
+    if (has_rows) {
+      if (H == 0)
+        dma_block<D, RT, E, 2>(kb_lo + j, kc, vlc, unmasked_blocks, a.scale_log2, qv, pos, m_run,
+                               lsum, o, 0);
+      else
+        dma_block<D, RT, E, 2>(kb_lo + j, kc + 32 * P::ROWB, vhc, unmasked_blocks, a.scale_log2,
+                               qv, pos, m_run, lsum, o, 32);
+    }
+  };
+  for (int j = 0; j < nb; j += 4) {
+    step(j, k0, vl0, vh0, k3, vl3, vh3);
+    if (j + 1 < nb) step(j + 1, k1, vl1, vh1, k0, vl0, vh0);
+    if (j + 2 < nb) step(j + 2, k2, vl2, vh2, k1, vl1, vh1);
+    if (j + 3 < nb) step(j + 3, k3, vl3, vh3, k2, vl2, vh2);
+  }
+
+  // ---- the halves' states of the same rows meet in the idle stages (tiles
+  //      of waves 0-1 in k0, 2-3 in k1, maxima and sums in vl0): half 1
+  //      parks, half 0 combines and writes the split's slot ----
+  __syncthreads();  // every wave is done with the stages
+  float* xo = reinterpret_cast<float*>(r < 2 ? k0 : k1) + (r & 1) * P::NX * kWave * 4;
+  float* xm = reinterpret_cast<float*>(vl0) + r * 2 * kWave;
+  if (H == 1) {
+#pragma unroll
+    for (int x = 0; x < P::NX; ++x)
+      *reinterpret_cast<f32x4*>(xo + (x * kWave + lane) * 4) = o[0][x];
+    xm[lane] = m_run[0];
+    xm[kWave + lane] = lsum[0][0];
+  }
+  __syncthreads();
+  if (H == 1 || !valid[0]) return;
+  const float pm = xm[lane];
+  const float mm = fmaxf(m_run[0], pm);
+  const float a0 = m_run[0] == kNegInf ? 0.f : exp2_fast(m_run[0] - mm);
+  const float a1 = pm == kNegInf ? 0.f : exp2_fast(pm - mm);
+  const float l = a0 * lsum[0][0] + a1 * xm[kWave + lane];
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const int row = wr0 + n;
+  const int64_t slot_row =
+      ((int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G) * a.KS + ks;
+  float* orow = a.pre_o + slot_row * D + 4 * g;
+#pragma unroll
+  for (int x = 0; x < P::NX; ++x)
+    *reinterpret_cast<f32x4*>(orow + 16 * x) =
+        (a0 * o[0][x] + a1 * *reinterpret_cast<const f32x4*>(xo + (x * kWave + lane) * 4)) * inv;
+  if (g == 0) a.pre_lse[slot_row] = l > 0.f ? mm + log2f(l) : kNegInf;
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline int log2_exact(int x) {
   if (x <= 0 || (x & (x - 1))) return -1;
@@ -1661,10 +1950,10 @@ inline int log2_exact(int x) {
   return l;
 }
 
-template <int D, int RT, bool CASCADE = false, class E = Fp16>
+template <int D, int RT, class E = Fp16>
 void launch_prefill(const PrefillArgs& a, int blocks, hipStream_t stream) {
   using P = PCfg<D, RT>;
-  hipLaunchKernelGGL((prefill_kernel<D, RT, CASCADE, E>), dim3(blocks * a.Hkv * a.KS),
+  hipLaunchKernelGGL((prefill_kernel<D, RT, E>), dim3(blocks * a.Hkv * a.KS),
                      dim3(kThreads), 2 * P::STAGE, stream, a);
 }
 
@@ -1890,11 +2179,11 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
     if (head_dim == 64) launch_prefill_dma<64, Fp16>(a, s); else launch_prefill_dma<128, Fp16>(a, s);
   } else if (bf16) {
     if (head_dim == 64) {
-      if (p.rt == 2) launch_prefill<64, 2, false, Bf16>(a, p.blocks, s);
-      else launch_prefill<64, 1, false, Bf16>(a, p.blocks, s);
+      if (p.rt == 2) launch_prefill<64, 2, Bf16>(a, p.blocks, s);
+      else launch_prefill<64, 1, Bf16>(a, p.blocks, s);
     } else {
-      if (p.rt == 2) launch_prefill<128, 2, false, Bf16>(a, p.blocks, s);
-      else launch_prefill<128, 1, false, Bf16>(a, p.blocks, s);
+      if (p.rt == 2) launch_prefill<128, 2, Bf16>(a, p.blocks, s);
+      else launch_prefill<128, 1, Bf16>(a, p.blocks, s);
     }
   } else if (head_dim == 64) {
     if (p.rt == 2) launch_prefill<64, 2>(a, p.blocks, s); else launch_prefill<64, 1>(a, p.blocks, s);
@@ -2021,9 +2310,14 @@ size_t cascade_prefix_scratch_bytes(int num_groups, int batch, int hq, int hkv, 
   return align256(rows * d * sizeof(float)) + align256(rows * sizeof(float));
 }
 
-int cascade_prefix_launch(const CascadePrefix& c, hipStream_t stream) {
+int cascade_prefix_launch(CascadePrefix& c, hipStream_t stream) {
+  // prefix_dma_kernel: 64-row blocks, each 8-key run of a 64-key block in one
+  // page (the shared-prefix decode takes block sizes that are multiples of 16)
+  if (c.bs % 16 != 0) return FE_ERR_UNSUPPORTED;
   const Plan p = plan(c.num_groups, c.batch, c.hq, c.hkv);
-  if ((int64_t)p.blocks * c.hkv > kMaxTickets) return FE_ERR_UNSUPPORTED;
+  const int blocks =
+      (int)(((int64_t)c.batch * (c.hq / c.hkv) + kWaves * 16 - 1) / (kWaves * 16)) + c.num_groups;
+  if ((int64_t)blocks * c.hkv * p.ks + 1 >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
   if ((int64_t)c.num_blocks * c.bs >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
   if (!(c.scale > 0.f)) return FE_ERR_INVALID_ARGUMENT;  // row max on unscaled scores
   PrefillArgs a;
@@ -2035,11 +2329,9 @@ int cascade_prefix_launch(const CascadePrefix& c, hipStream_t stream) {
   a.tables = c.tables;
   a.q_off = c.group_offsets;
   a.ctx = c.ctx;
-  a.tickets = c.tickets;
-  const size_t rows = (size_t)p.ks * c.batch * c.hq;
-  a.part_o = (float*)c.scratch;
-  a.part_lse = p.ks > 1 ? (float*)((char*)c.scratch + align256(rows * c.d * sizeof(float)))
-                        : nullptr;
+  a.tickets = nullptr;
+  a.part_o = nullptr;
+  a.part_lse = nullptr;
   a.q_stride = c.q_stride;
   a.W = c.table_stride;
   a.S = c.num_groups;
@@ -2054,23 +2346,28 @@ int cascade_prefix_launch(const CascadePrefix& c, hipStream_t stream) {
   a.nwg_max = 0;
   a.scale_log2 = c.scale * kLog2e;
   a.prefix_len = c.prefix_len;
-  a.pre_o = c.pre_o;
-  a.pre_lse = c.pre_lse;
   a.tok0 = c.tok0;
-  if (c.bf16) {
-    if (c.d == 64) {
-      if (p.rt == 2) launch_prefill<64, 2, true, Bf16>(a, p.blocks, stream);
-      else launch_prefill<64, 1, true, Bf16>(a, p.blocks, stream);
-    } else {
-      if (p.rt == 2) launch_prefill<128, 2, true, Bf16>(a, p.blocks, stream);
-      else launch_prefill<128, 1, true, Bf16>(a, p.blocks, stream);
-    }
-  } else if (c.d == 64) {
-    if (p.rt == 2) launch_prefill<64, 2, true>(a, p.blocks, stream);
-    else launch_prefill<64, 1, true>(a, p.blocks, stream);
+  // every key split writes its own slot (the decode launch folds them in):
+  // one slot fits pre_o / pre_lse, several the key-split scratch
+  if (p.ks > 1) {
+    const size_t rows = (size_t)p.ks * c.batch * c.hq;
+    a.pre_o = (float*)c.scratch;
+    a.pre_lse = (float*)((char*)c.scratch + align256(rows * c.d * sizeof(float)));
   } else {
-    if (p.rt == 2) launch_prefill<128, 2, true>(a, p.blocks, stream);
-    else launch_prefill<128, 1, true>(a, p.blocks, stream);
+    a.pre_o = c.pre_o;
+    a.pre_lse = c.pre_lse;
+  }
+  c.out_o = a.pre_o;
+  c.out_lse = a.pre_lse;
+  c.splits = p.ks;
+  const dim3 grid(blocks * a.Hkv * a.KS + 1);  // + the suffix-start workgroup
+  const dim3 block(kPfxThreads);
+  if (c.bf16) {
+    if (c.d == 64) hipLaunchKernelGGL((prefix_dma_kernel<64, Bf16>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((prefix_dma_kernel<128, Bf16>), grid, block, 0, stream, a);
+  } else {
+    if (c.d == 64) hipLaunchKernelGGL((prefix_dma_kernel<64, Fp16>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((prefix_dma_kernel<128, Fp16>), grid, block, 0, stream, a);
   }
   return FE_LAUNCH_STATUS();
 }
