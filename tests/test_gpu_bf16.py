@@ -252,6 +252,16 @@ def test_bf16_shared_prefix_c3_shape():
     close_bf16(got, exp, "bf16 cascade C3 (2x8)")
 
 
+def test_bf16_shared_prefix_long_prefix():
+    """A 20000-token prefix in bf16: the prefix pass's splits cross the
+    mid-pipeline block-id reload."""
+    w = to_bf16(workloads.shared_prefix_workload(23, [(3, 20000)], singles=1, hq=12, hkv=2,
+                                                 d=128, tail=(1, 200)))
+    got, _ = _shared_prefix(w, fuse=False)
+    exp, _, _ = oracle_decode(w)
+    close_bf16(got, exp, "bf16 cascade, 20000-token prefix")
+
+
 @pytest.mark.parametrize("hq,hkv,d,bs", [(12, 2, 128, 16), (14, 2, 64, 32)])
 def test_bf16_shared_prefix_edge_groups(hq, hkv, d, bs):
     """Groups of 3 (prefix of 40 tokens: whole blocks only), 1 and 0 members and one of

@@ -407,6 +407,20 @@ def test_shared_prefix_full_c3_against_plain_decode_and_repeatable():
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
 
 
+@pytest.mark.parametrize("hq,hkv,d,bs", [(12, 2, 128, 16), (8, 1, 64, 32)])
+def test_shared_prefix_long_prefixes_cross_the_block_id_reload(hq, hkv, d, bs):
+    """Prefixes of 20000 and 17000 tokens: each of the prefix pass's four key
+    splits holds more than 61 blocks of 64 keys, so every wave reloads its
+    block ids in mid-pipeline (the next 64 blocks' ids); one member's context
+    ends inside its prefix and one row has none."""
+    groups = [(3, 20000), (2, 17000)]
+    w = workloads.shared_prefix_workload(31 + d, groups, singles=1, hq=hq, hkv=hkv, d=d,
+                                         block_size=bs, tail=(1, 200), member_lens={4: 9000})
+    got, _ = run_shared_prefix(w)
+    exp, _, _ = oracle_decode(w)
+    assert_attention_close(got.numpy(), exp, what=f"long prefixes {hq}/{hkv}/{d} bs{bs}")
+
+
 # --------------------------------------------------------------------------------------
 # large batches: the plain decode (piece kernel) at 160 and 2048 rows, and the
 # shared-prefix decode, whose suffix pass runs the balanced kernel from 128 rows
