@@ -53,6 +53,9 @@ SIGNATURES: dict[str, tuple] = {
     "fe_paged_decode_shared_prefix_bf16": (_i, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i, _p, _i,
                                                 _p, _p, _p, _i, _p, _sz, _i, _i, _i, _i, _i, _f,
                                                 _i, _p]),
+    "fe_paged_decode_shared_prefix_f32": (_i, [_p, _i64, _p, _p, _p, _i64, _p, _p, _i, _p, _i,
+                                               _p, _p, _p, _i, _p, _sz, _i, _i, _i, _i, _i, _f,
+                                               _i, _p]),
     "fe_lse_merge": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),
     "fe_lse_merge_bf16": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),
     "fe_prefill_paged": (_i, [_p, _p, _p, _p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _i,

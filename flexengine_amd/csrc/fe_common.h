@@ -402,6 +402,7 @@ struct CascadePrefix {
   int32_t* tok0;     // [batch]
   void* scratch;     // key-split partials, cascade_prefix_scratch_bytes
   bool bf16;         // q and the pools are bfloat16 (fp16 otherwise)
+  bool f32;          // q and the pools are float32
   // set by cascade_prefix_launch: the prefix result the decode launch folds
   // into every row with a shared prefix -- `splits` slots per query-head row
   // r (row-major: the slots of a row are adjacent), slot s a normalised

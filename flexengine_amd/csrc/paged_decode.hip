@@ -1418,8 +1418,9 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
                 bool f32 = false) {
   FE_CHECK_ARG(batch >= 0 && num_q_heads > 0 && kv_heads > 0 && num_blocks > 0 &&
                table_stride > 0 && target_splits >= 0);
-  // fp32 pools: the unplanned piece kernel only (no plan, no shared prefix)
-  if (f32 && (plan != nullptr || cascade != nullptr)) return FE_ERR_UNSUPPORTED;
+  // fp32 pools: the unplanned piece kernel only (no plan; a shared-prefix call
+  // runs its suffix pass on the piece kernel too)
+  if (f32 && plan != nullptr) return FE_ERR_UNSUPPORTED;
   if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
   FE_CHECK_ARG(num_q_heads % kv_heads == 0);
   const int G = num_q_heads / kv_heads;
@@ -1499,7 +1500,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     a.plan = (int*)plan;
     set_plan_key(a);
   }
-  if (cascade) {
+  if (cascade && !f32) {  // the balanced kernel has 16-bit forms only
     const BalancedPlan bp =
         head_dim == 64 ? plan_balanced<64>(batch, kv_heads, G, block_size, max_len, need)
                        : plan_balanced<128>(batch, kv_heads, G, block_size, max_len, need);
@@ -1527,6 +1528,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     c.bs = block_size;
     c.scale = scale;
     c.bf16 = bf16;
+    c.f32 = f32;
     c.tok0 = (int32_t*)cw;
     cw += align256((size_t)batch * sizeof(int32_t));
     c.pre_o = (float*)cw;
@@ -1685,13 +1687,13 @@ int shared_prefix_impl(const void* q, int64_t q_batch_stride, void* out, const v
                        const int32_t* group_prefix_lens, int num_groups, void* workspace,
                        size_t workspace_bytes, int batch, int num_q_heads, int kv_heads,
                        int head_dim, int block_size, float scale, int target_splits,
-                       fe_stream_t stream, bool bf16) {
+                       fe_stream_t stream, bool bf16, bool f32 = false) {
   FE_CHECK_ARG(num_groups >= 0 && num_groups <= batch + 1);
   if (num_groups == 0 || batch == 0)
     return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
                        num_blocks, block_tables, table_stride, context_lens, workspace,
                        workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
-                       target_splits, nullptr, (hipStream_t)stream, nullptr, 0, bf16);
+                       target_splits, nullptr, (hipStream_t)stream, nullptr, 0, bf16, f32);
   FE_CHECK_ARG(group_offsets && group_prefix_lens);
   CascadePrefix c{};
   c.group_offsets = group_offsets;
@@ -1700,7 +1702,7 @@ int shared_prefix_impl(const void* q, int64_t q_batch_stride, void* out, const v
   return decode_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
                      num_blocks, block_tables, table_stride, context_lens, workspace,
                      workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size, scale,
-                     target_splits, &c, (hipStream_t)stream, nullptr, 0, bf16);
+                     target_splits, &c, (hipStream_t)stream, nullptr, 0, bf16, f32);
 }
 
 }  // namespace
@@ -1731,6 +1733,20 @@ extern "C" int fe_paged_decode_shared_prefix_bf16(
                             group_offsets, group_prefix_lens, num_groups, workspace,
                             workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size,
                             scale, target_splits, stream, true);
+}
+
+extern "C" int fe_paged_decode_shared_prefix_f32(
+    const void* q, int64_t q_batch_stride, void* out, const void* k_new, const void* v_new,
+    int64_t new_batch_stride, void* k_pool, void* v_pool, int num_blocks,
+    const int32_t* block_tables, int table_stride, const int32_t* context_lens,
+    const int32_t* group_offsets, const int32_t* group_prefix_lens, int num_groups,
+    void* workspace, size_t workspace_bytes, int batch, int num_q_heads, int kv_heads,
+    int head_dim, int block_size, float scale, int target_splits, fe_stream_t stream) {
+  return shared_prefix_impl(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool,
+                            v_pool, num_blocks, block_tables, table_stride, context_lens,
+                            group_offsets, group_prefix_lens, num_groups, workspace,
+                            workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size,
+                            scale, target_splits, stream, false, true);
 }
 
 // ---------------------------------------------------------------------------

@@ -546,20 +546,33 @@ void prefill_kernel(const PrefillArgs a) {
 // (F32Core: fp32 products on v_mfma_f32_16x16x4_f32, fp32 softmax), every
 // column masking the keys past its own position, then normalises and stores
 // its 16 rows: no LDS, no key splits.
-template <int D, bool LIST>
+//
+// CASCADE: the prefix pass of the fp32 shared-prefix decode.  "Sequence" s is
+// a group of decode rows (locate_rows' cascade mode), every row reads the
+// group's whole-block prefix from the group's first table row (none for a row
+// whose context does not pass it), and the result is one prefix slot per
+// (row, query head): the normalised output in pre_o and its base-2 LSE in
+// pre_lse; the grid's last workgroup writes the suffix starts.
+template <int D, bool LIST, bool CASCADE = false>
 __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs a) {
   constexpr int ROWS = kWaves * 16;
+  if constexpr (CASCADE) {
+    if (blockIdx.x == gridDim.x - 1) {
+      write_suffix_starts(a, a.q_off);
+      return;
+    }
+  }
   const int item = blockIdx.x / a.Hkv;
   const int h = blockIdx.x - item * a.Hkv;
   RowBlock rb;
-  if (!locate_rows<ROWS, false>(a, item, rb)) return;
+  if (!locate_rows<ROWS, CASCADE>(a, item, rb)) return;
   const int G = a.G;
   const int lane = lane_id();
   const int g = lane >> 4;
   const int n = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int total_rows = rb.n * G;
-  const int cached = rb.ctx >= rb.n ? rb.ctx - rb.n : 0;
+  const int cached = CASCADE ? 0 : (rb.ctx >= rb.n ? rb.ctx - rb.n : 0);
   const int wr0 = rb.rb * ROWS + 16 * w;
   if (wr0 >= total_rows) return;
   const int r_last = min(wr0 + 16, total_rows) - 1;
@@ -572,15 +585,20 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs
   core.v_pool = reinterpret_cast<const float*>(a.v_pool);
   core.k_pool_w = nullptr;
   core.v_pool_w = nullptr;
-  core.trow = a.tables + (int64_t)rb.s * a.W;
+  core.trow = a.tables + (int64_t)(CASCADE ? rb.q0 : rb.s) * a.W;
   core.rs = a.Hkv * D;
   core.hoff = h * D;
   core.W = a.W;
   core.NB = a.NB;
   core.BS = a.BS;
   core.bs_log2 = a.bs_log2;
-  core.tok_end = cached + r_last / G + 1;  // the wave's last row reads the most keys
-  core.limit = valid ? cached + rc / G + 1 : 0;
+  if constexpr (CASCADE) {
+    core.tok_end = rb.ctx;  // the group's prefix
+    core.limit = valid && member_len(a, rb.q0 + rc / G) > rb.ctx ? rb.ctx : 0;
+  } else {
+    core.tok_end = cached + r_last / G + 1;  // the wave's last row reads the most keys
+    core.limit = valid ? cached + rc / G + 1 : 0;
+  }
   core.scale_log2 = a.scale_log2;
   core.knew_row = nullptr;
   core.vnew_row = nullptr;
@@ -597,10 +615,18 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs
   const float l = core.l_total();
   const float inv = l > 0.f ? 1.f / l : 0.f;
   if (valid) {
-    const int64_t orow = ((int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G) * D + 4 * g;
+    const int64_t r = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
+    if constexpr (CASCADE) {
+      float* orow = a.pre_o + r * D + 4 * g;
 #pragma unroll
-    for (int x = 0; x < F32Core<D, LIST>::NX; ++x)
-      store_out4<F32>(a.out, orow + 16 * x, core.o[x] * inv);
+      for (int x = 0; x < F32Core<D, LIST>::NX; ++x)
+        *reinterpret_cast<f32x4*>(orow + 16 * x) = core.o[x] * inv;
+      if (g == 0) a.pre_lse[r] = l > 0.f ? core.m_run + log2f(l) : kNegInf;
+    } else {
+#pragma unroll
+      for (int x = 0; x < F32Core<D, LIST>::NX; ++x)
+        store_out4<F32>(a.out, r * D + 4 * g + 16 * x, core.o[x] * inv);
+    }
   }
 }
 
@@ -2356,6 +2382,21 @@ int cascade_prefix_launch(CascadePrefix& c, hipStream_t stream) {
   } else {
     a.pre_o = c.pre_o;
     a.pre_lse = c.pre_lse;
+  }
+  if (c.f32) {
+    // fp32: the fp32 prefill kernel's cascade mode, one slot per row
+    a.KS = 1;
+    a.pre_o = c.pre_o;
+    a.pre_lse = c.pre_lse;
+    c.out_o = a.pre_o;
+    c.out_lse = a.pre_lse;
+    c.splits = 1;
+    const dim3 grid(blocks * a.Hkv + 1);  // + the suffix-start workgroup
+    if (c.d == 64)
+      hipLaunchKernelGGL((prefill_f32_kernel<64, true, true>), grid, dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((prefill_f32_kernel<128, true, true>), grid, dim3(kThreads), 0, stream, a);
+    return FE_LAUNCH_STATUS();
   }
   c.out_o = a.pre_o;
   c.out_lse = a.pre_lse;

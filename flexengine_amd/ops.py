@@ -381,12 +381,10 @@ def paged_decode_shared_prefix(q: torch.Tensor, k_pool: torch.Tensor, v_pool: to
     blocks at the start of row group_offsets[s]'s table, shared by every member.
     Same result as paged_decode: the shared keys are attended once per group,
     the private suffixes per row, merged by log-sum-exp (fe_paged_decode_shared_prefix,
-    or its _bf16 form for bfloat16 q and pools).
+    or its _bf16 / _f32 form for bfloat16 / float32 q and pools).
     """
     (dev, nb, bs, hkv, d, batch, hq, block_tables, context_lens, new_stride, out,
      scale) = _decode_args(q, k_pool, v_pool, block_tables, context_lens, scale, k_new, v_new, out)
-    if q.dtype not in DTYPES_16:
-        raise ValueError("the shared-prefix decode takes fp16 or bf16 pools")
     group_offsets = _int32(group_offsets, "group_offsets")
     group_prefix_lens = _int32(group_prefix_lens, "group_prefix_lens")
     if group_offsets.ndim != 1 or group_prefix_lens.ndim != 1 or \
@@ -401,8 +399,8 @@ def paged_decode_shared_prefix(q: torch.Tensor, k_pool: torch.Tensor, v_pool: to
         workspace = decode_workspace(dev, need)
     elif workspace.numel() * workspace.element_size() < need:
         raise ValueError(f"workspace too small: need {need} bytes")
-    sfx = "_bf16" if q.dtype == BF16 else ""
-    _lib.call("fe_paged_decode_shared_prefix" + sfx, q.data_ptr(), q.stride(0), out.data_ptr(),
+    _lib.call("fe_paged_decode_shared_prefix" + _SFX[q.dtype], q.data_ptr(), q.stride(0),
+              out.data_ptr(),
               _ptr(k_new), _ptr(v_new), new_stride, k_pool.data_ptr(), v_pool.data_ptr(), nb,
               block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(),
               group_offsets.data_ptr(), group_prefix_lens.data_ptr(), ngroups,

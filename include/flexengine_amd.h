@@ -406,6 +406,26 @@ int fe_paged_decode_shared_prefix_bf16(const void* q, int64_t q_batch_stride, vo
                                        fe_stream_t stream);
 
 /*
+ * fp32 form of fe_paged_decode_shared_prefix: the same arguments, workspace
+ * and results with q, out, the pools and the new rows in float32 (the prefix
+ * pass on the fp32 matrix-core engine of fe_prefill_paged_f32, the suffix
+ * decode on fe_paged_decode_f32's, fp32 softmax and merge).  Replaces the same
+ * route for the float32 caches the reference allocates by default
+ * (allocator.py:26; runtime.py:37-40 builds the cache in the model's dtype).
+ */
+int fe_paged_decode_shared_prefix_f32(const void* q, int64_t q_batch_stride, void* out,
+                                      const void* k_new, const void* v_new,
+                                      int64_t new_batch_stride, void* k_pool, void* v_pool,
+                                      int num_blocks, const int32_t* block_tables,
+                                      int table_stride, const int32_t* context_lens,
+                                      const int32_t* group_offsets,
+                                      const int32_t* group_prefix_lens, int num_groups,
+                                      void* workspace, size_t workspace_bytes,
+                                      int batch, int num_q_heads, int kv_heads, int head_dim,
+                                      int block_size, float scale, int target_splits,
+                                      fe_stream_t stream);
+
+/*
  * Log-sum-exp merge of split attention results:
  *   LSE[r]   = log(sum_s exp(part_lse[s, r]))
  *   out[r,:] = sum_s exp(part_lse[s, r] - LSE[r]) * part_out[s, r, :]

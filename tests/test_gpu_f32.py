@@ -1,5 +1,5 @@
-"""GPU: float32 forms -- the KV page movers, the decode and the prefill -- against
-the oracle.
+"""GPU: float32 forms -- the KV page movers, the decode, the prefill and the
+shared-prefix decode -- against the oracle.
 
 The reference's PagedKVCache defaults to float32 (allocator.py:26), the engine
 builds the cache in the model's dtype, float32 among them (runtime.py:37-40,
@@ -261,17 +261,59 @@ def test_f32_cache_reference_case_noncontiguous_pages(length):
     close_f32(got, exp, f"prefill length {length}")
 
 
-def test_f32_forms_without_a_plan_or_shared_prefix_refuse():
-    """fp32 pools have no plan and no shared-prefix form (the C ABI has no such entry
-    points); ops refuses them before launching anything."""
+def test_f32_decode_plan_refuses():
+    """fp32 pools have no decode plan (the C ABI has no planned fp32 entry point);
+    ops refuses one before launching anything."""
     w = _decode_cases()[0]
     d = w.to(DEV)
     nb, bs, hkv = d.k_pool.shape[0], d.k_pool.shape[1], d.k_pool.shape[2]
     plan = ops.paged_decode_plan(d.block_tables, d.context_lens, nb, hkv, bs)
     with pytest.raises(ValueError, match="fp32"):
         ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens, plan=plan)
-    go = torch.tensor([0, w.batch], dtype=torch.int32, device=DEV)
-    pl = torch.tensor([16], dtype=torch.int32, device=DEV)
-    with pytest.raises(ValueError, match="fp16 or bf16"):
-        ops.paged_decode_shared_prefix(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens,
-                                       go, pl)
+
+
+# --------------------------------------------------------------------------------------
+# shared-prefix decode (fe_paged_decode_shared_prefix_f32): the prefix pass on the fp32
+# prefill engine, the suffixes on the fp32 piece kernel, merged in fp32
+# --------------------------------------------------------------------------------------
+
+def _shared_prefix(w: workloads.DecodeWorkload, fuse: bool = False):
+    d = w.to(DEV)
+    out = ops.paged_decode_shared_prefix(
+        d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens,
+        d.meta["group_offsets"].to(DEV), d.meta["prefix_lens"].to(DEV),
+        k_new=d.k_new if fuse else None, v_new=d.v_new if fuse else None)
+    torch.cuda.synchronize()
+    return out, d
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", [(12, 2, 128, 16), (14, 2, 64, 32), (8, 1, 128, 16)])
+def test_f32_shared_prefix_edge_groups(hq, hkv, d, bs):
+    """Groups of 3 (prefix 40 tokens: whole blocks only), 1 and 0 members, a group of
+    5 with one member ending at the prefix, one inside it and one inactive, and rows
+    outside every group."""
+    groups = [(3, 40), (1, 64), (0, 32), (5, 512)]
+    w = to_f32(workloads.shared_prefix_workload(41 + d, groups, singles=3, hq=hq, hkv=hkv, d=d,
+                                                block_size=bs,
+                                                member_lens={5: 512, 6: 505, 7: 0}), 42 + d)
+    got, _ = _shared_prefix(w)
+    exp, _, _ = oracle_decode(w)
+    close_f32(got, exp, f"fp32 cascade edges {hq}/{hkv}/{d} bs{bs}")
+    assert not got[7].any(), "inactive member must give exact zeros"
+
+
+def test_f32_shared_prefix_with_page_write_and_long_prefix():
+    """C3-like groups with the fused page write (pools bit-exact after the call), then
+    a 20000-token prefix; the cascade agrees with the plain fp32 decode."""
+    w = to_f32(workloads.shared_prefix_workload(12, [(6, 256), (4, 1024)], singles=2,
+                                                with_new_kv=True), 43)
+    got, d = _shared_prefix(w, fuse=True)
+    exp, kp, vp = oracle_decode(w)
+    close_f32(got, exp, "fp32 cascade with page write")
+    assert np.array_equal(d.k_pool.cpu().numpy(), kp) and np.array_equal(d.v_pool.cpu().numpy(), vp)
+    w = to_f32(workloads.shared_prefix_workload(44, [(3, 20000)], singles=1, tail=(1, 200)), 45)
+    got, d = _shared_prefix(w)
+    exp, _, _ = oracle_decode(w)
+    close_f32(got, exp, "fp32 cascade, 20000-token prefix")
+    plain = ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens)
+    close_f32(got, plain.cpu().numpy().astype(np.float64), "fp32 cascade vs plain")
