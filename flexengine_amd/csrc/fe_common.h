@@ -418,6 +418,47 @@ __attribute__((visibility("hidden"))) size_t cascade_prefix_scratch_bytes(int nu
 __attribute__((visibility("hidden"))) int cascade_prefix_launch(CascadePrefix& c,
                                                                 hipStream_t stream);
 
+// ---- generic attention (attn_generic.hip): the shapes the matrix-core kernels
+// do not take -- head_dim other than 64 / 128, or more than 16 query heads per
+// KV head.  A decode row attends keys 0 .. ctx[row] - 1 of table row `row`,
+// cut into `splits` key ranges (more than one: normalised partial outputs and
+// base-2 LSEs in part_o [rows * hq][splits][d] / part_lse [rows * hq][splits],
+// folded by a second launch); a prefill token (q_offsets != null) of sequence
+// s attends keys 0 .. cached + its index, cached = ctx[s] - n_s (0 when
+// ctx[s] < n_s).  Rows with no keys give zeros. ----
+constexpr int kGenericMaxHeadDim = 512;
+constexpr int kGenericMaxGroup = 32;    // query heads per KV head
+constexpr int kGenericMaxElems = 4096;  // group size * head_dim
+struct GenericAttn {
+  const void* q;
+  int64_t q_stride;    // elements between consecutive query rows
+  void* out;
+  int64_t out_stride;  // elements between consecutive output rows
+  const void* k_new;   // decode page write at key ctx[row] - 1 (null: none)
+  const void* v_new;
+  int64_t new_stride;
+  void* k_pool;
+  void* v_pool;
+  int num_blocks;
+  const int32_t* tables;
+  int table_stride;
+  const int32_t* ctx;
+  const int32_t* q_offsets;  // prefill: [num_seqs + 1]; null for a decode
+  int num_seqs;
+  int rows;  // decode: batch; prefill: total_q
+  int hq, hkv, d, bs;
+  float scale;
+  int elem;  // 0 fp16, 1 bf16, 2 fp32
+  int splits;  // decode key splits per row (<= 32)
+  float* part_o;
+  float* part_lse;
+};
+// head_dim rounded up to a multiple of 8 (the kernel's LDS rows)
+__attribute__((visibility("hidden"))) int generic_padded_dims(int d);
+__attribute__((visibility("hidden"))) bool generic_shape(int hq, int hkv, int d);
+__attribute__((visibility("hidden"))) int generic_attention(const GenericAttn& g,
+                                                            hipStream_t stream);
+
 }  // namespace fe
 
 #define FE_CHECK_ARG(cond)                 \

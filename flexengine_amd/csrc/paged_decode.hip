@@ -28,6 +28,7 @@
 // columns), so every K/V byte is read from HBM once per step; the reference's
 // Triton kernel reads it G times, once per query head
 // (src/flexengine/inference/kernels/paged_attention.py:99-139).
+#include <algorithm>
 #include <mutex>
 
 #include "attn_core.h"
@@ -1392,17 +1393,114 @@ int launch_decode(const DecodeArgs& a, hipStream_t stream) {
 
 }  // namespace
 
+// The generic kernel's split partials: [batch * hq][splits] outputs and LSEs
+inline size_t generic_ws_bytes(int batch, int hq, int d, int splits) {
+  return align256((size_t)batch * hq * splits * d * sizeof(float)) +
+         align256((size_t)batch * hq * splits * sizeof(float));
+}
+constexpr int kGenericWsSplits = 16;  // splits per row the workspace size allows for
+
 extern "C" size_t fe_paged_decode_workspace_size(int batch, int num_q_heads, int head_dim,
                                                  int max_context, int target_splits) {
   if (batch < 0 || num_q_heads <= 0 || head_dim <= 0 || max_context < 0 || target_splits < 0)
     return 0;
   // sized for the largest default (kv_heads = 1): valid for every kv_heads
   const int target = effective_target(batch, 1, max_context, target_splits);
-  return kTicketBytes + ws_o_bytes(batch, num_q_heads, head_dim, target) +
-         ws_lse_bytes(batch, num_q_heads, target);
+  const size_t pieces = kTicketBytes + ws_o_bytes(batch, num_q_heads, head_dim, target) +
+                        ws_lse_bytes(batch, num_q_heads, target);
+  // head dims other than 64 / 128 run on the generic kernel: room for its splits
+  if (head_dim != 64 && head_dim != 128) {
+    const size_t gen =
+        kTicketBytes + generic_ws_bytes(batch, num_q_heads, head_dim, kGenericWsSplits);
+    return gen > pieces ? gen : pieces;
+  }
+  return pieces;
 }
 
 namespace {
+
+bool aligned_to(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+constexpr int generic_max_splits = 32;
+constexpr int kGenericWorkgroups = 2048;  // the generic decode's default launch size
+
+// Shapes the matrix-core decode does not take (head_dim other than 64 / 128,
+// or more than 16 query heads per KV head): the generic kernel, no plan.  Each
+// row's keys are cut into as many splits as fit the workspace region the
+// piece partials would use ((target + batch) rows of partials: 1 + target /
+// batch splits per row, at most 32 and one per 64 keys of the table width).
+// A shared-prefix call lands here as a plain decode: every row attends its own
+// table, whose first pages are the shared ones, so the result is the same.
+int decode_generic(const void* q, int64_t q_batch_stride, void* out, const void* k_new,
+                   const void* v_new, int64_t new_batch_stride, void* k_pool, void* v_pool,
+                   int num_blocks, const int32_t* block_tables, int table_stride,
+                   const int32_t* context_lens, void* workspace, size_t workspace_bytes,
+                   int batch, int num_q_heads, int kv_heads, int head_dim, int block_size,
+                   float scale, int target_splits, hipStream_t stream, bool planned, int elem) {
+  if (!generic_shape(num_q_heads, kv_heads, head_dim) || planned) return FE_ERR_UNSUPPORTED;
+  if (log2_exact(block_size) < 0) return FE_ERR_UNSUPPORTED;
+  // key indices and pool rows (block * block_size + offset) are 32-bit in the kernel
+  if ((int64_t)table_stride * block_size >= ((int64_t)1 << 31) ||
+      (int64_t)num_blocks * block_size >= ((int64_t)1 << 31))
+    return FE_ERR_UNSUPPORTED;
+  if (batch == 0) return FE_OK;
+  FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && context_lens);
+  FE_CHECK_ARG((k_new == nullptr) == (v_new == nullptr));
+  const size_t el = elem == 2 ? 4 : 2;
+  FE_CHECK_ARG(q_batch_stride >= (int64_t)num_q_heads * head_dim);
+  FE_CHECK_ARG(aligned_to(q, el) && aligned_to(out, el) && aligned_to(k_pool, el) &&
+               aligned_to(v_pool, el));
+  if (k_new) {
+    FE_CHECK_ARG(new_batch_stride >= (int64_t)kv_heads * head_dim && aligned_to(k_new, el) &&
+                 aligned_to(v_new, el));
+  }
+  const int max_len = table_stride * block_size;
+  const int target = effective_target(batch, kv_heads, max_len, target_splits);
+  const size_t need = fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, max_len, target);
+  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+    return FE_ERR_WORKSPACE;
+  // key splits per row: about kGenericWorkgroups workgroups in all (or
+  // target_splits per KV head when given), no more than one per 64 keys of the
+  // table width, and as many as the workspace holds
+  const int64_t want = target_splits > 0 ? (int64_t)target_splits * kv_heads : kGenericWorkgroups;
+  int64_t splits = (want + (int64_t)batch * kv_heads - 1) / ((int64_t)batch * kv_heads);
+  splits = std::min<int64_t>(splits, generic_max_splits);
+  splits = std::min<int64_t>(splits, (max_len + 63) / 64);
+  while (splits > 1 &&
+         kTicketBytes + generic_ws_bytes(batch, num_q_heads, head_dim, (int)splits) > workspace_bytes)
+    --splits;
+  if (splits < 1) splits = 1;
+  GenericAttn g{};
+  g.splits = (int)splits;
+  // past the split-K tickets, which the other decode kernels need at zero and
+  // this one leaves alone
+  char* const parts = (char*)workspace + kTicketBytes;
+  g.part_o = (float*)parts;
+  g.part_lse =
+      (float*)(parts + align256((size_t)batch * num_q_heads * splits * head_dim * sizeof(float)));
+  g.q = q;
+  g.q_stride = q_batch_stride;
+  g.out = out;
+  g.out_stride = (int64_t)num_q_heads * head_dim;
+  g.k_new = k_new;
+  g.v_new = v_new;
+  g.new_stride = new_batch_stride;
+  g.k_pool = k_pool;
+  g.v_pool = v_pool;
+  g.num_blocks = num_blocks;
+  g.tables = block_tables;
+  g.table_stride = table_stride;
+  g.ctx = context_lens;
+  g.q_offsets = nullptr;
+  g.num_seqs = batch;
+  g.rows = batch;
+  g.hq = num_q_heads;
+  g.hkv = kv_heads;
+  g.d = head_dim;
+  g.bs = block_size;
+  g.scale = scale;
+  g.elem = elem;
+  return generic_attention(g, stream);
+}
 
 // Everything fe_paged_decode and fe_paged_decode_shared_prefix share: argument
 // checks, workspace carving and the decode launch.  `cascade` (null for plain
@@ -1421,10 +1519,13 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   // fp32 pools: the unplanned piece kernel only (no plan; a shared-prefix call
   // runs its suffix pass on the piece kernel too)
   if (f32 && plan != nullptr) return FE_ERR_UNSUPPORTED;
-  if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
   FE_CHECK_ARG(num_q_heads % kv_heads == 0);
   const int G = num_q_heads / kv_heads;
-  if (G > kMaxGroup) return FE_ERR_UNSUPPORTED;
+  if ((head_dim != 64 && head_dim != 128) || G > kMaxGroup)
+    return decode_generic(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
+                          num_blocks, block_tables, table_stride, context_lens, workspace,
+                          workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size,
+                          scale, target_splits, stream, plan != nullptr, bf16 ? 1 : (f32 ? 2 : 0));
   if ((int64_t)batch * kv_heads > kMaxTickets) return FE_ERR_UNSUPPORTED;
   const int bs_log2 = log2_exact(block_size);
   if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;

@@ -2092,6 +2092,50 @@ extern "C" size_t fe_prefill_workspace_size(int num_seqs, int total_q, int num_q
 
 namespace {
 
+bool aligned_to(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+
+// head_dim other than 64 / 128: the generic kernel (one workgroup per token and
+// KV head, causal over the sequence's cached keys and the chunk up to the
+// token), no workspace and no plan.
+int prefill_generic(const void* q, void* out, const void* k_pool, const void* v_pool,
+                    int num_blocks, const int32_t* block_tables, int table_stride,
+                    const int32_t* q_offsets, const int32_t* context_lens, int num_seqs,
+                    int total_q, int num_q_heads, int kv_heads, int head_dim, int block_size,
+                    float scale, hipStream_t stream, bool planned, int elem) {
+  if (!generic_shape(num_q_heads, kv_heads, head_dim) || planned) return FE_ERR_UNSUPPORTED;
+  if (log2_exact(block_size) < 0) return FE_ERR_UNSUPPORTED;
+  // key indices and pool rows (block * block_size + offset) are 32-bit in the kernel
+  if ((int64_t)table_stride * block_size >= ((int64_t)1 << 31) ||
+      (int64_t)num_blocks * block_size >= ((int64_t)1 << 31))
+    return FE_ERR_UNSUPPORTED;
+  if (num_seqs == 0 || total_q == 0) return FE_OK;
+  FE_CHECK_ARG(q && out && k_pool && v_pool && block_tables && q_offsets && context_lens);
+  const size_t el = elem == 2 ? 4 : 2;
+  FE_CHECK_ARG(aligned_to(q, el) && aligned_to(out, el) && aligned_to(k_pool, el) &&
+               aligned_to(v_pool, el));
+  GenericAttn g{};
+  g.q = q;
+  g.q_stride = (int64_t)num_q_heads * head_dim;
+  g.out = out;
+  g.out_stride = g.q_stride;
+  g.k_pool = const_cast<void*>(k_pool);
+  g.v_pool = const_cast<void*>(v_pool);
+  g.num_blocks = num_blocks;
+  g.tables = block_tables;
+  g.table_stride = table_stride;
+  g.ctx = context_lens;
+  g.q_offsets = q_offsets;
+  g.num_seqs = num_seqs;
+  g.rows = total_q;
+  g.hq = num_q_heads;
+  g.hkv = kv_heads;
+  g.d = head_dim;
+  g.bs = block_size;
+  g.scale = scale;
+  g.elem = elem;
+  return generic_attention(g, stream);
+}
+
 // fe_prefill_paged and its bf16 form: argument checks, workspace carving, launch.
 int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_pool, int num_blocks,
                  const int32_t* block_tables, int table_stride, const int32_t* q_offsets,
@@ -2101,8 +2145,12 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
                  void* step_plan = nullptr, size_t plan_bytes = 0, bool f32 = false) {
   FE_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 &&
                kv_heads > 0 && num_blocks > 0 && table_stride > 0);
-  if (head_dim != 64 && head_dim != 128) return FE_ERR_UNSUPPORTED;
   FE_CHECK_ARG(num_q_heads % kv_heads == 0);
+  if (head_dim != 64 && head_dim != 128)
+    return prefill_generic(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride,
+                           q_offsets, context_lens, num_seqs, total_q, num_q_heads, kv_heads,
+                           head_dim, block_size, scale, (hipStream_t)stream,
+                           step_plan != nullptr, bf16 ? 1 : (f32 ? 2 : 0));
   const int bs_log2 = log2_exact(block_size);
   if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
   // pool rows (block * block_size + offset) are 32-bit in the kernel

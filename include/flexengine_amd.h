@@ -22,8 +22,16 @@
  *       covers, INCLUDING the token being decoded.  0 marks an inactive row,
  *       whose output is exact zeros (paged_attention.py:131,138).
  *
- * Supported shapes: head_dim in {64, 128}; num_q_heads a multiple of
- * kv_heads with a group size of at most 16; block_size a power of two.
+ * Supported shapes: num_q_heads a multiple of kv_heads; block_size a power
+ * of two.  head_dim 64 and 128 with a decode group (num_q_heads / kv_heads)
+ * of at most 16 run on the matrix-core kernels, as does the prefill at any
+ * group size.  Every other head_dim from 1 to 512, and decode groups of 17
+ * to 32, run on a generic kernel (one workgroup per query row and KV head,
+ * fp32 arithmetic) as long as group * head_dim <= 4096: same entry points,
+ * same results to the same tolerances, no workspace used, no plan taken
+ * (the _planned calls return FE_ERR_UNSUPPORTED there), and a shared-prefix
+ * decode attends each row over its own table.  The KV page movers need
+ * head_dim % 8 == 0 (fp16 / bf16) or % 4 == 0 (fp32).
  * Element types: fp16 (the unsuffixed entry points), bfloat16 (_bf16) and
  * fp32 (_f32: the KV movers, the decode and the prefill).
  */

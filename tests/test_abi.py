@@ -68,13 +68,31 @@ def test_version_and_error_strings(lib):
 def test_host_side_validation_rejects_before_launch(lib):
     """Invalid configurations return an error code without touching the GPU."""
     null = None
-    # head_dim 96 is not built
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    # head_dim 1024 is past the generic kernel's 512
     rc = lib.fe_paged_decode(null, 0, null, null, null, 0, null, null, 1, null, 1, null, null, 0,
-                             1, 12, 2, 96, 16, 0.1, 0, null)
+                             1, 12, 2, 1024, 16, 0.1, 0, null)
     assert rc == _lib.FE_ERR_UNSUPPORTED
-    # group size 32 > 16
+    # group size 64 > 32; group 32 x head_dim 192 > 4096 elements
+    rc = lib.fe_paged_decode(null, 0, null, null, null, 0, null, null, 1, null, 1, null, null, 0,
+                             1, 64, 1, 128, 16, 0.1, 0, null)
+    assert rc == _lib.FE_ERR_UNSUPPORTED
+    rc = lib.fe_paged_decode(null, 0, null, null, null, 0, null, null, 1, null, 1, null, null, 0,
+                             1, 32, 1, 192, 16, 0.1, 0, null)
+    assert rc == _lib.FE_ERR_UNSUPPORTED
+    # the generic shapes (head_dim 96, group 32) take no plan; without one their null
+    # pointers are the error
+    rc = lib.fe_paged_decode_planned(null, 0, null, null, null, 0, null, null, 1, null, 1, null,
+                                     null, 0, 1, 12, 2, 96, 16, 0.1, 0, fake, 0, null)
+    assert rc == _lib.FE_ERR_UNSUPPORTED
     rc = lib.fe_paged_decode(null, 0, null, null, null, 0, null, null, 1, null, 1, null, null, 0,
                              1, 32, 1, 128, 16, 0.1, 0, null)
+    assert rc == _lib.FE_ERR_INVALID_ARGUMENT
+    rc = lib.fe_prefill_paged(null, null, null, null, 1, null, 1, null, null, 1, 1, 1, 12, 2, 96,
+                              16, 0.1, null, 0, null)
+    assert rc == _lib.FE_ERR_INVALID_ARGUMENT
+    rc = lib.fe_prefill_paged(null, null, null, null, 1, null, 1, null, null, 1, 1, 1, 2, 1, 520,
+                              16, 0.1, null, 0, null)
     assert rc == _lib.FE_ERR_UNSUPPORTED
     # block size not a power of two
     rc = lib.fe_paged_decode(null, 0, null, null, null, 0, null, null, 1, null, 1, null, null, 0,

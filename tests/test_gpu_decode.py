@@ -241,8 +241,8 @@ def test_lse_merge_entry_point():
 
 
 def test_error_codes_surface_as_exceptions():
-    q = torch.zeros(1, 12, 96, dtype=torch.float16, device=DEV)
-    pool = torch.zeros(4, 16, 2, 96, dtype=torch.float16, device=DEV)
+    q = torch.zeros(1, 12, 1024, dtype=torch.float16, device=DEV)
+    pool = torch.zeros(4, 16, 2, 1024, dtype=torch.float16, device=DEV)
     t = torch.zeros(1, 1, dtype=torch.int32, device=DEV)
     c = torch.ones(1, dtype=torch.int32, device=DEV)
     with pytest.raises(RuntimeError, match="unsupported"):
