@@ -30,6 +30,8 @@
 // new row from k_new / v_new directly.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "attn_core.h"
 #include "flexengine_amd.h"
 
@@ -38,13 +40,12 @@ using namespace fe;
 namespace {
 
 #ifndef GEN_WAVES
-#define GEN_WAVES 2
+#define GEN_WAVES 3
 #endif
 constexpr int kGThreads = 256;
 constexpr int kGWaves = kGThreads / kWave;
 constexpr int kGMaxRows = 64;     // query rows of one item (tokens x group)
 constexpr int kGRowStep = 4;      // rows scored per pass over a key's row
-constexpr int kGMaxQuads = 4;     // output quads per thread: rows x padded dims <= 4096
 constexpr int kGPre = 4;          // prefetched 16-byte K (and V) vectors per thread: a row holds <= 4 x (256 / CK)
 constexpr int kGMaxSplits = 32;   // decode key splits per row
 
@@ -130,6 +131,55 @@ __device__ __forceinline__ void lds8(const unsigned char* p, float (&x)[8]) {
   }
 }
 
+// sum_i a[i] * b[i] + c over 8 16-bit elements, four fp32 dot products of pairs
+// (v_dot2_f32_f16 / v_dot2_f32_bf16)
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+template <class E>
+__device__ __forceinline__ float dot8(f16x8 a, f16x8 b, float c) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const h2_t x = h2_t{a[2 * i], a[2 * i + 1]};
+    const h2_t y = h2_t{b[2 * i], b[2 * i + 1]};
+    if constexpr (__is_same(E, Bf16))
+      c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2_t, x), __builtin_bit_cast(b2_t, y), c,
+                                          false);
+    else
+      c = __builtin_amdgcn_fdot2(x, y, c, false);
+  }
+  return c;
+}
+
+// c + a.x * b.x + a.y * b.y for a pair of 16-bit elements in one dword each
+template <class E>
+__device__ __forceinline__ float dot2w(uint32_t a, uint32_t b, float c) {
+  if constexpr (__is_same(E, Bf16))
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2_t, a), __builtin_bit_cast(b2_t, b), c,
+                                           false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a), __builtin_bit_cast(h2_t, b), c, false);
+}
+
+// o + p * V over one unit of the product pass, for 4 consecutive dims at
+// vcol: fp32, key m (p an fp32, V rows of DP floats); 16-bit, keys 2m and
+// 2m + 1 (p a pair of E, V pair rows of 2 DP elements, dim-major within a
+// pair, so a dword holds both keys' element of one dim)
+template <class E>
+__device__ __forceinline__ f32x4 pv_unit(const unsigned char* prow, const unsigned char* vcol,
+                                         int m, int DP, f32x4 o) {
+  if constexpr (kIsF32<E>) {
+    const float p = reinterpret_cast<const float*>(prow)[m];
+    return o + p * *reinterpret_cast<const f32x4*>(vcol + m * DP * 4);
+  } else {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const uint32_t pp = reinterpret_cast<const uint32_t*>(prow)[m];
+    const u32x4 v = *reinterpret_cast<const u32x4*>(vcol + m * DP * 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = dot2w<E>(pp, v[e], o[e]);
+    return o;
+  }
+}
+
 // 4 consecutive LDS elements of type E as floats
 template <class E>
 __device__ __forceinline__ f32x4 lds4(const unsigned char* p) {
@@ -141,13 +191,56 @@ __device__ __forceinline__ f32x4 lds4(const unsigned char* p) {
   }
 }
 
+// v[u] combined (op) over the CK lanes of this lane's segment, for RS values
+// at once, every lane of the segment getting the result: DPP row operations
+// within 16 lanes (quad swaps, then the 8- and 16-lane mirrors), across the
+// four rows of the wave with readlane (CK = 64), or xor shuffles (CK = 32).
+template <int CK, int RS, class Op>
+__device__ __forceinline__ void seg_reduce(float (&v)[RS], Op op) {
+  auto dppf = [](auto ctrl, float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl)::value,
+                                           0xF, 0xF, false));
+  };
+  if constexpr (CK == 32) {
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) {
+#pragma unroll
+      for (int u = 0; u < RS; ++u) v[u] = op(v[u], shfl_xor_f(v[u], m));
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < RS; ++u)
+      v[u] = op(v[u], dppf(std::integral_constant<int, dpp::kQuadXor1>{}, v[u]));
+#pragma unroll
+    for (int u = 0; u < RS; ++u)
+      v[u] = op(v[u], dppf(std::integral_constant<int, dpp::kQuadXor2>{}, v[u]));
+#pragma unroll
+    for (int u = 0; u < RS; ++u)
+      v[u] = op(v[u], dppf(std::integral_constant<int, dpp::kRowHalfMirror>{}, v[u]));
+    if constexpr (CK >= 16) {
+#pragma unroll
+      for (int u = 0; u < RS; ++u)
+        v[u] = op(v[u], dppf(std::integral_constant<int, dpp::kRowMirror>{}, v[u]));
+    }
+    if constexpr (CK == 64) {
+      auto rl = [](float x, int l) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+      };
+#pragma unroll
+      for (int u = 0; u < RS; ++u)
+        v[u] = op(op(rl(v[u], 0), rl(v[u], 16)), op(rl(v[u], 32), rl(v[u], 48)));
+    }
+  }
+}
+
 // LDS layout of one workgroup (byte offsets), from the item's most rows R and
-// padded dims DP: q [R][DP] fp32 | K [CK][DP elements + 16 bytes] | V [CK][DP]
-// | p [R][CK] fp32 | rescale [R] | (max, sum) [R][2].  The K / V region holds
-// the product pass's per-part partials at the end (4 KB; the p region starts
-// after whichever is larger).
+// padded dims DP: q [R][DP] fp32 (16-bit types: their own type) | K [CK][DP
+// elements + 16 bytes] | V [CK][DP] (16-bit types: by key pairs) | p [R][CK]
+// fp32 (16-bit types: their own type) | rescale [R] | (max, sum) [R][2] |
+// the product pass's accumulators.
 struct GLds {
-  int q, k, v, p, al, ml, bytes, kst;
+  int q, k, v, p, al, ml, acc, bytes, kst;
 };
 template <class E, int CK>
 __host__ __device__ inline GLds glds(int R, int DP) {
@@ -156,12 +249,14 @@ __host__ __device__ inline GLds glds(int R, int DP) {
   l.q = 0;
   l.k = R * DP * 4;
   l.v = l.k + CK * l.kst;
-  const int kv_end = l.v + CK * DP * kElemBytes<E>;
-  const int part_end = l.k + kGThreads * 16;
-  l.p = kv_end > part_end ? kv_end : part_end;
+  l.p = l.v + CK * DP * kElemBytes<E>;
   l.al = l.p + R * CK * 4;
   l.ml = l.al + R * 4;
-  l.bytes = l.ml + R * 8;
+  l.acc = (l.ml + R * 8 + 15) & ~15;
+  // the product pass's accumulators: a quad's (or a quad part's) f32x4 each,
+  // max(256, R * DP / 4) of them
+  const int nacc = R * DP / 4 > kGThreads ? R * DP / 4 : kGThreads;
+  l.bytes = l.acc + nacc * 16;
   return l;
 }
 
@@ -184,6 +279,7 @@ __device__ __forceinline__ void generic_segment(const GArgs& a, unsigned char* l
   unsigned char* const ks = lds + L.k;
   unsigned char* const vs = lds + L.v;
   float* const ps = reinterpret_cast<float*>(lds + L.p);
+  f16* const ps16 = reinterpret_cast<f16*>(lds + L.p);  // 16-bit types: p in E
   float* const al = reinterpret_cast<float*>(lds + L.al);
   float* const ml = reinterpret_cast<float*>(lds + L.ml);
   const int tid = threadIdx.x;
@@ -202,13 +298,70 @@ __device__ __forceinline__ void generic_segment(const GArgs& a, unsigned char* l
   const unsigned char* const vnew = reinterpret_cast<const unsigned char*>(a.v_new);
   const int64_t new_off = (int64_t)trow * a.new_stride + (int64_t)h * D;
 
-  // ---- the rows' queries, scaled, padded with zeros ----
+  // 16-byte vectors: TPP threads per key pair (keys 2m, 2m + 1 of the chunk),
+  // thread tid moving vectors tid % TPP + TPP u of both keys of pair tid / TPP
+  // (one address per key; a pair shares its block unless the block size is
+  // 1), so the 16-bit V pairs interleave in registers; the next chunk's are
+  // loaded into registers while the current one is scored
+  constexpr int TPP = 2 * kGThreads / CK;
+  constexpr int UP = kGPre / 2;  // vectors of each key per thread
+  const int vpr = D / VW;
+  const int my_pm = tid / TPP;
+  const int my_v0 = tid % TPP;
+  f32x4 kr[2][UP], vr[2][UP];
+  // the block ids of this thread's keys in the next chunk to fetch, loaded one
+  // fetch ahead (a fetch is then one round trip, not a table lookup and a load)
+  const int32_t* const trow_ids = a.tables + (int64_t)trow * a.W;
+  auto block_of = [&](int k) __attribute__((always_inline)) {
+    return k < k_hi ? trow_ids[k >> a.bs_log2] : 0;
+  };
+  int blk_next[2] = {0, 0};
+  auto next_ids = [&](int c0) __attribute__((always_inline)) {
+    blk_next[0] = block_of(c0 + 2 * my_pm);
+    blk_next[1] = a.bs_log2 == 0 ? block_of(c0 + 2 * my_pm + 1) : blk_next[0];
+  };
+  auto fetch = [&](int c0) __attribute__((always_inline)) {
+    const int blk[2] = {clamp_block(blk_next[0], a.NB), clamp_block(blk_next[1], a.NB)};
+    next_ids(c0 + CK);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int k = c0 + 2 * my_pm + e;
+#pragma unroll
+      for (int u = 0; u < UP; ++u) vr[e][u] = f32x4{0.f, 0.f, 0.f, 0.f};  // keys past the range
+      if (k < k_hi) {
+        const bool nw = k == new_key;
+        const int64_t off =
+            ((nw ? new_off : ((int64_t)blk[e] * a.BS + (k & (a.BS - 1))) * rs + (int64_t)h * D) +
+             (int64_t)my_v0 * VW) * EB;
+        const unsigned char* const kb = (nw ? knew : kpool) + off;
+        const unsigned char* const vb = (nw ? vnew : vpool) + off;
+#pragma unroll
+        for (int u = 0; u < UP; ++u) {
+          if (my_v0 + TPP * u < vpr) {
+            kr[e][u] = *reinterpret_cast<const f32x4*>(kb + TPP * 16 * u);
+            vr[e][u] = *reinterpret_cast<const f32x4*>(vb + TPP * 16 * u);
+          }
+        }
+      }
+    }
+  };
+  // the first chunk's loads go out before the queries'
+  if (a.vec && k_lo < k_hi) {
+    next_ids(k_lo);
+    fetch(k_lo);
+  }
+
+  // ---- the rows' queries, padded with zeros: fp32 scaled to base 2, or the
+  //      16-bit values as they are (their scores are scaled instead) ----
+  uint16_t* const qs16 = reinterpret_cast<uint16_t*>(lds + L.q);
   for (int i = tid; i < R * DP; i += kGThreads) {
     const int r = i / DP, d = i - r * DP;
     const int tok = r / G, g = r - tok * G;
-    qs[i] = d < D ? ld_el<E>(a.q, (int64_t)(t0 + tok) * a.q_stride + (int64_t)(h * G + g) * D + d) *
-                        a.scale_log2
-                  : 0.f;
+    const int64_t qi = (int64_t)(t0 + tok) * a.q_stride + (int64_t)(h * G + g) * D + d;
+    if constexpr (kIsF32<E>)
+      qs[i] = d < D ? reinterpret_cast<const float*>(a.q)[qi] * a.scale_log2 : 0.f;
+    else
+      qs16[i] = d < D ? reinterpret_cast<const uint16_t*>(a.q)[qi] : (uint16_t)0;
   }
   // ---- the product pass's ownership: NQ quads of 4 dims ----
   const int QPR = DP / 4;  // quads per row
@@ -220,57 +373,51 @@ __device__ __forceinline__ void generic_segment(const GArgs& a, unsigned char* l
   const int my_q = many ? tid : tid % NQ;
   const int part = many ? 0 : tid / NQ;
   const int my_cnt = many ? 1 : (kGThreads - 1 - my_q) / NQ + 1;
-  f32x4 acc[kGMaxQuads];
-#pragma unroll
-  for (int i = 0; i < kGMaxQuads; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // accumulators in LDS: quad tid + 256 i (NQ >= 256), or quad my_q's part
+  // `part` at tid (= part * NQ + my_q)
+  f32x4* const accl = reinterpret_cast<f32x4*>(lds + L.acc);
+  const int nacc = many ? NQ : kGThreads;
+  for (int i = tid; i < nacc; i += kGThreads) accl[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int r = tid; r < R; r += kGThreads) {
     ml[2 * r] = kNegInf;
     ml[2 * r + 1] = 0.f;
   }
   __syncthreads();
 
-  // 16-byte vectors: TPK threads per key row, thread tid moving vectors
-  // tid % TPK + TPK u of key tid / TPK (one table lookup and one address per
-  // thread); the next chunk's are loaded into registers while the current one
-  // is scored
-  constexpr int TPK = kGThreads / CK;
-  const int vpr = D / VW;
-  const int my_kj = tid / TPK;
-  const int my_v0 = tid % TPK;
-  f32x4 kr[kGPre], vr[kGPre];
-  auto fetch = [&](int c0) __attribute__((always_inline)) {
-    const int k = c0 + my_kj;
-    if (k < k_hi) {
-      const bool nw = k == new_key;
-      const int blk = clamp_block(a.tables[(int64_t)trow * a.W + (k >> a.bs_log2)], a.NB);
-      const int64_t off =
-          ((nw ? new_off : ((int64_t)blk * a.BS + (k & (a.BS - 1))) * rs + (int64_t)h * D) +
-           (int64_t)my_v0 * VW) * EB;
-      const unsigned char* const kb = (nw ? knew : kpool) + off;
-      const unsigned char* const vb = (nw ? vnew : vpool) + off;
-#pragma unroll
-      for (int u = 0; u < kGPre; ++u) {
-        if (my_v0 + TPK * u < vpr) {
-          kr[u] = *reinterpret_cast<const f32x4*>(kb + TPK * 16 * u);
-          vr[u] = *reinterpret_cast<const f32x4*>(vb + TPK * 16 * u);
-        }
-      }
-    }
-  };
-  if (a.vec && k_lo < k_hi) fetch(k_lo);
-
   for (int c0 = k_lo; c0 < k_hi; c0 += CK) {
     const int nk = min(CK, k_hi - c0);
     // ---- stage the chunk's K and V rows ----
     if (a.vec) {
-      if (my_kj < nk) {
-        unsigned char* const kd = ks + my_kj * L.kst + my_v0 * 16;
-        unsigned char* const vd = vs + (my_kj * DP + my_v0 * VW) * EB;
 #pragma unroll
-        for (int u = 0; u < kGPre; ++u) {
-          if (my_v0 + TPK * u < vpr) {
-            *reinterpret_cast<f32x4*>(kd + TPK * 16 * u) = kr[u];
-            *reinterpret_cast<f32x4*>(vd + TPK * 16 * u) = vr[u];
+      for (int e = 0; e < 2; ++e) {
+        const int kj = 2 * my_pm + e;
+        if (kj < nk) {
+          unsigned char* const kd = ks + kj * L.kst + my_v0 * 16;
+#pragma unroll
+          for (int u = 0; u < UP; ++u)
+            if (my_v0 + TPP * u < vpr) *reinterpret_cast<f32x4*>(kd + TPP * 16 * u) = kr[e][u];
+          if constexpr (kIsF32<E>) {
+            unsigned char* const vd = vs + (kj * DP + my_v0 * VW) * EB;
+#pragma unroll
+            for (int u = 0; u < UP; ++u)
+              if (my_v0 + TPP * u < vpr) *reinterpret_cast<f32x4*>(vd + TPP * 16 * u) = vr[e][u];
+          }
+        }
+      }
+      if constexpr (!kIsF32<E>) {
+        // V by key pairs, dims interleaved (a key past the range is zeros)
+        if (2 * my_pm < nk) {
+          unsigned char* const vd = vs + my_pm * 4 * DP + my_v0 * 32;
+#pragma unroll
+          for (int u = 0; u < UP; ++u) {
+            if (my_v0 + TPP * u < vpr) {
+              const f16x8 a0 = __builtin_bit_cast(f16x8, vr[0][u]);
+              const f16x8 b0 = __builtin_bit_cast(f16x8, vr[1][u]);
+              *reinterpret_cast<f16x8*>(vd + TPP * 32 * u) =
+                  __builtin_shufflevector(a0, b0, 0, 8, 1, 9, 2, 10, 3, 11);
+              *reinterpret_cast<f16x8*>(vd + TPP * 32 * u + 16) =
+                  __builtin_shufflevector(a0, b0, 4, 12, 5, 13, 6, 14, 7, 15);
+            }
           }
         }
       }
@@ -281,7 +428,9 @@ __device__ __forceinline__ void generic_segment(const GArgs& a, unsigned char* l
         }
       }
     } else {
-      for (int i = tid; i < nk * DP; i += kGThreads) {
+      // (16-bit: keys up to the next even count, the odd tail's partner zero)
+      const int nkv = kIsF32<E> ? nk : (nk + 1) & ~1;
+      for (int i = tid; i < nkv * DP; i += kGThreads) {
         const int kj = i / DP, d = i - kj * DP;
         const int k = c0 + kj;
         const bool nw = k == new_key;
@@ -290,16 +439,18 @@ __device__ __forceinline__ void generic_segment(const GArgs& a, unsigned char* l
         const unsigned char* const vb = nw ? vnew : vpool;
         const int64_t off =
             nw ? new_off : ((int64_t)blk * a.BS + (k & (a.BS - 1))) * rs + (int64_t)h * D;
+        const bool in = d < D && kj < nk;
         unsigned char* kd = ks + kj * L.kst + d * EB;
-        unsigned char* vd = vs + (kj * DP + d) * EB;
         if constexpr (kIsF32<E>) {
-          *reinterpret_cast<float*>(kd) = d < D ? reinterpret_cast<const float*>(kb)[off + d] : 0.f;
-          *reinterpret_cast<float*>(vd) = d < D ? reinterpret_cast<const float*>(vb)[off + d] : 0.f;
+          unsigned char* vd = vs + (kj * DP + d) * EB;
+          *reinterpret_cast<float*>(kd) = in ? reinterpret_cast<const float*>(kb)[off + d] : 0.f;
+          *reinterpret_cast<float*>(vd) = in ? reinterpret_cast<const float*>(vb)[off + d] : 0.f;
         } else {
+          unsigned char* vd = vs + (kj >> 1) * 4 * DP + d * 4 + (kj & 1) * 2;
           *reinterpret_cast<uint16_t*>(kd) =
-              d < D ? reinterpret_cast<const uint16_t*>(kb)[off + d] : (uint16_t)0;
+              in ? reinterpret_cast<const uint16_t*>(kb)[off + d] : (uint16_t)0;
           *reinterpret_cast<uint16_t*>(vd) =
-              d < D ? reinterpret_cast<const uint16_t*>(vb)[off + d] : (uint16_t)0;
+              in ? reinterpret_cast<const uint16_t*>(vb)[off + d] : (uint16_t)0;
         }
       }
     }
@@ -307,78 +458,84 @@ __device__ __forceinline__ void generic_segment(const GArgs& a, unsigned char* l
     if (a.vec && c0 + CK < k_hi) fetch(c0 + CK);
 
     // ---- scores and the online softmax: lane = key j, rows of this segment,
-    //      kGRowStep at a time; a row's running (max, sum) lives in LDS, read by
-    //      the segment's lanes and written back by its lane 0 ----
+    //      RS at a time (RS = 1 or 2 when the wave holds only that many); a
+    //      row's running (max, sum) lives in LDS, read by the segment's lanes
+    //      and written back by its lane 0 ----
     {
       const unsigned char* krow = ks + j * L.kst;
-      for (int i0 = 0; i0 < nslots; i0 += kGRowStep) {  // wave-uniform
+      auto rows_step = [&](auto rs_c, int i0) __attribute__((always_inline)) {
+        constexpr int RS = decltype(rs_c)::value;
         // the step's rows (a row past R reads row 0 and is discarded): no
         // branches in the dot products, so a step's LDS reads issue together
-        const float* qrow[kGRowStep];
+        int qoff[RS];
 #pragma unroll
-        for (int u = 0; u < kGRowStep; ++u) {
+        for (int u = 0; u < RS; ++u) {
           const int r = w + kGWaves * (seg + NSEG * (i0 + u));
-          qrow[u] = qs + (i0 + u < nslots && r < R ? r : 0) * DP;
+          qoff[u] = (r < R ? r : 0) * DP;
         }
-        float s[kGRowStep];
+        float s[RS];
 #pragma unroll
-        for (int u = 0; u < kGRowStep; ++u) s[u] = 0.f;
-#pragma unroll 1
+        for (int u = 0; u < RS; ++u) s[u] = 0.f;
         for (int d = 0; d < DP; d += 8) {
-          float kx[8];
-          lds8<E>(krow + d * EB, kx);
+          if constexpr (kIsF32<E>) {
+            float kx[8];
+            lds8<E>(krow + d * EB, kx);
 #pragma unroll
-          for (int u = 0; u < kGRowStep; ++u) {
-            const f32x4 qa = *reinterpret_cast<const f32x4*>(qrow[u] + d);
-            const f32x4 qb = *reinterpret_cast<const f32x4*>(qrow[u] + d + 4);
-            float t = s[u];
-            t += qa[0] * kx[0];
-            t += qa[1] * kx[1];
-            t += qa[2] * kx[2];
-            t += qa[3] * kx[3];
-            t += qb[0] * kx[4];
-            t += qb[1] * kx[5];
-            t += qb[2] * kx[6];
-            t += qb[3] * kx[7];
-            s[u] = t;
+            for (int u = 0; u < RS; ++u) {
+              const f32x4 qa = *reinterpret_cast<const f32x4*>(qs + qoff[u] + d);
+              const f32x4 qb = *reinterpret_cast<const f32x4*>(qs + qoff[u] + d + 4);
+              float t = s[u];
+              t += qa[0] * kx[0];
+              t += qa[1] * kx[1];
+              t += qa[2] * kx[2];
+              t += qa[3] * kx[3];
+              t += qb[0] * kx[4];
+              t += qb[1] * kx[5];
+              t += qb[2] * kx[6];
+              t += qb[3] * kx[7];
+              s[u] = t;
+            }
+          } else {
+            // 16-bit q and K as they are: fp32 dot products of element pairs
+            const f16x8 kv = *reinterpret_cast<const f16x8*>(krow + d * 2);
+#pragma unroll
+            for (int u = 0; u < RS; ++u) {
+              const f16x8 qv = *reinterpret_cast<const f16x8*>(qs16 + qoff[u] + d);
+              s[u] = dot8<E>(qv, kv, s[u]);
+            }
           }
         }
         // the online softmax of the step's rows, their reductions interleaved;
-        // every lane joins them, and rows past R (slots past nslots among them)
-        // have nothing valid and write nothing
-        float mo[kGRowStep], mn[kGRowStep], lo[kGRowStep], pv[kGRowStep];
+        // every lane joins them, and rows past R have nothing valid and write
+        // nothing
+        float mo[RS], mn[RS], lo[RS], pv[RS];
 #pragma unroll
-        for (int u = 0; u < kGRowStep; ++u) {
+        for (int u = 0; u < RS; ++u) {
           const int r = w + kGWaves * (seg + NSEG * (i0 + u));
           const bool valid = r < R && j < nk && c0 + j < lim0 + r / G;
           const int rr = r < R ? r : 0;
           mo[u] = ml[2 * rr];
           lo[u] = ml[2 * rr + 1];
-          s[u] = valid ? s[u] : kNegInf;
+          s[u] = valid ? (kIsF32<E> ? s[u] : s[u] * a.scale_log2) : kNegInf;
           mn[u] = s[u];
         }
+        seg_reduce<CK, RS>(mn, [](float x, float y) { return fmaxf(x, y); });
 #pragma unroll
-        for (int m = CK / 2; m >= 1; m >>= 1) {
-#pragma unroll
-          for (int u = 0; u < kGRowStep; ++u) mn[u] = fmaxf(mn[u], shfl_xor_f(mn[u], m));
-        }
-#pragma unroll
-        for (int u = 0; u < kGRowStep; ++u) {
+        for (int u = 0; u < RS; ++u) {
           mn[u] = fmaxf(mo[u], mn[u]);
           pv[u] = s[u] == kNegInf ? 0.f : exp2f(s[u] - mn[u]);
           s[u] = pv[u];
         }
+        seg_reduce<CK, RS>(s, [](float x, float y) { return x + y; });
 #pragma unroll
-        for (int m = CK / 2; m >= 1; m >>= 1) {
-#pragma unroll
-          for (int u = 0; u < kGRowStep; ++u) s[u] += shfl_xor_f(s[u], m);
-        }
-#pragma unroll
-        for (int u = 0; u < kGRowStep; ++u) {
+        for (int u = 0; u < RS; ++u) {
           const int r = w + kGWaves * (seg + NSEG * (i0 + u));
           const float alpha = mo[u] == kNegInf ? 0.f : exp2f(mo[u] - mn[u]);
           if (r < R) {
-            ps[r * CK + j] = pv[u];
+            if constexpr (kIsF32<E>)
+              ps[r * CK + j] = pv[u];
+            else
+              ps16[r * CK + j] = to16<E>(pv[u]);
             if (j == 0) {
               al[r] = alpha;
               ml[2 * r] = mn[u];
@@ -386,71 +543,57 @@ __device__ __forceinline__ void generic_segment(const GArgs& a, unsigned char* l
             }
           }
         }
+      };
+      if (nslots == 1) {  // wave-uniform
+        rows_step(std::integral_constant<int, 1>{}, 0);
+      } else if (nslots == 2) {
+        rows_step(std::integral_constant<int, 2>{}, 0);
+      } else {
+        for (int i0 = 0; i0 < nslots; i0 += kGRowStep)
+          rows_step(std::integral_constant<int, kGRowStep>{}, i0);
       }
     }
     lds_barrier();
 
-    // ---- products: quads (row r, dims 4x .. 4x + 3) ----
-    if (many) {
-      // up to four quads per thread (tid + 256 i), every key; the quads' chains
-      // are interleaved key by key
-      const float* pr[kGMaxQuads];
-      const unsigned char* vc[kGMaxQuads];
-#pragma unroll
-      for (int i = 0; i < kGMaxQuads; ++i) {
-        const int qd = tid + kGThreads * i;
-        const int qc = qd < NQ ? qd : 0;  // past NQ: quad 0 again, discarded
-        const int r = qc / QPR, x = qc - r * QPR;
-        acc[i] *= al[r];
-        pr[i] = ps + r * CK;
-        vc[i] = vs + x * 4 * EB;
-      }
-#pragma unroll 2
-      for (int kj = 0; kj < nk; ++kj) {
-#pragma unroll
-        for (int i = 0; i < kGMaxQuads; ++i)
-          acc[i] += pr[i][kj] * lds4<E>(vc[i] + kj * DP * EB);
-      }
-    } else {
-      // one quad, keys part, part + cnt, ... four per step with their LDS
-      // reads issued together
-      const int r = my_q / QPR, x = my_q - r * QPR;
-      f32x4 o = acc[0] * al[r];
-      const float* pr = ps + r * CK;
-      const unsigned char* vcol = vs + x * 4 * EB;
-      const int vstep = my_cnt * DP * EB;
+    // ---- products: quads (row r, dims 4x .. 4x + 3) over the chunk's units
+    //      (fp32: keys; 16-bit: key pairs) ----
+    const int nu = kIsF32<E> ? nk : (nk + 1) >> 1;
+    const unsigned char* const pbase = lds + L.p;
+    constexpr int PRB = kIsF32<E> ? 4 * CK : 2 * CK;  // bytes of a row's probabilities
+    // quads tid, tid + 256, ... (NQ >= 256: every unit), or quad my_q's units
+    // part, part + cnt, ...; four units per step with their LDS reads issued
+    // together
+    for (int idx = tid; idx < nacc; idx += kGThreads) {
+      const int qd = many ? idx : my_q;
+      const int m0 = many ? 0 : part;
+      const int cnt = many ? 1 : my_cnt;
+      const int r = qd / QPR, x = qd - r * QPR;
+      f32x4 o = accl[idx] * al[r];
       f32x4 o1 = f32x4{0.f, 0.f, 0.f, 0.f};
-      int kj = part;
-      for (; kj + 3 * my_cnt < nk; kj += 4 * my_cnt) {
-        const unsigned char* v0 = vcol + kj * DP * EB;
-        const float p0 = pr[kj], p1 = pr[kj + my_cnt], p2 = pr[kj + 2 * my_cnt],
-                    p3 = pr[kj + 3 * my_cnt];
-        const f32x4 w0 = lds4<E>(v0), w1 = lds4<E>(v0 + vstep), w2 = lds4<E>(v0 + 2 * vstep),
-                    w3 = lds4<E>(v0 + 3 * vstep);
-        o += p0 * w0;
-        o1 += p1 * w1;
-        o += p2 * w2;
-        o1 += p3 * w3;
+      const unsigned char* const pr = pbase + r * PRB;
+      const unsigned char* const vcol = vs + x * 16;
+      int m = m0;
+      for (; m + 3 * cnt < nu; m += 4 * cnt) {
+        o = pv_unit<E>(pr, vcol, m, DP, o);
+        o1 = pv_unit<E>(pr, vcol, m + cnt, DP, o1);
+        o = pv_unit<E>(pr, vcol, m + 2 * cnt, DP, o);
+        o1 = pv_unit<E>(pr, vcol, m + 3 * cnt, DP, o1);
       }
-      for (; kj < nk; kj += my_cnt) o += pr[kj] * lds4<E>(vcol + kj * DP * EB);
-      acc[0] = o + o1;
+      for (; m < nu; m += cnt) o = pv_unit<E>(pr, vcol, m, DP, o);
+      accl[idx] = o + o1;
     }
     lds_barrier();
   }
 
-  // ---- the key parts summed ----
-  f32x4* const parts = reinterpret_cast<f32x4*>(lds + L.k);  // [part][NQ] when NQ < 256
-  if (!many) parts[tid] = acc[0];
+  // ---- the key parts summed (the accumulators of part p of quad q at
+  //      p * NQ + q) ----
   __syncthreads();
-#pragma unroll
-  for (int i = 0; i < kGMaxQuads; ++i) {
-    const int qd = many ? tid + kGThreads * i : (i == 0 ? tid : NQ);
-    if (qd < NQ) {
-      f32x4 o = acc[i];
+  for (int qd = tid; qd < NQ; qd += kGThreads) {
+    {
+      f32x4 o = accl[qd];
       if (!many) {
-        o = parts[qd];
         const int cnt = (kGThreads - 1 - qd) / NQ + 1;
-        for (int p2 = 1; p2 < cnt; ++p2) o += parts[p2 * NQ + qd];
+        for (int p2 = 1; p2 < cnt; ++p2) o += accl[p2 * NQ + qd];
       }
       const int r = qd / QPR, x = qd - r * QPR;
       const int tok = r / G, g = r - tok * G;
@@ -476,12 +619,12 @@ __device__ __forceinline__ void generic_segment(const GArgs& a, unsigned char* l
   __syncthreads();  // the next segment reuses the LDS
 }
 
-template <class E, int CK>
+template <class E, int CK, bool PREFILL>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(GEN_WAVES, GEN_WAVES)))
 void generic_attn_kernel(const GArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
   const int max_len = a.W * a.BS;
-  if (a.q_off == nullptr) {
+  if constexpr (!PREFILL) {
     // ---- decode: item = (row b, KV head h, split s) ----
     const int s = blockIdx.x % a.splits;
     const int bh = blockIdx.x / a.splits;
@@ -547,31 +690,41 @@ void generic_attn_kernel(const GArgs a) {
   }
 }
 
-// Decode splits folded: row r = (b, query head), its splits' normalised
-// outputs weighted by 2^(lse_s - max).
+// Decode splits folded: one wave per row r = (b, query head), lane s holding
+// split s's weight 2^(lse_s - max); each lane then sums dims lane, lane + 64, ...
+// over the splits.
+constexpr int kGMergeRows = 4;  // rows (waves) per merge workgroup
 template <class E>
-__global__ __launch_bounds__(kWave) void generic_merge_kernel(const GArgs a) {
-  const int r = blockIdx.x;  // b * Hq + hq
+__global__ __launch_bounds__(kWave * kGMergeRows) void generic_merge_kernel(const GArgs a) {
+  const int lane = lane_id();
+  const int r = blockIdx.x * kGMergeRows + threadIdx.x / kWave;  // b * Hq + hq
+  if (r >= a.total * a.Hq) return;                             // wave-uniform
   const int S = a.splits;
-  const float* lse = a.part_lse + (int64_t)r * S;
-  float M = kNegInf;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, lse[s]);
-  float wgt[kGMaxSplits];
-  float den = 0.f;
+  const float ls = lane < S ? a.part_lse[(int64_t)r * S + lane] : kNegInf;
+  float M = ls;
 #pragma unroll
-  for (int s = 0; s < kGMaxSplits; ++s) {
-    const float ls = lse[s < S ? s : 0];
-    wgt[s] = s < S && ls != kNegInf ? exp2f(ls - M) : 0.f;
-    den += wgt[s];
-  }
+  for (int m = kWave / 2; m >= 1; m >>= 1) M = fmaxf(M, shfl_xor_f(M, m));
+  const float wl = ls == kNegInf ? 0.f : exp2f(ls - M);
+  float den = wl;
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m >>= 1) den += shfl_xor_f(den, m);
   const float inv = den > 0.f ? 1.f / den : 0.f;
   const int b = r / a.Hq, hq = r - b * a.Hq;
   const float* po = a.part_o + (int64_t)r * S * a.D;
-  for (int d = threadIdx.x; d < a.D; d += kWave) {
+  auto wsplit = [&](int s) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), s));
+  };
+  for (int d = lane; d < a.D; d += kWave) {
     float num = 0.f;
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {  // eight loads in flight
+      float v[8];
 #pragma unroll
-    for (int s = 0; s < kGMaxSplits; ++s)
-      if (wgt[s] > 0.f) num += wgt[s] * po[(int64_t)s * a.D + d];
+      for (int i = 0; i < 8; ++i) v[i] = po[(int64_t)(s + i) * a.D + d];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) num += wsplit(s + i) * v[i];
+    }
+    for (; s < S; ++s) num += wsplit(s) * po[(int64_t)s * a.D + d];
     store_out1<E>(reinterpret_cast<f16*>(a.out), (int64_t)b * a.out_stride + (int64_t)hq * a.D + d,
                   num * inv);
   }
@@ -584,11 +737,18 @@ int launch_ck(const GArgs& a, hipStream_t stream) {
                             ? (int64_t)a.total * a.Hkv * a.splits
                             : (int64_t)((a.total + a.TQ - 1) / a.TQ) * a.Hkv;
   if (items >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((generic_attn_kernel<E, CK>), dim3((unsigned)items), dim3(kGThreads),
-                     (size_t)L.bytes, stream, a);
-  if (a.q_off == nullptr && a.splits > 1)
-    hipLaunchKernelGGL((generic_merge_kernel<E>), dim3((unsigned)((int64_t)a.total * a.Hq)),
-                       dim3(kWave), 0, stream, a);
+  if (a.q_off == nullptr)
+    hipLaunchKernelGGL((generic_attn_kernel<E, CK, false>), dim3((unsigned)items),
+                       dim3(kGThreads), (size_t)L.bytes, stream, a);
+  else
+    hipLaunchKernelGGL((generic_attn_kernel<E, CK, true>), dim3((unsigned)items),
+                       dim3(kGThreads), (size_t)L.bytes, stream, a);
+  if (a.q_off == nullptr && a.splits > 1) {
+    const int64_t rows = (int64_t)a.total * a.Hq;
+    hipLaunchKernelGGL((generic_merge_kernel<E>),
+                       dim3((unsigned)((rows + kGMergeRows - 1) / kGMergeRows)),
+                       dim3(kWave * kGMergeRows), 0, stream, a);
+  }
   return FE_LAUNCH_STATUS();
 }
 
