@@ -17,10 +17,12 @@ stream -- and prints one JSON line per config:
   the 48 decode rows in GB/s, and the whole step.
 
 Calls are replayed from a HIP graph, so each figure is GPU time per call.
+`--configs generic` times the generic kernel's shapes (head_dim 96, 80, 256, 8 and
+a group of 32 at D = 128) at C2's 64 context lengths.
+
 `--dtype bf16` runs the bf16 entry points on the same values rounded to bf16;
 `--dtype f32` the fp32 entry points on the values widened to float32 (bytes at
-4 per element, the C4 prefill against the 157.3 TFLOP/s fp32 MFMA peak; no plan
-and no shared-prefix form).
+4 per element, the C4 prefill against the 157.3 TFLOP/s fp32 MFMA peak; no plan).
 """
 from __future__ import annotations
 
@@ -33,6 +35,8 @@ import torch
 from flexengine_amd import ops, workloads
 
 HBM_PEAK = 8.0e12
+# (head_dim, q heads, KV heads) of `--configs generic`
+GENERIC_SHAPES = [(96, 12, 2), (80, 32, 8), (256, 8, 1), (256, 16, 8), (128, 32, 1), (8, 4, 2)]
 LAYERS = 28  # Qwen2.5-1.5B: calls per model step that share one plan
 MFMA_FP16_PEAK = 2.5e15
 MFMA_FP32_PEAK = 157.3e12
@@ -208,13 +212,22 @@ def main(argv=None) -> int:
         unique = w.unique_tokens * 2 * hkv * d * size + 2 * w.q.numel() * size
         print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique, dtype=dt)
                          | {"dtype": args.dtype}), flush=True)
-        if dt != torch.float32:  # the shared-prefix decode takes 16-bit pools
-            print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique,
-                                          shared_prefix=True, dtype=dt) | {"dtype": args.dtype}),
-                  flush=True)
+        print(json.dumps(bench_decode("C3", w, args.iters, args.copies, unique,
+                                      shared_prefix=True, dtype=dt) | {"dtype": args.dtype}),
+              flush=True)
     if "c4" in cfgs:
         print(json.dumps(bench_c4(args.iters, args.copies, dt) | {"dtype": args.dtype}),
               flush=True)
+    if "generic" in cfgs:
+        # the generic kernel's shapes (head_dim other than 64 / 128, decode groups
+        # above 16) at C2's 64 context lengths
+        lens = workloads.c2_lengths()
+        for d, hq, hkv in GENERIC_SHAPES:
+            w = workloads.make_decode_workload(f"G-d{d}-{hq}x{hkv}", 5, len(lens), hq, hkv, d,
+                                               lens)
+            print(json.dumps(bench_decode(w.name, w, args.iters, args.copies, dtype=dt)
+                             | {"dtype": args.dtype, "head_dim": d, "q_heads": hq,
+                                "kv_heads": hkv}), flush=True)
     return 0
 
 
