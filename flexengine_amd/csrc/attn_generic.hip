@@ -1,6 +1,6 @@
 // Attention for the shapes the matrix-core kernels do not take: head_dim other
-// than 64 and 128 (1 .. 512), and decode groups of 17 .. 32 query heads per KV
-// head.  The reference's Triton decode takes any head_dim (BLOCK_D =
+// than 64 and 128 (1 .. 512), and decode groups of 17 .. 128 query heads per KV
+// head (group x head_dim <= 8192).  The reference's Triton decode takes any head_dim (BLOCK_D =
 // next_power_of_2 and a dim mask, src/flexengine/inference/kernels/
 // paged_attention.py:106,112,152), and its own synthetic-model test runs
 // head_dim 8 (tests/unit/test_synthetic_qwen.py:55); these shapes keep that
@@ -44,7 +44,7 @@ namespace {
 #endif
 constexpr int kGThreads = 256;
 constexpr int kGWaves = kGThreads / kWave;
-constexpr int kGMaxRows = 64;     // query rows of one item (tokens x group)
+constexpr int kGMaxRows = 64;     // query rows of a prefill tile (tokens x group; one token at least)
 constexpr int kGRowStep = 4;      // rows scored per pass over a key's row
 constexpr int kGPre = 4;          // prefetched 16-byte K (and V) vectors per thread: a row holds <= 4 x (256 / CK)
 constexpr int kGMaxSplits = 32;   // decode key splits per row

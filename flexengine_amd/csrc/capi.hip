@@ -12,8 +12,8 @@ extern "C" const char* fe_error_string(int code) {
     case FE_ERR_INVALID_ARGUMENT:
       return "invalid argument (null pointer, size, stride or alignment)";
     case FE_ERR_UNSUPPORTED:
-      return "unsupported configuration (head_dim 1-512, decode group size <= 32, "
-             "group size * head_dim <= 4096, block_size a power of two; no plan or "
+      return "unsupported configuration (head_dim 1-512, decode group size <= 128, "
+             "group size * head_dim <= 8192, block_size a power of two; no plan or "
              "key-split prefix pass outside head_dim 64 / 128 with groups <= 16)";
     case FE_ERR_WORKSPACE:
       return "workspace missing, misaligned or smaller than fe_paged_decode_workspace_size()";

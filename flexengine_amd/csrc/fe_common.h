@@ -427,8 +427,8 @@ __attribute__((visibility("hidden"))) int cascade_prefix_launch(CascadePrefix& c
 // s attends keys 0 .. cached + its index, cached = ctx[s] - n_s (0 when
 // ctx[s] < n_s).  Rows with no keys give zeros. ----
 constexpr int kGenericMaxHeadDim = 512;
-constexpr int kGenericMaxGroup = 32;    // query heads per KV head
-constexpr int kGenericMaxElems = 4096;  // group size * head_dim
+constexpr int kGenericMaxGroup = 128;   // query heads per KV head
+constexpr int kGenericMaxElems = 8192;  // group size * head_dim (padded to 8): LDS of an item
 struct GenericAttn {
   const void* q;
   int64_t q_stride;    // elements between consecutive query rows

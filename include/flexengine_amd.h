@@ -26,11 +26,13 @@
  * of two.  head_dim 64 and 128 with a decode group (num_q_heads / kv_heads)
  * of at most 16 run on the matrix-core kernels, as does the prefill at any
  * group size.  Every other head_dim from 1 to 512, and decode groups of 17
- * to 32, run on a generic kernel (one workgroup per query row and KV head,
- * fp32 arithmetic) as long as group * head_dim <= 4096: same entry points,
- * same results to the same tolerances, no workspace used, no plan taken
- * (the _planned calls return FE_ERR_UNSUPPORTED there), and a shared-prefix
- * decode attends each row over its own table.  The KV page movers need
+ * to 128, run on a generic kernel (key splits of a row or tiles of prefill
+ * tokens per workgroup, fp32 arithmetic) as long as group * head_dim <= 8192
+ * (head_dim rounded up to a multiple of 8): same entry points, same results
+ * to the same tolerances; the decode's key-split partials use the workspace
+ * (fe_paged_decode_workspace_size covers them), the prefill none; no plan is
+ * taken (the _planned calls return FE_ERR_UNSUPPORTED there), and a
+ * shared-prefix decode attends each row over its own table.  The KV page movers need
  * head_dim % 8 == 0 (fp16 / bf16) or % 4 == 0 (fp32).
  * Element types: fp16 (the unsuffixed entry points), bfloat16 (_bf16) and
  * fp32 (_f32: the KV movers, the decode and the prefill).

@@ -1,5 +1,5 @@
 """GPU: the generic attention kernel -- head dims other than 64 / 128, and decode
-groups of 17-32 query heads per KV head -- against the oracle, in fp16, bf16 and
+groups of 17-128 query heads per KV head -- against the oracle, in fp16, bf16 and
 fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
 head_dim 64 / 128 below run there.)
 
@@ -51,8 +51,11 @@ SHAPES = [
     (256, 16, 2, 32, F32),
     (512, 4, 1, 16, FP16),
     (64, 32, 1, 16, FP16),   # group 32: past the matrix-core kernels' 16
-    (128, 32, 1, 16, BF16),  # group 32 x 128: the generic kernel's largest item
+    (128, 32, 1, 16, BF16),
     (128, 24, 1, 8, F32),
+    (64, 71, 1, 16, FP16),   # 71 query heads over one KV head
+    (128, 48, 1, 16, BF16),  # 48 over one
+    (128, 64, 1, 32, F32),   # group 64 x 128: the generic kernel's largest item
 ]
 
 
@@ -124,7 +127,7 @@ def test_generic_decode_matches_oracle_with_page_write(shape):
     assert (_bits(d.v_pool.cpu()) == vp).all(), "page write (V)"
 
 
-@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[5], SHAPES[11]], ids=_ids)
+@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[5], SHAPES[11], SHAPES[-1]], ids=_ids)
 def test_generic_decode_without_page_write_is_repeatable(shape):
     """Without new rows the pools are untouched, and repeated calls are bit-identical
     (no atomics, a fixed reduction order)."""
@@ -309,7 +312,7 @@ def test_generic_shapes_outside_the_envelope_are_refused():
     c = torch.ones(1, dtype=torch.int32, device=DEV)
     with pytest.raises(RuntimeError, match="unsupported"):
         ops.paged_decode(q, pool, pool, t, c)
-    q = torch.zeros(1, 40, 128, dtype=FP16, device=DEV)  # group 40 > 32
+    q = torch.zeros(1, 72, 128, dtype=FP16, device=DEV)  # group 72 x 128 > 8192
     pool = torch.zeros(2, 16, 1, 128, dtype=FP16, device=DEV)
     with pytest.raises(RuntimeError, match="unsupported"):
         ops.paged_decode(q, pool, pool, t, c)
