@@ -171,6 +171,45 @@ def test_generic_and_matrix_core_decodes_share_one_workspace():
     assert torch.count_nonzero(ws[:65536 * 4]) == 0, "split-K tickets left nonzero"
 
 
+def test_generic_decode_replays_from_a_graph():
+    """The generic decode (its split launch and merge launch, partials in the caller's
+    workspace) captured in a HIP graph: three replays, with eager decodes of another
+    shape on the same workspace between them, each bit-identical to the eager call."""
+    lens = [1, 90, 4096, 700, 33, 2000]
+    w = _decode_workload((96, 12, 2, 16, BF16), 795, lens)
+    w = workloads.DecodeWorkload(w.name, w.q, w.k_pool, w.v_pool, w.block_tables,
+                                 w.context_lens, None, None, w.unique_tokens, w.meta)
+    other = _decode_workload((80, 8, 2, 16, BF16), 796, [17, 300, 1200])
+    d, o = w.to(DEV), other.to(DEV)
+    need = max(ops.decode_workspace_bytes(len(lens), 12, 96, 4096),
+               ops.decode_workspace_bytes(3, 8, 80, o.block_tables.shape[1] * 16))
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    out = torch.empty_like(d.q)
+    eager = ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens,
+                             workspace=ws).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens, out=out,
+                         workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.paged_decode(d.q, d.k_pool, d.v_pool, d.block_tables, d.context_lens, out=out,
+                         workspace=ws)
+    for rep in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
+        ops.paged_decode(o.q, o.k_pool, o.v_pool, o.block_tables, o.context_lens, workspace=ws)
+        torch.cuda.synchronize()
+    exp = R.decode_reference(_np64(w.q), _np64(w.k_pool), _np64(w.v_pool), w.block_tables.numpy(),
+                             w.context_lens.numpy(), 16)
+    _close(out, exp, BF16, "graph replay")
+
+
 def test_generic_decode_strided_q_and_scale():
     """q rows with a batch stride wider than Hq * D (a fused qkv buffer's q slice) and an
     explicit scale."""
