@@ -18,7 +18,8 @@ stream -- and prints one JSON line per config:
 
 Calls are replayed from a HIP graph, so each figure is GPU time per call.
 `--configs generic` times the generic kernel's shapes (head_dim 96, 80, 256, 8 and
-a group of 32 at D = 128) at C2's 64 context lengths.
+a group of 32 at D = 128) at C2's 64 context lengths, and C4's prefill chunks at
+head_dim 96.
 
 `--dtype bf16` runs the bf16 entry points on the same values rounded to bf16;
 `--dtype f32` the fp32 entry points on the values widened to float32 (bytes at
@@ -189,6 +190,34 @@ def bench_c4(iters: int, copies: int, dtype=torch.float16) -> dict:
             "prefill_tokens": int(w.q.shape[0]), "chunks": w.meta["n_new"], "cached": w.meta["cached"]}
 
 
+def bench_generic_prefill(iters: int, copies: int, head_dim: int, dtype) -> dict:
+    """C4's prefill chunks (offsets, contexts, tables) at another head_dim, which runs
+    on the generic kernel: TFLOP/s over the valid query-key pairs."""
+    w = workloads.c4_workload()
+    gen = torch.Generator().manual_seed(96)
+    nb, bs, hkv, _ = w.k_pool.shape
+    hq = w.q.shape[1]
+
+    def draw(*shape):
+        return torch.randn(*shape, generator=gen).to(dtype).to("cuda:0")
+    q = draw(w.q.shape[0], hq, head_dim)
+    pools = [(draw(nb, bs, hkv, head_dim), draw(nb, bs, hkv, head_dim)) for _ in range(copies)]
+    tables, offs, ctx = (t.to("cuda:0") for t in (w.block_tables, w.q_offsets, w.context_lens))
+    out = torch.empty_like(q)
+    max_q = int((w.q_offsets[1:] - w.q_offsets[:-1]).max())
+
+    def prefill(i):
+        kp, vp = pools[i % len(pools)]
+        ops.prefill_paged(q, kp, vp, tables, offs, ctx, max_q, out=out)
+
+    sec = _timed(prefill, iters, len(pools))
+    flops = w.flops() // 128 * head_dim  # w.flops() counts 4 * Hq * 128 per pair
+    return {"config": f"C4-prefill-d{head_dim}", "kernel": "fe_prefill_paged (generic)",
+            "us_per_call": round(sec * 1e6, 2), "flops": flops,
+            "TFLOP_s": round(flops / sec / 1e12, 2),
+            "pct_mfma_fp16_peak": round(100 * flops / sec / MFMA_FP16_PEAK, 2)}
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--iters", type=int, default=200)
@@ -228,6 +257,8 @@ def main(argv=None) -> int:
             print(json.dumps(bench_decode(w.name, w, args.iters, args.copies, dtype=dt)
                              | {"dtype": args.dtype, "head_dim": d, "q_heads": hq,
                                 "kv_heads": hkv}), flush=True)
+        print(json.dumps(bench_generic_prefill(args.iters, args.copies, 96, dt)
+                         | {"dtype": args.dtype}), flush=True)
     return 0
 
 
