@@ -1521,7 +1521,11 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   if (f32 && plan != nullptr) return FE_ERR_UNSUPPORTED;
   FE_CHECK_ARG(num_q_heads % kv_heads == 0);
   const int G = num_q_heads / kv_heads;
-  if ((head_dim != 64 && head_dim != 128) || G > kMaxGroup)
+  // head_dim 256 in 16 bits runs on the piece kernel too (unplanned, no shared
+  // prefix; it spills 168-388 bytes per lane at the two-wave register budget and
+  // still beats the generic kernel 1.1-1.5x)
+  const bool mfma256 = head_dim == 256 && !f32 && plan == nullptr && cascade == nullptr;
+  if ((head_dim != 64 && head_dim != 128 && !mfma256) || G > kMaxGroup)
     return decode_generic(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
                           num_blocks, block_tables, table_stride, context_lens, workspace,
                           workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size,
@@ -1645,6 +1649,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     a.pre_splits = c.splits;
   }
   if (f32) return head_dim == 64 ? launch_decode<64, F32>(a, s) : launch_decode<128, F32>(a, s);
+  if (head_dim == 256) return bf16 ? launch_decode<256, Bf16>(a, s) : launch_decode<256, Fp16>(a, s);
   if (bf16) return head_dim == 64 ? launch_decode<64, Bf16>(a, s) : launch_decode<128, Bf16>(a, s);
   return head_dim == 64 ? launch_decode<64, Fp16>(a, s) : launch_decode<128, Fp16>(a, s);
 }

@@ -1,6 +1,7 @@
-"""GPU: the generic attention kernel -- head dims other than 64 / 128, and decode
-groups of 17-128 query heads per KV head -- against the oracle, in fp16, bf16 and
-fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
+"""GPU: head dims other than 64 / 128 and decode groups of 17-128 query heads per KV
+head -- the generic attention kernel, and for 16-bit decodes at head_dim 256 with
+groups <= 16 the matrix-core decode instantiated at 256 -- against the oracle, in
+fp16, bf16 and fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
 head_dim 64 / 128 below run there.)
 
 The reference's Triton decode takes any head_dim (BLOCK_D = next_power_of_2
@@ -47,7 +48,9 @@ SHAPES = [
     (80, 12, 2, 16, FP16),
     (96, 12, 2, 16, BF16),
     (96, 12, 4, 32, F32),
-    (256, 8, 1, 16, FP16),
+    (256, 8, 1, 16, FP16),   # 16-bit D 256, groups <= 16: the matrix-core decode
+    (256, 12, 2, 8, BF16),
+    (256, 32, 2, 32, FP16),
     (256, 16, 2, 32, F32),
     (512, 4, 1, 16, FP16),
     (64, 32, 1, 16, FP16),   # group 32: past the matrix-core kernels' 16
@@ -127,7 +130,8 @@ def test_generic_decode_matches_oracle_with_page_write(shape):
     assert (_bits(d.v_pool.cpu()) == vp).all(), "page write (V)"
 
 
-@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[5], SHAPES[11], SHAPES[-1]], ids=_ids)
+@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[5], SHAPES[8], SHAPES[13], SHAPES[-1]],
+                         ids=_ids)
 def test_generic_decode_without_page_write_is_repeatable(shape):
     """Without new rows the pools are untouched, and repeated calls are bit-identical
     (no atomics, a fixed reduction order)."""
