@@ -344,7 +344,11 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const DecodeArgs 
 
 template <int D, bool PAGE16, bool PLANNED = false, class E = Fp16>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(kIsF32<E> ? 1 : (PAGE16 ? FE_DECODE_WAVES_PER_EU : 2), 8)))
+// (fp32 and head_dim 256: one wave per SIMD, the rest of the register file held
+// as AGPRs -- at two waves D = 256 spilled 168-388 bytes per lane to scratch and
+// ran 1.6-1.8x slower)
+__attribute__((amdgpu_waves_per_eu(kIsF32<E> || D > 128 ? 1 : (PAGE16 ? FE_DECODE_WAVES_PER_EU : 2),
+                                   8)))
 void piece_decode_kernel(const DecodeArgs a) {
   using C = TileCfg<D>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -1522,8 +1526,8 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   FE_CHECK_ARG(num_q_heads % kv_heads == 0);
   const int G = num_q_heads / kv_heads;
   // head_dim 256 in 16 bits runs on the piece kernel too (unplanned, no shared
-  // prefix; it spills 168-388 bytes per lane at the two-wave register budget and
-  // still beats the generic kernel 1.1-1.5x)
+  // prefix; one wave per SIMD with its spills in AGPRs: 1.9-2.4x the generic
+  // kernel's rate)
   const bool mfma256 = head_dim == 256 && !f32 && plan == nullptr && cascade == nullptr;
   if ((head_dim != 64 && head_dim != 128 && !mfma256) || G > kMaxGroup)
     return decode_generic(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
