@@ -191,8 +191,9 @@ def bench_c4(iters: int, copies: int, dtype=torch.float16) -> dict:
 
 
 def bench_generic_prefill(iters: int, copies: int, head_dim: int, dtype) -> dict:
-    """C4's prefill chunks (offsets, contexts, tables) at another head_dim, which runs
-    on the generic kernel: TFLOP/s over the valid query-key pairs."""
+    """C4's prefill chunks (offsets, contexts, tables) at another head_dim (96: the
+    generic kernel; 256: the tile kernel instantiated at 256): TFLOP/s over the
+    valid query-key pairs."""
     w = workloads.c4_workload()
     gen = torch.Generator().manual_seed(96)
     nb, bs, hkv, _ = w.k_pool.shape
@@ -212,7 +213,7 @@ def bench_generic_prefill(iters: int, copies: int, head_dim: int, dtype) -> dict
 
     sec = _timed(prefill, iters, len(pools))
     flops = w.flops() // 128 * head_dim  # w.flops() counts 4 * Hq * 128 per pair
-    return {"config": f"C4-prefill-d{head_dim}", "kernel": "fe_prefill_paged (generic)",
+    return {"config": f"C4-prefill-d{head_dim}", "kernel": "fe_prefill_paged",
             "us_per_call": round(sec * 1e6, 2), "flops": flops,
             "TFLOP_s": round(flops / sec / 1e12, 2),
             "pct_mfma_fp16_peak": round(100 * flops / sec / MFMA_FP16_PEAK, 2)}
@@ -257,8 +258,9 @@ def main(argv=None) -> int:
             print(json.dumps(bench_decode(w.name, w, args.iters, args.copies, dtype=dt)
                              | {"dtype": args.dtype, "head_dim": d, "q_heads": hq,
                                 "kv_heads": hkv}), flush=True)
-        print(json.dumps(bench_generic_prefill(args.iters, args.copies, 96, dt)
-                         | {"dtype": args.dtype}), flush=True)
+        for d in (96, 256):
+            print(json.dumps(bench_generic_prefill(args.iters, args.copies, d, dt)
+                             | {"dtype": args.dtype}), flush=True)
     return 0
 
 

@@ -300,8 +300,9 @@ __device__ __forceinline__ void finish_split(const PrefillArgs& a, const RowBloc
   }
 }
 
+// (head_dim 256: one wave per SIMD, 174 VGPRs + 72 AGPRs, no scratch)
 template <int D, int RT, class E = Fp16>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8)))
 void prefill_kernel(const PrefillArgs a) {
   using P = PCfg<D, RT>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -2146,7 +2147,10 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   FE_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 &&
                kv_heads > 0 && num_blocks > 0 && table_stride > 0);
   FE_CHECK_ARG(num_q_heads % kv_heads == 0);
-  if (head_dim != 64 && head_dim != 128)
+  // head_dim 256 in 16 bits runs on the tile kernel (one row tile per wave, no
+  // plan); other head dims on the generic kernel
+  const bool mfma256 = head_dim == 256 && !f32 && step_plan == nullptr;
+  if (head_dim != 64 && head_dim != 128 && !mfma256)
     return prefill_generic(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride,
                            q_offsets, context_lens, num_seqs, total_q, num_q_heads, kv_heads,
                            head_dim, block_size, scale, (hipStream_t)stream,
@@ -2198,7 +2202,8 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
     return FE_LAUNCH_STATUS();
   }
   const int nwg = stream_wgs();
-  const bool dma = stream_ok(block_size, table_stride, total_q, num_q_heads / kv_heads, num_seqs,
+  const bool dma = head_dim != 256 &&
+                   stream_ok(block_size, table_stride, total_q, num_q_heads / kv_heads, num_seqs,
                              kv_heads, nwg);
   const Plan p = plan(num_seqs, total_q, num_q_heads, kv_heads);
   // split-K tickets of prefill_kernel: one per (row block, KV head)
@@ -2251,6 +2256,8 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
     if (head_dim == 64) launch_prefill_dma<64, Bf16>(a, s); else launch_prefill_dma<128, Bf16>(a, s);
   } else if (dma) {
     if (head_dim == 64) launch_prefill_dma<64, Fp16>(a, s); else launch_prefill_dma<128, Fp16>(a, s);
+  } else if (head_dim == 256) {
+    if (bf16) launch_prefill<256, 1, Bf16>(a, p.blocks, s); else launch_prefill<256, 1>(a, p.blocks, s);
   } else if (bf16) {
     if (head_dim == 64) {
       if (p.rt == 2) launch_prefill<64, 2, Bf16>(a, p.blocks, s);

@@ -1,7 +1,7 @@
 """GPU: head dims other than 64 / 128 and decode groups of 17-128 query heads per KV
-head -- the generic attention kernel, and for 16-bit decodes at head_dim 256 with
-groups <= 16 the matrix-core decode instantiated at 256 -- against the oracle, in
-fp16, bf16 and fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
+head -- the generic attention kernel, and at head_dim 256 in 16 bits the matrix-core
+decode (groups <= 16) and prefill instantiated at 256 -- against the oracle, in fp16,
+bf16 and fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
 head_dim 64 / 128 below run there.)
 
 The reference's Triton decode takes any head_dim (BLOCK_D = next_power_of_2
