@@ -432,7 +432,9 @@ __device__ __forceinline__ void generic_segment(const GArgs& a, unsigned char* l
       const int nkv = kIsF32<E> ? nk : (nk + 1) & ~1;
       for (int i = tid; i < nkv * DP; i += kGThreads) {
         const int kj = i / DP, d = i - kj * DP;
-        const int k = c0 + kj;
+        // the odd tail's partner (kj == nk) is zeros: its table entry may lie past
+        // the row, so it looks up the chunk's first key instead
+        const int k = c0 + (kj < nk ? kj : 0);
         const bool nw = k == new_key;
         const int blk = clamp_block(a.tables[(int64_t)trow * a.W + (k >> a.bs_log2)], a.NB);
         const unsigned char* const kb = nw ? knew : kpool;

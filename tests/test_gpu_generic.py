@@ -59,6 +59,9 @@ SHAPES = [
     (64, 71, 1, 16, FP16),   # 71 query heads over one KV head
     (128, 48, 1, 16, BF16),  # 48 over one
     (128, 64, 1, 32, F32),   # group 64 x 128: the generic kernel's largest item
+    (36, 6, 2, 16, FP16),    # head dims off the 16-byte vector: element loads
+    (6, 4, 1, 4, F32),
+    (20, 4, 2, 32, BF16),
 ]
 
 
