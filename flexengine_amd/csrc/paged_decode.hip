@@ -111,6 +111,10 @@ struct DecodeArgs {
   int64_t q_stride;
   int64_t new_stride;
   int W, B, Hq, Hkv, G, BS, bs_log2, NB, target;
+  // virtual KV heads per pool head (1, or a group above 16 split into hdiv
+  // groups of G query heads: virtual head h reads pool head h / hdiv, whose
+  // rows are (Hkv / hdiv) * D elements apart)
+  int hdiv;
   int max_len;       // W * BS: longest context the tables can address
   float scale_log2;  // softmax scale * log2(e)
   int nwg;           // balanced kernel: workgroups sharing the tile order (= grid size)
@@ -272,9 +276,10 @@ __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, 
 template <int D, class Core>
 __device__ __forceinline__ void setup_core(Core& core, const DecodeArgs& a, const Piece& pc, int h,
                                            unsigned char* stage) {
+  const int hp = h / a.hdiv;  // the pool's KV head
   core.trow = a.tables + (int64_t)pc.b * a.W;
-  core.rs = a.Hkv * D;
-  core.hoff = h * D;
+  core.rs = (a.Hkv / a.hdiv) * D;
+  core.hoff = hp * D;
   core.W = a.W;
   core.NB = a.NB;
   core.BS = a.BS;
@@ -283,8 +288,8 @@ __device__ __forceinline__ void setup_core(Core& core, const DecodeArgs& a, cons
   core.limit = pc.tok_end;
   core.scale_log2 = a.scale_log2;
   if (a.k_new != nullptr) {
-    core.knew_row = a.k_new + (int64_t)pc.b * a.new_stride + (int64_t)h * D;
-    core.vnew_row = a.v_new + (int64_t)pc.b * a.new_stride + (int64_t)h * D;
+    core.knew_row = a.k_new + (int64_t)pc.b * a.new_stride + (int64_t)hp * D;
+    core.vnew_row = a.v_new + (int64_t)pc.b * a.new_stride + (int64_t)hp * D;
     core.new_pos = pc.L - 1;
   } else {
     core.knew_row = nullptr;
@@ -445,8 +450,8 @@ void piece_decode_kernel(const DecodeArgs a) {
     core.k_pool_w = reinterpret_cast<float*>(a.k_pool);
     core.v_pool_w = reinterpret_cast<float*>(a.v_pool);
     core.trow = a.tables + (int64_t)b * a.W;
-    core.rs = a.Hkv * D;
-    core.hoff = h * D;
+    core.rs = (a.Hkv / a.hdiv) * D;
+    core.hoff = (h / a.hdiv) * D;
     core.W = a.W;
     core.NB = a.NB;
     core.BS = a.BS;
@@ -458,7 +463,7 @@ void piece_decode_kernel(const DecodeArgs a) {
     core.knew_row = nullptr;
     core.vnew_row = nullptr;
     if (a.k_new != nullptr) {
-      const int64_t nr = (int64_t)b * a.new_stride + (int64_t)h * D;
+      const int64_t nr = (int64_t)b * a.new_stride + (int64_t)(h / a.hdiv) * D;
       core.knew_row = reinterpret_cast<const float*>(a.k_new) + nr;
       core.vnew_row = reinterpret_cast<const float*>(a.v_new) + nr;
       core.new_pos = pc.L - 1;
@@ -495,8 +500,8 @@ void piece_decode_kernel(const DecodeArgs a) {
     TileListCore<D, E> core;
     core.k_pool = a.k_pool;
     core.v_pool = a.v_pool;
-    core.rs = a.Hkv * D;
-    core.hoff = h * D;
+    core.rs = (a.Hkv / a.hdiv) * D;
+    core.hoff = (h / a.hdiv) * D;
     core.scale_log2 = a.scale_log2;
     core.stage = smem + w * C::STAGE;
     const int ntiles = t_first < t_end ? (t_end - t_first + kWaves - 1) / kWaves : 0;
@@ -520,8 +525,8 @@ void piece_decode_kernel(const DecodeArgs a) {
       if (tn >= 0 && tn % kWaves == 0) {
         core.new_tile = tn / kWaves;
         core.new_row = (pc.L - 1) & (kTile - 1);
-        const f16* kr = a.k_new + (int64_t)b * a.new_stride + (int64_t)h * D;
-        const f16* vr = a.v_new + (int64_t)b * a.new_stride + (int64_t)h * D;
+        const f16* kr = a.k_new + (int64_t)b * a.new_stride + (int64_t)(h / a.hdiv) * D;
+        const f16* vr = a.v_new + (int64_t)b * a.new_stride + (int64_t)(h / a.hdiv) * D;
 #pragma unroll
         for (int s = 0; s < C::NK; ++s) core.knew[s] = ld16(kr + (4 * s + g) * 8);
         core.vnew = ld16(vr + (lane % C::CPR) * 8);
@@ -1529,12 +1534,27 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   // prefix; one wave per SIMD with its spills in AGPRs: 1.9-2.4x the generic
   // kernel's rate)
   const bool mfma256 = head_dim == 256 && !f32 && plan == nullptr && cascade == nullptr;
-  if ((head_dim != 64 && head_dim != 128 && !mfma256) || G > kMaxGroup)
+  // a group above 16 (unplanned, no shared prefix) is split into hdiv virtual
+  // KV heads of G / hdiv <= 16 query heads, each reading its pool head's K/V;
+  // splits that would leave fewer than 8 query heads per read of the K/V (a
+  // group with no divisor in 8..16) stay on the generic kernel
+  int hdiv = 1;
+  if (G > kMaxGroup && plan == nullptr && cascade == nullptr) {
+    for (int v = 2; v <= G; ++v) {
+      if (G % v == 0 && G / v <= kMaxGroup) {
+        if (G / v >= 8) hdiv = v;
+        break;
+      }
+    }
+  }
+  const int hkv_v = kv_heads * hdiv;  // KV heads as the kernels see them
+  const int G_v = G / hdiv;
+  if ((head_dim != 64 && head_dim != 128 && !mfma256) || G_v > kMaxGroup)
     return decode_generic(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
                           num_blocks, block_tables, table_stride, context_lens, workspace,
                           workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size,
                           scale, target_splits, stream, plan != nullptr, bf16 ? 1 : (f32 ? 2 : 0));
-  if ((int64_t)batch * kv_heads > kMaxTickets) return FE_ERR_UNSUPPORTED;
+  if ((int64_t)batch * hkv_v > kMaxTickets) return FE_ERR_UNSUPPORTED;
   const int bs_log2 = log2_exact(block_size);
   if (bs_log2 < 0) return FE_ERR_UNSUPPORTED;
   // the shared-prefix split needs 16-token-aligned suffixes (block-size-16k path)
@@ -1554,7 +1574,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   // kMaxPieces pieces: contexts up to 64 * 64 * 64 = 262144 tokens
   if ((int64_t)table_stride * block_size > 262144) return FE_ERR_UNSUPPORTED;
   const int max_len = table_stride * block_size;
-  const int target = effective_target(batch, kv_heads, max_len, target_splits);
+  const int target = effective_target(batch, hkv_v, max_len, target_splits);
   if ((int64_t)(target + batch) * num_q_heads * head_dim * (int64_t)sizeof(float) >= ((int64_t)1 << 31))
     return FE_ERR_UNSUPPORTED;
   const size_t need = fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, max_len, target);
@@ -1589,8 +1609,9 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   a.W = table_stride;
   a.B = batch;
   a.Hq = num_q_heads;
-  a.Hkv = kv_heads;
-  a.G = G;
+  a.Hkv = hkv_v;
+  a.G = G_v;
+  a.hdiv = hdiv;
   a.BS = block_size;
   a.bs_log2 = bs_log2;
   a.NB = num_blocks;
@@ -1701,6 +1722,7 @@ extern "C" int fe_paged_decode_plan(const int32_t* block_tables, int table_strid
   a.W = table_stride;
   a.B = batch;
   a.Hkv = kv_heads;
+  a.hdiv = 1;
   a.BS = block_size;
   a.bs_log2 = bs_log2;
   a.NB = num_blocks;

@@ -26,7 +26,9 @@
  * of two.  head_dim 64 and 128 with a decode group (num_q_heads / kv_heads)
  * of at most 16 run on the matrix-core kernels, as does the prefill at any
  * group size; so do the fp16 / bf16 decode (group <= 16, no shared prefix) and
- * prefill at head_dim 256, unplanned.  Every other head_dim from 1 to 512, and decode groups of 17
+ * prefill at head_dim 256, unplanned, and an unplanned decode (no shared
+ * prefix) whose group above 16 has a divisor from 8 to 16: it is split into
+ * that many-headed virtual KV heads, each reading its pool head's K/V.  Every other head_dim from 1 to 512, and decode groups of 17
  * to 128, run on a generic kernel (key splits of a row or tiles of prefill
  * tokens per workgroup, fp32 arithmetic) as long as group * head_dim <= 8192
  * (head_dim rounded up to a multiple of 8): same entry points, same results

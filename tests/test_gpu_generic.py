@@ -1,7 +1,8 @@
 """GPU: head dims other than 64 / 128 and decode groups of 17-128 query heads per KV
-head -- the generic attention kernel, and at head_dim 256 in 16 bits the matrix-core
-decode (groups <= 16) and prefill instantiated at 256 -- against the oracle, in fp16,
-bf16 and fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
+head -- the generic attention kernel; at head_dim 256 in 16 bits the matrix-core
+decode (groups <= 16) and prefill instantiated at 256; and groups above 16 with a
+divisor in 8..16 (24, 32, 48, 64 below) split into virtual KV heads on the matrix-core
+decode -- against the oracle, in fp16, bf16 and fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
 head_dim 64 / 128 below run there.)
 
 The reference's Triton decode takes any head_dim (BLOCK_D = next_power_of_2
@@ -358,7 +359,7 @@ def test_generic_shapes_outside_the_envelope_are_refused():
     c = torch.ones(1, dtype=torch.int32, device=DEV)
     with pytest.raises(RuntimeError, match="unsupported"):
         ops.paged_decode(q, pool, pool, t, c)
-    q = torch.zeros(1, 72, 128, dtype=FP16, device=DEV)  # group 72 x 128 > 8192
+    q = torch.zeros(1, 67, 128, dtype=FP16, device=DEV)  # group 67 (prime) x 128 > 8192
     pool = torch.zeros(2, 16, 1, 128, dtype=FP16, device=DEV)
     with pytest.raises(RuntimeError, match="unsupported"):
         ops.paged_decode(q, pool, pool, t, c)
