@@ -1429,7 +1429,6 @@ extern "C" size_t fe_paged_decode_workspace_size(int batch, int num_q_heads, int
 namespace {
 
 bool aligned_to(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
-constexpr int generic_max_splits = 32;
 constexpr int kGenericWorkgroups = 2048;  // the generic decode's default launch size
 
 // Shapes the matrix-core decode does not take (head_dim other than 64 / 128,
@@ -1468,14 +1467,15 @@ int decode_generic(const void* q, int64_t q_batch_stride, void* out, const void*
   if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
     return FE_ERR_WORKSPACE;
   // key splits per row: about kGenericWorkgroups workgroups in all (or
-  // target_splits per KV head when given), no more than one per 64 keys of the
-  // table width, and as many as the workspace holds
+  // target_splits per KV head when given), no more than the documented
+  // workspace size holds (so a larger workspace does not change the result)
+  // nor one per 64 keys of the table width
   const int64_t want = target_splits > 0 ? (int64_t)target_splits * kv_heads : kGenericWorkgroups;
   int64_t splits = (want + (int64_t)batch * kv_heads - 1) / ((int64_t)batch * kv_heads);
-  splits = std::min<int64_t>(splits, generic_max_splits);
+  splits = std::min<int64_t>(splits, kGenericWsSplits);
   splits = std::min<int64_t>(splits, (max_len + 63) / 64);
   while (splits > 1 &&
-         kTicketBytes + generic_ws_bytes(batch, num_q_heads, head_dim, (int)splits) > workspace_bytes)
+         kTicketBytes + generic_ws_bytes(batch, num_q_heads, head_dim, (int)splits) > need)
     --splits;
   if (splits < 1) splits = 1;
   GenericAttn g{};

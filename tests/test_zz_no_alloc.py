@@ -134,6 +134,19 @@ def test_noalloc_decode_matches_the_workspace_entry_point_twice():
     _check(small, "noalloc 16 rows")
 
 
+def test_noalloc_decode_at_other_head_dims_and_groups_then_c2():
+    """Head_dim 96 (the generic kernel: its key-split partials in the scratch past the
+    split-K tickets) and a group of 32 split into virtual KV heads, each byte-identical
+    to the workspace form; then C2 again on the same scratch, whose tickets the
+    generic kernel has left at zero."""
+    lens = [1, 90, 700, 4000, 33, 2048]
+    _check(workloads.make_decode_workload("d96", 23, len(lens), 12, 2, 96, lens,
+                                          with_new_kv=True), "noalloc D 96")
+    _check(workloads.make_decode_workload("g32", 24, len(lens), 32, 1, 128, lens,
+                                          with_new_kv=True), "noalloc group 32")
+    _check(workloads.c2_workload(), "noalloc C2 after")
+
+
 def test_noalloc_refuses_calls_beyond_its_scratch():
     """A call whose partials exceed the 16 MiB array returns FE_ERR_SCRATCH_LIMIT and
     launches nothing (the output keeps its contents)."""
