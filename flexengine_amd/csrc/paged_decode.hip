@@ -1530,6 +1530,10 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   if (f32 && plan != nullptr) return FE_ERR_UNSUPPORTED;
   FE_CHECK_ARG(num_q_heads % kv_heads == 0);
   const int G = num_q_heads / kv_heads;
+  // the shared-prefix kernels take head_dim 64 / 128 and groups <= 16: at other
+  // shapes a shared-prefix call is a plain decode of every row over its own
+  // table (whose first pages are the shared ones), on whichever kernel takes it
+  if (cascade && ((head_dim != 64 && head_dim != 128) || G > kMaxGroup)) cascade = nullptr;
   // head_dim 256 in 16 bits runs on the piece kernel too (unplanned, no shared
   // prefix; one wave per SIMD with its spills in AGPRs: 1.9-2.4x the generic
   // kernel's rate)

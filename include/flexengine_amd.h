@@ -35,7 +35,9 @@
  * to the same tolerances; the decode's key-split partials use the workspace
  * (fe_paged_decode_workspace_size covers them), the prefill none; no plan is
  * taken (the _planned calls return FE_ERR_UNSUPPORTED there), and a
- * shared-prefix decode attends each row over its own table.  The KV page movers need
+ * shared-prefix decode at any shape but head_dim 64 / 128 with a group <= 16
+ * attends each row over its own table (a plain decode, on whichever kernel
+ * takes the shape).  The KV page movers need
  * head_dim % 8 == 0 (fp16 / bf16) or % 4 == 0 (fp32).
  * Element types: fp16 (the unsuffixed entry points), bfloat16 (_bf16) and
  * fp32 (_f32: the KV movers, the decode and the prefill).

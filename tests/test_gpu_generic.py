@@ -269,11 +269,14 @@ def test_generic_prefill_matches_oracle(shape):
     _close(out, exp, shape[4], f"prefill {_ids(shape)}")
 
 
-def test_generic_shared_prefix_equals_plain_decode():
-    """fe_paged_decode_shared_prefix at a generic shape attends every row over its own
-    table (whose first pages are the shared ones): the same result as fe_paged_decode."""
-    d, hq, hkv, bs = 96, 12, 2, 16
-    g = torch.Generator().manual_seed(781)
+@pytest.mark.parametrize("d,hq,hkv", [(96, 12, 2), (256, 8, 1), (128, 32, 1)])
+def test_generic_shared_prefix_equals_plain_decode(d, hq, hkv):
+    """fe_paged_decode_shared_prefix at shapes the shared-prefix kernels do not take
+    (head_dim 96: the generic kernel; 256 and a group of 32: the piece kernel) attends
+    every row over its own table (whose first pages are the shared ones): the same
+    result as fe_paged_decode."""
+    bs = 16
+    g = torch.Generator().manual_seed(781 + d + hq)
     prefix, suffixes = 160, [1, 30, 77, 200]
     pre_pages = prefix // bs
     pages = [pre_pages + math.ceil(s / bs) for s in suffixes]
