@@ -421,14 +421,19 @@ struct F32Core {
 // form a list held one per lane (lane k: tile k, k < 64), filled from the block
 // tables before the first load, so no table access sits between two tiles'
 // K/V loads.
-template <int D, class E = Fp16>
+//
+// PAD: the real head_dim is below D (D = the next of 64 / 128 / 256 computed):
+// rows are nch 16-byte chunks long in the pool, the chunks past them are zeros
+// in the K and V registers (q is zero there too) and never written.
+template <int D, class E = Fp16, bool PAD = false>
 struct TileListCore {
   using C = TileCfg<D>;
 
   const f16* k_pool;
   const f16* v_pool;
-  int rs;                 // elements per pool row (kv_heads * D)
-  int hoff;               // kv_head * D
+  int rs;                 // elements per pool row (kv_heads * head_dim)
+  int hoff;               // kv_head * head_dim
+  int nch;                // PAD: 16-byte chunks of a real row
   float scale_log2;
   unsigned char* stage;   // per-wave LDS tile, C::STAGE bytes
   int ntiles;             // tiles in the list (<= 64)
@@ -493,7 +498,10 @@ struct TileListCore {
     const uint64_t addr = reinterpret_cast<uint64_t>(pool + base);
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)addr);
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32));
-    const int nrec = __builtin_amdgcn_readfirstlane(rows * rs * 2);
+    // PAD: the extent ends at the real end of the last key's row, so the
+    // chunks past it in that row read as zeros rather than past the pool
+    const int nrec = __builtin_amdgcn_readfirstlane(
+        PAD ? (rows > 0 ? ((rows - 1) * rs + nch * 8) * 2 : 0) : rows * rs * 2);
     void* p = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
     // dword 3 = 0x00020000: 32-bit data format, the gfx9 setting for raw dword access
     return __builtin_amdgcn_make_buffer_rsrc(p, 0, nrec, 0x00020000);
@@ -506,11 +514,27 @@ struct TileListCore {
     const __amdgpu_buffer_rsrc_t kr = tile_rsrc(k_pool, base, rows);
     const __amdgpu_buffer_rsrc_t vr = tile_rsrc(v_pool, base, rows);
     const uint32_t ko = k_off0();
-#pragma unroll
-    for (int s = 0; s < C::NK; ++s) kk[s] = buf_ld16(kr, ko, k_soff(s));
     const uint32_t vo = v_off0();
+    if constexpr (PAD) {
+      // only the real chunks of a row are loaded: the rest stay zeros
+      const int lane = lane_id();
 #pragma unroll
-    for (int j = 0; j < C::NK; ++j) vv[j] = buf_ld16(vr, vo, v_soff(j));
+      for (int s = 0; s < C::NK; ++s) {
+        kk[s] = f16x8{};
+        if (4 * s + (lane >> 4) < nch) kk[s] = buf_ld16(kr, ko, k_soff(s));
+      }
+      const bool vin = lane % C::CPR < nch;
+#pragma unroll
+      for (int j = 0; j < C::NK; ++j) {
+        vv[j] = f16x8{};
+        if (vin) vv[j] = buf_ld16(vr, vo, v_soff(j));
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < C::NK; ++s) kk[s] = buf_ld16(kr, ko, k_soff(s));
+#pragma unroll
+      for (int j = 0; j < C::NK; ++j) vv[j] = buf_ld16(vr, vo, v_soff(j));
+    }
   }
 
   // One tile held in kk / vv: scores, V staging, softmax and PV.
@@ -571,12 +595,13 @@ struct TileListCore {
     if ((lane & 15) == new_row) {
 #pragma unroll
       for (int s = 0; s < C::NK; ++s)
-        *reinterpret_cast<f16x8*>(kb + k_off0() + k_soff(s)) = knew[s];
+        if (!PAD || 4 * s + (lane >> 4) < nch)
+          *reinterpret_cast<f16x8*>(kb + k_off0() + k_soff(s)) = knew[s];
     }
     const int vrow = lane / C::CPR;
 #pragma unroll
     for (int j = 0; j < C::NK; ++j)
-      if (j * C::RPI + vrow == new_row)
+      if (j * C::RPI + vrow == new_row && (!PAD || lane % C::CPR < nch))
         *reinterpret_cast<f16x8*>(vb + v_off0() + v_soff(j)) = vnew;
   }
 

@@ -455,6 +455,15 @@ struct GenericAttn {
 };
 // head_dim rounded up to a multiple of 8 (the kernel's LDS rows)
 __attribute__((visibility("hidden"))) int generic_padded_dims(int d);
+
+// head_dim as the 16-bit matrix-core decode and prefill compute it: a multiple
+// of 8 below 256 other than 64 / 128 runs padded to the next of 64 / 128 / 256
+// (the dims past head_dim zeros in q and K, never read from the pools nor
+// written to the output)
+inline int mfma_padded_head_dim(int d) {
+  if (d % 8 != 0 || d >= 256) return d;
+  return d <= 64 ? 64 : (d <= 128 ? 128 : 256);
+}
 __attribute__((visibility("hidden"))) bool generic_shape(int hq, int hkv, int d);
 __attribute__((visibility("hidden"))) int generic_attention(const GenericAttn& g,
                                                             hipStream_t stream);

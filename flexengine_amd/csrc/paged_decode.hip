@@ -115,6 +115,10 @@ struct DecodeArgs {
   // groups of G query heads: virtual head h reads pool head h / hdiv, whose
   // rows are (Hkv / hdiv) * D elements apart)
   int hdiv;
+  // head dims computed as the next of 64 / 128 / 256 (the padded kernels): the
+  // real head_dim, by which q, the pools, the new rows and the outputs are laid
+  // out; the dims past it are zeros in q and K and never stored
+  int dr;
   int max_len;       // W * BS: longest context the tables can address
   float scale_log2;  // softmax scale * log2(e)
   int nwg;           // balanced kernel: workgroups sharing the tile order (= grid size)
@@ -219,7 +223,7 @@ __device__ __forceinline__ void fold_prefix(const DecodeArgs& a, int64_t r, int 
   M = newM;
 }
 
-template <int D, class E = Fp16>
+template <int D, class E = Fp16, bool PAD = false>
 __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, int first,
                                              int ns, bool pre = false) {
   const int G = a.G;
@@ -269,7 +273,13 @@ __device__ __forceinline__ void merge_pieces(const DecodeArgs& a, int b, int h, 
     // the shared-prefix part, written by the launch before this one
     if (pre) fold_prefix<D>(a, (int64_t)b * a.Hq + h * G + hh, (e4 * 4) % D, M, den, num);
     const float inv = 1.f / den;
-    store_out4<E>(a.out, ((int64_t)b * a.Hq + h * G) * D + e4 * 4, num * inv);
+    if constexpr (PAD) {
+      const int d = e4 * 4 - hh * D;  // the partials keep the padded layout
+      if (d < a.dr)
+        store_out4<E>(a.out, ((int64_t)b * a.Hq + h * G + hh) * a.dr + d, num * inv);
+    } else {
+      store_out4<E>(a.out, ((int64_t)b * a.Hq + h * G) * D + e4 * 4, num * inv);
+    }
   }
 }
 
@@ -347,7 +357,7 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const DecodeArgs 
       tile_list_row(a, pc, w);
 }
 
-template <int D, bool PAGE16, bool PLANNED = false, class E = Fp16>
+template <int D, bool PAGE16, bool PLANNED = false, class E = Fp16, bool PAD = false>
 __global__ __launch_bounds__(kThreads)
 // (fp32 and head_dim 256: one wave per SIMD, the rest of the register file held
 // as AGPRs -- at two waves D = 256 spilled 168-388 bytes per lane to scratch and
@@ -359,6 +369,8 @@ void piece_decode_kernel(const DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
 
   FE_TL_MARK(0);  // start
+  // the real head_dim (layout of q, pools, new rows, outputs)
+  const int DR = PAD ? a.dr : D;
   const int h = blockIdx.x % a.Hkv;
   const int item = blockIdx.x / a.Hkv;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -407,8 +419,8 @@ void piece_decode_kernel(const DecodeArgs a) {
       // not this call's plan: every workgroup of the grid (items >= batch, so one
       // per row and kv head) fills its row's heads with NaN; the error word is set
       if (item < a.B) {
-        for (int e = threadIdx.x; e < a.G * D; e += kThreads)
-          store_out1<E>(a.out, ((int64_t)item * a.Hq + h * a.G) * D + e, __builtin_nanf(""));
+        for (int e = threadIdx.x; e < a.G * DR; e += kThreads)
+          store_out1<E>(a.out, ((int64_t)item * a.Hq + h * a.G) * DR + e, __builtin_nanf(""));
       }
       if (item == 0 && h == 0 && threadIdx.x == 0)
         __hip_atomic_store(a.plan + kPlanDesc - 1, kPlanErrSizes, __ATOMIC_RELAXED,
@@ -418,8 +430,8 @@ void piece_decode_kernel(const DecodeArgs a) {
     // spare workgroup: zero rows of inactive sequences
     const int b = spare_row;
     if (b < a.B && seq_len(a.ctx, b, a.max_len) == 0) {
-      for (int e = threadIdx.x; e < a.G * D; e += kThreads)
-        store_out1<E>(a.out, ((int64_t)b * a.Hq + h * a.G) * D + e, 0.f);
+      for (int e = threadIdx.x; e < a.G * DR; e += kThreads)
+        store_out1<E>(a.out, ((int64_t)b * a.Hq + h * a.G) * DR + e, 0.f);
     }
     return;
   }
@@ -488,20 +500,28 @@ void piece_decode_kernel(const DecodeArgs a) {
   f16x8 qv[C::NK];
   {
     const int hq = h * G + (n < G ? n : G - 1);
-    const f16* qrow = a.q + (int64_t)b * a.q_stride + (int64_t)hq * D;
+    const f16* qrow = a.q + (int64_t)b * a.q_stride + (int64_t)hq * DR;
 #pragma unroll
     for (int s = 0; s < C::NK; ++s) {
-      const f16x8 v = ld16(qrow + (4 * s + g) * 8);
-      qv[s] = n < G ? v : f16x8{};
+      if constexpr (PAD) {
+        // chunks past the real head_dim are zeros (and not loaded)
+        const bool in = (4 * s + g) * 8 < DR;
+        const f16x8 v = in ? ld16(qrow + (4 * s + g) * 8) : f16x8{};
+        qv[s] = n < G ? v : f16x8{};
+      } else {
+        const f16x8 v = ld16(qrow + (4 * s + g) * 8);
+        qv[s] = n < G ? v : f16x8{};
+      }
     }
   }
   if constexpr (PAGE16) {
     // the wave's tiles t_first, t_first + 4, ... of the piece as a tile list
-    TileListCore<D, E> core;
+    TileListCore<D, E, PAD> core;
     core.k_pool = a.k_pool;
     core.v_pool = a.v_pool;
-    core.rs = (a.Hkv / a.hdiv) * D;
-    core.hoff = (h / a.hdiv) * D;
+    core.rs = (a.Hkv / a.hdiv) * DR;
+    core.hoff = (h / a.hdiv) * DR;
+    core.nch = DR / 8;
     core.scale_log2 = a.scale_log2;
     core.stage = smem + w * C::STAGE;
     const int ntiles = t_first < t_end ? (t_end - t_first + kWaves - 1) / kWaves : 0;
@@ -525,11 +545,18 @@ void piece_decode_kernel(const DecodeArgs a) {
       if (tn >= 0 && tn % kWaves == 0) {
         core.new_tile = tn / kWaves;
         core.new_row = (pc.L - 1) & (kTile - 1);
-        const f16* kr = a.k_new + (int64_t)b * a.new_stride + (int64_t)(h / a.hdiv) * D;
-        const f16* vr = a.v_new + (int64_t)b * a.new_stride + (int64_t)(h / a.hdiv) * D;
+        const f16* kr = a.k_new + (int64_t)b * a.new_stride + (int64_t)(h / a.hdiv) * DR;
+        const f16* vr = a.v_new + (int64_t)b * a.new_stride + (int64_t)(h / a.hdiv) * DR;
+        if constexpr (PAD) {
 #pragma unroll
-        for (int s = 0; s < C::NK; ++s) core.knew[s] = ld16(kr + (4 * s + g) * 8);
-        core.vnew = ld16(vr + (lane % C::CPR) * 8);
+          for (int s = 0; s < C::NK; ++s)
+            core.knew[s] = (4 * s + g) * 8 < DR ? ld16(kr + (4 * s + g) * 8) : f16x8{};
+          core.vnew = (lane % C::CPR) * 8 < DR ? ld16(vr + (lane % C::CPR) * 8) : f16x8{};
+        } else {
+#pragma unroll
+          for (int s = 0; s < C::NK; ++s) core.knew[s] = ld16(kr + (4 * s + g) * 8);
+          core.vnew = ld16(vr + (lane % C::CPR) * 8);
+        }
       }
     }
 #pragma unroll
@@ -610,9 +637,11 @@ void piece_decode_kernel(const DecodeArgs a) {
   const int hq = h * G + (n < G ? n : G - 1);
   if (!split) {
     if (n < G) {
-      const int64_t orow = ((int64_t)b * a.Hq + hq) * D + 4 * g;
+      const int64_t orow = ((int64_t)b * a.Hq + hq) * DR + 4 * g;
 #pragma unroll
-      for (int xi = 0; xi < XW; ++xi) store_out4<E>(a.out, orow + 16 * (w * XW + xi), ox[xi]);
+      for (int xi = 0; xi < XW; ++xi)
+        if (!PAD || 16 * (w * XW + xi) + 4 * g < DR)
+          store_out4<E>(a.out, orow + 16 * (w * XW + xi), ox[xi]);
     }
     FE_TL_MARK(4);  // output stores issued
     return;
@@ -644,7 +673,7 @@ void piece_decode_kernel(const DecodeArgs a) {
   FE_TL_SET(6, *flag ? 7 : 3);
   if (!*flag) return;
   if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  merge_pieces<D, E>(a, b, h, pc.id - pc.split, pc.nsplit, pc.tok0 > 0);
+  merge_pieces<D, E, PAD>(a, b, h, pc.id - pc.split, pc.nsplit, pc.tok0 > 0);
   FE_TL_MARK(5);  // merge stores issued
 }
 
@@ -1400,6 +1429,15 @@ int launch_decode(const DecodeArgs& a, hipStream_t stream) {
   return FE_LAUNCH_STATUS();
 }
 
+// Padded head dims: 16-bit pools, unplanned, block sizes that are multiples of 16.
+template <int D, class E>
+int launch_decode_padded(const DecodeArgs& a, hipStream_t stream) {
+  const dim3 grid((a.target + 2 * a.B) * a.Hkv);
+  hipLaunchKernelGGL((piece_decode_kernel<D, true, false, E, true>), grid, dim3(kThreads),
+                     PieceLds<D>::bytes, stream, a);
+  return FE_LAUNCH_STATUS();
+}
+
 }  // namespace
 
 // The generic kernel's split partials: [batch * hq][splits] outputs and LSEs
@@ -1415,7 +1453,9 @@ extern "C" size_t fe_paged_decode_workspace_size(int batch, int num_q_heads, int
     return 0;
   // sized for the largest default (kv_heads = 1): valid for every kv_heads
   const int target = effective_target(batch, 1, max_context, target_splits);
-  const size_t pieces = kTicketBytes + ws_o_bytes(batch, num_q_heads, head_dim, target) +
+  // the padded kernels keep their partials at the computed head_dim
+  const size_t pieces = kTicketBytes +
+                        ws_o_bytes(batch, num_q_heads, mfma_padded_head_dim(head_dim), target) +
                         ws_lse_bytes(batch, num_q_heads, target);
   // head dims other than 64 / 128 run on the generic kernel: room for its splits
   if (head_dim != 64 && head_dim != 128) {
@@ -1553,7 +1593,13 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   }
   const int hkv_v = kv_heads * hdiv;  // KV heads as the kernels see them
   const int G_v = G / hdiv;
-  if ((head_dim != 64 && head_dim != 128 && !mfma256) || G_v > kMaxGroup)
+  // other multiples of 8 below 256 (16-bit, unplanned, no shared prefix, pages
+  // of 16k tokens): the piece kernel at the next of 64 / 128 / 256, the dims
+  // past head_dim zeros in q and K and never stored
+  const int dpad = mfma_padded_head_dim(head_dim);
+  const bool padded = dpad != head_dim && !f32 && plan == nullptr && cascade == nullptr &&
+                      block_size % kTile == 0;
+  if ((head_dim != 64 && head_dim != 128 && !mfma256 && !padded) || G_v > kMaxGroup)
     return decode_generic(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
                           num_blocks, block_tables, table_stride, context_lens, workspace,
                           workspace_bytes, batch, num_q_heads, kv_heads, head_dim, block_size,
@@ -1579,7 +1625,8 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   if ((int64_t)table_stride * block_size > 262144) return FE_ERR_UNSUPPORTED;
   const int max_len = table_stride * block_size;
   const int target = effective_target(batch, hkv_v, max_len, target_splits);
-  if ((int64_t)(target + batch) * num_q_heads * head_dim * (int64_t)sizeof(float) >= ((int64_t)1 << 31))
+  const int dc = padded ? dpad : head_dim;  // head_dim as computed
+  if ((int64_t)(target + batch) * num_q_heads * dc * (int64_t)sizeof(float) >= ((int64_t)1 << 31))
     return FE_ERR_UNSUPPORTED;
   const size_t need = fe_paged_decode_workspace_size(batch, num_q_heads, head_dim, max_len, target);
   const size_t need_all =
@@ -1602,7 +1649,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   a.tickets = (int*)ws;
   ws += kTicketBytes;
   a.ws_o = (float*)ws;
-  ws += ws_o_bytes(batch, num_q_heads, head_dim, target);
+  ws += ws_o_bytes(batch, num_q_heads, dc, target);
   a.ws_lse = (float*)ws;
   a.tok0 = nullptr;
   a.pre_o = nullptr;
@@ -1616,6 +1663,7 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   a.Hkv = hkv_v;
   a.G = G_v;
   a.hdiv = hdiv;
+  a.dr = head_dim;
   a.BS = block_size;
   a.bs_log2 = bs_log2;
   a.NB = num_blocks;
@@ -1678,6 +1726,13 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     a.pre_splits = c.splits;
   }
   if (f32) return head_dim == 64 ? launch_decode<64, F32>(a, s) : launch_decode<128, F32>(a, s);
+  if (padded) {
+    if (dpad == 64)
+      return bf16 ? launch_decode_padded<64, Bf16>(a, s) : launch_decode_padded<64, Fp16>(a, s);
+    if (dpad == 128)
+      return bf16 ? launch_decode_padded<128, Bf16>(a, s) : launch_decode_padded<128, Fp16>(a, s);
+    return bf16 ? launch_decode_padded<256, Bf16>(a, s) : launch_decode_padded<256, Fp16>(a, s);
+  }
   if (head_dim == 256) return bf16 ? launch_decode<256, Bf16>(a, s) : launch_decode<256, Fp16>(a, s);
   if (bf16) return head_dim == 64 ? launch_decode<64, Bf16>(a, s) : launch_decode<128, Bf16>(a, s);
   return head_dim == 64 ? launch_decode<64, Fp16>(a, s) : launch_decode<128, Fp16>(a, s);
@@ -1727,6 +1782,7 @@ extern "C" int fe_paged_decode_plan(const int32_t* block_tables, int table_strid
   a.B = batch;
   a.Hkv = kv_heads;
   a.hdiv = 1;
+  a.dr = 0;
   a.BS = block_size;
   a.bs_log2 = bs_log2;
   a.NB = num_blocks;

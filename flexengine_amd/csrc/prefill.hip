@@ -97,6 +97,7 @@ struct PrefillArgs {
   int64_t q_stride;  // elements from one query row (token or sequence) to the next
   int W, S, total_q, Hq, Hkv, G, BS, bs_log2, NB, KS;
   int nwg_max;       // stream-K kernel: workgroups of the launch
+  int dr;            // padded tile kernel: the real head_dim (layout of q, pools, out)
   float scale_log2;
   // shared-prefix (cascade) mode: "sequence" s is a group of decode rows
   // q_off[s] .. q_off[s+1]-1 sharing the first prefix_len[s] keys of row
@@ -195,13 +196,14 @@ __device__ void write_suffix_starts(const PrefillArgs& a, Offs offs) {
 // m_run (base 2) and its sum l.  One split: normalise and store.  Several:
 // write this split's partial (device-coherent stores), draw the row block's
 // ticket; the last split merges all of them.
-template <int D, int RT, class E>
+template <int D, int RT, class E, bool PAD = false>
 __device__ __forceinline__ void finish_split(const PrefillArgs& a, const RowBlock& rb, int item,
                                              int h, int ks, int wr0, int r0, int r_last,
                                              const bool (&valid)[RT], const float (&m_run)[RT],
                                              const float (&l)[RT], const f32x4 (&o)[RT][D / 16],
                                              int* last) {
   constexpr int NX = D / 16;
+  const int DR = PAD ? a.dr : D;  // output row length
   const int G = a.G;
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -221,10 +223,11 @@ __device__ __forceinline__ void finish_split(const PrefillArgs& a, const RowBloc
     const int64_t orow_idx = (int64_t)(rb.q0 + row / G) * a.Hq + h * G + row % G;
     const float inv = l[rt] > 0.f ? 1.f / l[rt] : 0.f;
     if (!split) {
-      f16* orow = a.out + orow_idx * D + 4 * g;
+      f16* orow = a.out + orow_idx * DR + 4 * g;
 #pragma unroll
       for (int x = 0; x < NX; ++x)
-        *reinterpret_cast<f16x4*>(orow + 16 * x) = to16x4<E>(o[rt][x] * inv);
+        if (!PAD || 16 * x + 4 * g < DR)
+          *reinterpret_cast<f16x4*>(orow + 16 * x) = to16x4<E>(o[rt][x] * inv);
     } else {
       // device-coherent stores through one wave-uniform descriptor per array
       // (the host keeps the partial arrays under 2 GiB)
@@ -295,16 +298,22 @@ __device__ __forceinline__ void finish_split(const PrefillArgs& a, const RowBloc
         den += wgt;
       }
       const float inv = den > 0.f ? 1.f / den : 0.f;
-      *reinterpret_cast<f16x4*>(a.out + orow_idx[u] * D + d4) = to16x4<E>(num * inv);
+      if (!PAD || d4 < DR)
+        *reinterpret_cast<f16x4*>(a.out + orow_idx[u] * DR + d4) = to16x4<E>(num * inv);
     }
   }
 }
 
 // (head_dim 256: one wave per SIMD, 174 VGPRs + 72 AGPRs, no scratch)
-template <int D, int RT, class E = Fp16>
+//
+// PAD: head_dim a.dr below D (a multiple of 8): q, the pools and the output are
+// laid out by a.dr; the dims past it are zeros in q, K and V (never loaded)
+// and never stored.
+template <int D, int RT, class E = Fp16, bool PAD = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8)))
 void prefill_kernel(const PrefillArgs a) {
   using P = PCfg<D, RT>;
+  const int DR = PAD ? a.dr : D;
   extern __shared__ __align__(16) unsigned char smem[];
 
   // workgroup i: (KV head, key split) pair i % P, row block i / P (P = Hkv * KS);
@@ -349,10 +358,10 @@ void prefill_kernel(const PrefillArgs a) {
     valid[rt] = row < total_rows;
     const int rc = valid[rt] ? row : r_last;
     pos[rt] = valid[rt] ? cached + rc / G : -1;
-    const f16* qrow = a.q + (int64_t)(rb.q0 + rc / G) * a.q_stride + (h * G + rc % G) * D + 8 * g;
+    const f16* qrow = a.q + (int64_t)(rb.q0 + rc / G) * a.q_stride + (h * G + rc % G) * DR + 8 * g;
 #pragma unroll
     for (int c = 0; c < P::NC; ++c) {
-      const f16x8 v = ld16(qrow + 32 * c);
+      const f16x8 v = !PAD || 32 * c + 8 * g < DR ? ld16(qrow + 32 * c) : f16x8{};
       qv[rt][c] = valid[rt] ? v : f16x8{};
     }
   }
@@ -377,6 +386,7 @@ void prefill_kernel(const PrefillArgs a) {
   const int32_t* trow = a.tables + (int64_t)rb.s * a.W;
   const int chunk = tid % P::CPR;
   const int krow = tid / P::CPR;
+  const bool chunk_in = !PAD || chunk * 8 < DR;  // a real chunk of the row
   f16x8 kst[P::LOADS], vst[P::LOADS];
   int ids[P::LOADS];
   auto fetch_ids = [&](int kb) __attribute__((always_inline)) {
@@ -396,9 +406,15 @@ void prefill_kernel(const PrefillArgs a) {
       // gives it probability 0 (no block below unmasked_blocks reaches it)
       const int kc = min(kb * kBlockKeys + krow + P::KPL * i, key_end - 1);
       const int blk = clamp_block(ids[i], a.NB);
-      const int64_t off = (int64_t)(blk * a.BS + (kc & (a.BS - 1))) * (a.Hkv * D) + h * D + chunk * 8;
-      kst[i] = ld16(a.k_pool + off);
-      vst[i] = ld16(a.v_pool + off);
+      const int64_t off = (int64_t)(blk * a.BS + (kc & (a.BS - 1))) * (a.Hkv * DR) + h * DR + chunk * 8;
+      if (PAD) {
+        kst[i] = f16x8{};
+        vst[i] = f16x8{};
+      }
+      if (chunk_in) {
+        kst[i] = ld16(a.k_pool + off);
+        vst[i] = ld16(a.v_pool + off);
+      }
     }
   };
   auto store_block = [&](int stage) __attribute__((always_inline)) {
@@ -534,7 +550,7 @@ void prefill_kernel(const PrefillArgs a) {
     lt[rt] += shfl_xor_f(lt[rt], 32);
   }
   __shared__ int last;
-  finish_split<D, RT, E>(a, rb, item, h, ks, wr0, r0, r_last, valid, m_run, lt, o, &last);
+  finish_split<D, RT, E, PAD>(a, rb, item, h, ks, wr0, r0, r_last, valid, m_run, lt, o, &last);
 }
 
 // ---------------------------------------------------------------------------
@@ -1977,10 +1993,10 @@ inline int log2_exact(int x) {
   return l;
 }
 
-template <int D, int RT, class E = Fp16>
+template <int D, int RT, class E = Fp16, bool PAD = false>
 void launch_prefill(const PrefillArgs& a, int blocks, hipStream_t stream) {
   using P = PCfg<D, RT>;
-  hipLaunchKernelGGL((prefill_kernel<D, RT, E>), dim3(blocks * a.Hkv * a.KS),
+  hipLaunchKernelGGL((prefill_kernel<D, RT, E, PAD>), dim3(blocks * a.Hkv * a.KS),
                      dim3(kThreads), 2 * P::STAGE, stream, a);
 }
 
@@ -2025,10 +2041,12 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 struct Plan {
   int rt, blocks, ks;
 };
-inline Plan plan(int num_seqs, int total_q, int num_q_heads, int kv_heads) {
+// rt2: whether the kernel to launch has a two-row-tile form (head_dim 256 has
+// one only: its row blocks, and so the grid, are then sized for one tile)
+inline Plan plan(int num_seqs, int total_q, int num_q_heads, int kv_heads, bool rt2 = true) {
   const int64_t rows = (int64_t)total_q * num_q_heads;  // (token, query head) rows
   Plan p;
-  p.rt = rows >= (int64_t)kRt2Blocks * PCfg<128, 2>::ROWS ? 2 : 1;
+  p.rt = rt2 && rows >= (int64_t)kRt2Blocks * PCfg<128, 2>::ROWS ? 2 : 1;
   const int per = kWaves * 16 * p.rt;
   const int G = num_q_heads / kv_heads;
   p.blocks = (int)(((int64_t)total_q * G + per - 1) / per) + num_seqs;
@@ -2082,12 +2100,14 @@ extern "C" size_t fe_prefill_workspace_size(int num_seqs, int total_q, int num_q
     return 0;
   // enough for either kernel (the size does not depend on the block size)
   const Plan p = plan(num_seqs, total_q, num_q_heads, kv_heads);
+  // the padded tile kernel keeps its partials at the computed head_dim
+  const int dc = mfma_padded_head_dim(head_dim);
   size_t need = kTicketBytes;
   if (p.ks > 1) {
     const size_t rows = (size_t)p.ks * total_q * num_q_heads;
-    need += align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
+    need += align256(rows * dc * sizeof(float)) + align256(rows * sizeof(float));
   }
-  const size_t sk = stream_ws_bytes(head_dim);
+  const size_t sk = stream_ws_bytes(dc);
   return need > sk ? need : sk;
 }
 
@@ -2150,7 +2170,11 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   // head_dim 256 in 16 bits runs on the tile kernel (one row tile per wave, no
   // plan); other head dims on the generic kernel
   const bool mfma256 = head_dim == 256 && !f32 && step_plan == nullptr;
-  if (head_dim != 64 && head_dim != 128 && !mfma256)
+  // other multiples of 8 below 256 in 16 bits (no plan): the tile kernel at the
+  // next of 64 / 128 / 256, the dims past head_dim zeros
+  const int dpad = mfma_padded_head_dim(head_dim);
+  const bool padded = dpad != head_dim && !f32 && step_plan == nullptr;
+  if (head_dim != 64 && head_dim != 128 && !mfma256 && !padded)
     return prefill_generic(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride,
                            q_offsets, context_lens, num_seqs, total_q, num_q_heads, kv_heads,
                            head_dim, block_size, scale, (hipStream_t)stream,
@@ -2202,10 +2226,11 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
     return FE_LAUNCH_STATUS();
   }
   const int nwg = stream_wgs();
-  const bool dma = head_dim != 256 &&
+  const bool dma = head_dim != 256 && !padded &&
                    stream_ok(block_size, table_stride, total_q, num_q_heads / kv_heads, num_seqs,
                              kv_heads, nwg);
-  const Plan p = plan(num_seqs, total_q, num_q_heads, kv_heads);
+  // (the workspace size takes the two-tile plan: its key splits are never fewer)
+  const Plan p = plan(num_seqs, total_q, num_q_heads, kv_heads, dpad != 256);
   // split-K tickets of prefill_kernel: one per (row block, KV head)
   if (!dma && (int64_t)p.blocks * kv_heads > kMaxTickets) return FE_ERR_UNSUPPORTED;
   // a plan is for the stream-K kernel (fe_prefill_plan refuses the sizes it cannot take)
@@ -2229,7 +2254,7 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   ws += kTicketBytes;
   const size_t rows = dma ? (size_t)2 * nwg * kDmaRows : (size_t)p.ks * total_q * num_q_heads;
   a.part_o = (float*)ws;
-  ws += align256(rows * head_dim * sizeof(float));
+  ws += align256(rows * (padded ? dpad : head_dim) * sizeof(float));
   a.part_lse = (float*)ws;
   ws += align256(rows * sizeof(float));
   a.W = table_stride;
@@ -2243,6 +2268,7 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   a.NB = num_blocks;
   a.KS = dma ? 1 : p.ks;
   a.nwg_max = nwg;
+  a.dr = head_dim;
   a.scale_log2 = scale * kLog2e;
   a.q_stride = (int64_t)num_q_heads * head_dim;
   a.prefix_len = nullptr;
@@ -2256,6 +2282,22 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
     if (head_dim == 64) launch_prefill_dma<64, Bf16>(a, s); else launch_prefill_dma<128, Bf16>(a, s);
   } else if (dma) {
     if (head_dim == 64) launch_prefill_dma<64, Fp16>(a, s); else launch_prefill_dma<128, Fp16>(a, s);
+  } else if (padded && dpad == 256) {
+    if (bf16) launch_prefill<256, 1, Bf16, true>(a, p.blocks, s);
+    else launch_prefill<256, 1, Fp16, true>(a, p.blocks, s);
+  } else if (padded) {
+    const bool r2 = p.rt == 2;
+    if (dpad == 64) {
+      if (bf16) r2 ? launch_prefill<64, 2, Bf16, true>(a, p.blocks, s)
+                   : launch_prefill<64, 1, Bf16, true>(a, p.blocks, s);
+      else r2 ? launch_prefill<64, 2, Fp16, true>(a, p.blocks, s)
+              : launch_prefill<64, 1, Fp16, true>(a, p.blocks, s);
+    } else {
+      if (bf16) r2 ? launch_prefill<128, 2, Bf16, true>(a, p.blocks, s)
+                   : launch_prefill<128, 1, Bf16, true>(a, p.blocks, s);
+      else r2 ? launch_prefill<128, 2, Fp16, true>(a, p.blocks, s)
+              : launch_prefill<128, 1, Fp16, true>(a, p.blocks, s);
+    }
   } else if (head_dim == 256) {
     if (bf16) launch_prefill<256, 1, Bf16>(a, p.blocks, s); else launch_prefill<256, 1>(a, p.blocks, s);
   } else if (bf16) {

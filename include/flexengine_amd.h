@@ -28,7 +28,12 @@
  * group size; so do the fp16 / bf16 decode (group <= 16, no shared prefix) and
  * prefill at head_dim 256, unplanned, and an unplanned decode (no shared
  * prefix) whose group above 16 has a divisor from 8 to 16: it is split into
- * that many-headed virtual KV heads, each reading its pool head's K/V.  Every other head_dim from 1 to 512, and decode groups of 17
+ * that many-headed virtual KV heads, each reading its pool head's K/V; an
+ * unplanned fp16 / bf16 decode (no shared prefix, block_size a multiple of 16)
+ * at any other head_dim that is a multiple of 8 below 256 runs on the
+ * matrix-core decode padded to the next of 64 / 128 / 256 (the dims past
+ * head_dim are zeros, never read from the pool nor written to the output;
+ * its workspace is sized at the padded head_dim).  Every other head_dim from 1 to 512, and decode groups of 17
  * to 128, run on a generic kernel (key splits of a row or tiles of prefill
  * tokens per workgroup, fp32 arithmetic) as long as group * head_dim <= 8192
  * (head_dim rounded up to a multiple of 8): same entry points, same results

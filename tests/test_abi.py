@@ -73,12 +73,16 @@ def test_host_side_validation_rejects_before_launch(lib):
     rc = lib.fe_paged_decode(null, 0, null, null, null, 0, null, null, 1, null, 1, null, null, 0,
                              1, 12, 2, 1024, 16, 0.1, 0, null)
     assert rc == _lib.FE_ERR_UNSUPPORTED
-    # group size 129 > 128; group 64 x head_dim 192 > 8192 elements
+    # group size 129 > 128; group 67 (no divisor from 8 to 16) x head_dim 136 > 8192
+    # elements (group 64 x 192 is taken: four virtual KV heads, padded to 256)
     rc = lib.fe_paged_decode(null, 0, null, null, null, 0, null, null, 1, null, 1, null, null, 0,
                              1, 129, 1, 8, 16, 0.1, 0, null)
     assert rc == _lib.FE_ERR_UNSUPPORTED
     rc = lib.fe_paged_decode(null, 0, null, null, null, 0, null, null, 1, null, 1, null, null, 0,
                              1, 64, 1, 192, 16, 0.1, 0, null)
+    assert rc == _lib.FE_ERR_INVALID_ARGUMENT
+    rc = lib.fe_paged_decode(null, 0, null, null, null, 0, null, null, 1, null, 1, null, null, 0,
+                             1, 67, 1, 136, 16, 0.1, 0, null)
     assert rc == _lib.FE_ERR_UNSUPPORTED
     # the generic shapes (head_dim 96, group 32) take no plan; without one their null
     # pointers are the error

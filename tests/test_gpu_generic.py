@@ -2,7 +2,9 @@
 head -- the generic attention kernel; at head_dim 256 in 16 bits the matrix-core
 decode (groups <= 16) and prefill instantiated at 256; and groups above 16 with a
 divisor in 8..16 (24, 32, 48, 64 below) split into virtual KV heads on the matrix-core
-decode -- against the oracle, in fp16, bf16 and fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
+decode; and 16-bit decodes at other multiples of 8 below 256 over pages of 16k
+tokens, on the matrix-core decode padded to the next of 64 / 128 / 256 -- against
+the oracle, in fp16, bf16 and fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
 head_dim 64 / 128 below run there.)
 
 The reference's Triton decode takes any head_dim (BLOCK_D = next_power_of_2
@@ -60,6 +62,13 @@ SHAPES = [
     (64, 71, 1, 16, FP16),   # 71 query heads over one KV head
     (128, 48, 1, 16, BF16),  # 48 over one
     (128, 64, 1, 32, F32),   # group 64 x 128: the generic kernel's largest item
+    (112, 16, 2, 16, BF16),  # multiples of 8 in 16 bits, pages of 16k tokens: the
+    (192, 8, 1, 32, FP16),   # matrix-core decode padded to 64 / 128 / 256
+    (48, 8, 8, 16, FP16),
+    (160, 20, 4, 64, BF16),
+    (96, 32, 1, 16, FP16),   # padded, and group 32 as two virtual KV heads
+    (24, 4, 4, 16, FP16),
+    (8, 4, 2, 16, BF16),
     (36, 6, 2, 16, FP16),    # head dims off the 16-byte vector: element loads
     (6, 4, 1, 4, F32),
     (20, 4, 2, 32, BF16),
@@ -267,6 +276,21 @@ def test_generic_prefill_matches_oracle(shape):
     exp = R.prefill_reference(_np64(q), offs.numpy(), ctx.numpy(), _np64(kp), _np64(vp),
                               tables.numpy(), shape[3])
     _close(out, exp, shape[4], f"prefill {_ids(shape)}")
+
+
+@pytest.mark.parametrize("shape", [(256, 32, 4, 16, FP16), (160, 32, 4, 16, BF16)], ids=_ids)
+def test_prefill_with_more_than_65536_rows_at_one_row_tile(shape):
+    """2100 new tokens x 32 query heads = 67200 (token, head) rows, past the size at
+    which the tile kernel's plan takes two row tiles per wave: at head_dim 256 (and
+    dims padded to it) the kernel has one, and its grid is sized for that."""
+    n_new, cached = [2100, 3], [0, 50]
+    q, offs, ctx, tables, kp, vp = _prefill_case(shape, 900 + shape[0], n_new, cached)
+    out = ops.prefill_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), tables.to(DEV), offs.to(DEV),
+                            ctx.to(DEV), max(n_new))
+    torch.cuda.synchronize()
+    exp = R.prefill_reference(_np64(q), offs.numpy(), ctx.numpy(), _np64(kp), _np64(vp),
+                              tables.numpy(), shape[3])
+    _close(out, exp, shape[4], f"prefill {_ids(shape)} 67200 rows")
 
 
 @pytest.mark.parametrize("d,hq,hkv", [(96, 12, 2), (256, 8, 1), (128, 32, 1)])

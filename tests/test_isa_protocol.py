@@ -133,7 +133,7 @@ def _plant(text: str, start: str, end: str, old: str, new: str) -> str:
 
 PLANTS = {
     # the wave's wait for its partial stores before the ticket
-    "no_wait": ("auto store_partial", "merge_pieces<D, E>(a, b, h",
+    "no_wait": ("auto store_partial", "merge_pieces<D, E, PAD>(a, b, h",
                 "wait_stores();  // this wave", "// (planted) no wait"),
     # the partial outputs written with default caching instead of sc1
     "store_not_coherent": ("auto store_partial", "store_coherent(a.ws_lse",
