@@ -17,9 +17,10 @@ stream -- and prints one JSON line per config:
   the 48 decode rows in GB/s, and the whole step.
 
 Calls are replayed from a HIP graph, so each figure is GPU time per call.
-`--configs generic` times the generic kernel's shapes (head_dim 96, 80, 256, 8 and
-a group of 32 at D = 128) at C2's 64 context lengths, and C4's prefill chunks at
-head_dim 96.
+`--configs generic` times the shapes outside head_dim 64 / 128 (96, 80, 8: the
+matrix-core kernels padded to 128 / 64 in 16 bits, the generic kernel in fp32; 160
+padded to 256; 256; a group of 32 at D = 128) at C2's 64 context lengths, and C4's
+prefill chunks at head_dim 96, 160 and 256.
 
 `--dtype bf16` runs the bf16 entry points on the same values rounded to bf16;
 `--dtype f32` the fp32 entry points on the values widened to float32 (bytes at
@@ -37,7 +38,8 @@ from flexengine_amd import ops, workloads
 
 HBM_PEAK = 8.0e12
 # (head_dim, q heads, KV heads) of `--configs generic`
-GENERIC_SHAPES = [(96, 12, 2), (80, 32, 8), (256, 8, 1), (256, 16, 8), (128, 32, 1), (8, 4, 2)]
+GENERIC_SHAPES = [(96, 12, 2), (80, 32, 8), (160, 16, 2), (256, 8, 1), (256, 16, 8),
+                  (128, 32, 1), (8, 4, 2)]
 LAYERS = 28  # Qwen2.5-1.5B: calls per model step that share one plan
 MFMA_FP16_PEAK = 2.5e15
 MFMA_FP32_PEAK = 157.3e12
@@ -191,9 +193,9 @@ def bench_c4(iters: int, copies: int, dtype=torch.float16) -> dict:
 
 
 def bench_generic_prefill(iters: int, copies: int, head_dim: int, dtype) -> dict:
-    """C4's prefill chunks (offsets, contexts, tables) at another head_dim (96: the
-    generic kernel; 256: the tile kernel instantiated at 256): TFLOP/s over the
-    valid query-key pairs."""
+    """C4's prefill chunks (offsets, contexts, tables) at another head_dim (16-bit:
+    the tile kernel at 256, or padded to 128 / 256 for 96 / 160; fp32: the generic
+    kernel): TFLOP/s over the valid query-key pairs."""
     w = workloads.c4_workload()
     gen = torch.Generator().manual_seed(96)
     nb, bs, hkv, _ = w.k_pool.shape
@@ -258,7 +260,7 @@ def main(argv=None) -> int:
             print(json.dumps(bench_decode(w.name, w, args.iters, args.copies, dtype=dt)
                              | {"dtype": args.dtype, "head_dim": d, "q_heads": hq,
                                 "kv_heads": hkv}), flush=True)
-        for d in (96, 256):
+        for d in (96, 160, 256):
             print(json.dumps(bench_generic_prefill(args.iters, args.copies, d, dt)
                              | {"dtype": args.dtype}), flush=True)
     return 0
