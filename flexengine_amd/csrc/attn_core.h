@@ -248,7 +248,11 @@ struct TileCore {
 // (LIST, block sizes that are multiples of 16) the wave's tile rows held one
 // per lane.  Column n accepts keys < limit (decode: tok_end; prefill: its
 // position + 1).
-template <int D, bool LIST = false>
+//
+// PAD: the real head_dim dr is below D (a multiple of 4): rows are dr floats
+// apart within a pool row, the dims past dr are zeros in K and V (not loaded,
+// and not written by the page write), and q is zero there too.
+template <int D, bool LIST = false, bool PAD = false>
 struct F32Core {
   static constexpr int NC = D / 16;  // 16-byte K and q chunks per lane
   static constexpr int NX = D / 16;  // output tiles of 16 dims
@@ -256,8 +260,9 @@ struct F32Core {
   const float* k_pool;
   const float* v_pool;
   const int32_t* trow;  // block-table row of the sequence
-  int64_t rs;           // elements per pool row (kv_heads * D)
-  int hoff;             // kv_head * D
+  int64_t rs;           // elements per pool row (kv_heads * head_dim)
+  int hoff;             // kv_head * head_dim
+  int dr;               // PAD: the real head_dim
   int W, NB, BS, bs_log2;
   int tok_end;          // keys >= tok_end are never read
   int limit;            // this lane's column accepts keys < limit
@@ -321,12 +326,19 @@ struct F32Core {
       if (tk == new_pos) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          kk[c] = *reinterpret_cast<const f32x4*>(knew_row + 16 * c + 4 * g);
-          *reinterpret_cast<f32x4*>(k_pool_w + off + 16 * c) = kk[c];
+          kk[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (!PAD || 16 * c + 4 * g < dr) {
+            kk[c] = *reinterpret_cast<const f32x4*>(knew_row + 16 * c + 4 * g);
+            *reinterpret_cast<f32x4*>(k_pool_w + off + 16 * c) = kk[c];
+          }
         }
       } else {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) kk[c] = *reinterpret_cast<const f32x4*>(k_pool + off + 16 * c);
+        for (int c = 0; c < NC; ++c) {
+          kk[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (!PAD || 16 * c + 4 * g < dr)
+            kk[c] = *reinterpret_cast<const f32x4*>(k_pool + off + 16 * c);
+        }
       }
     }
 #pragma unroll
@@ -337,13 +349,17 @@ struct F32Core {
       if (tv == new_pos) {
 #pragma unroll
         for (int x = 0; x < NX; ++x) {
-          vv[r][x] = vnew_row[16 * x + n];
-          v_pool_w[off + 16 * x] = vv[r][x];
+          vv[r][x] = 0.f;
+          if (!PAD || 16 * x + n < dr) {
+            vv[r][x] = vnew_row[16 * x + n];
+            v_pool_w[off + 16 * x] = vv[r][x];
+          }
         }
       } else {
 #pragma unroll
         for (int x = 0; x < NX; ++x) {
-          const float val = v_pool[off + 16 * x];
+          float val = 0.f;
+          if (!PAD || 16 * x + n < dr) val = v_pool[off + 16 * x];
           vv[r][x] = ok ? val : 0.f;
         }
       }

@@ -456,14 +456,15 @@ void piece_decode_kernel(const DecodeArgs a) {
   if constexpr (kIsF32<E>) {
     // fp32 pools: the fp32 engine (tile lists for block sizes that are multiples
     // of 16, a table lookup per key row otherwise; no plan)
-    F32Core<D, PAGE16> core;
+    F32Core<D, PAGE16, PAD> core;
     core.k_pool = reinterpret_cast<const float*>(a.k_pool);
     core.v_pool = reinterpret_cast<const float*>(a.v_pool);
     core.k_pool_w = reinterpret_cast<float*>(a.k_pool);
     core.v_pool_w = reinterpret_cast<float*>(a.v_pool);
     core.trow = a.tables + (int64_t)b * a.W;
-    core.rs = (a.Hkv / a.hdiv) * D;
-    core.hoff = (h / a.hdiv) * D;
+    core.rs = (a.Hkv / a.hdiv) * DR;
+    core.hoff = (h / a.hdiv) * DR;
+    core.dr = DR;
     core.W = a.W;
     core.NB = a.NB;
     core.BS = a.BS;
@@ -475,7 +476,7 @@ void piece_decode_kernel(const DecodeArgs a) {
     core.knew_row = nullptr;
     core.vnew_row = nullptr;
     if (a.k_new != nullptr) {
-      const int64_t nr = (int64_t)b * a.new_stride + (int64_t)(h / a.hdiv) * D;
+      const int64_t nr = (int64_t)b * a.new_stride + (int64_t)(h / a.hdiv) * DR;
       core.knew_row = reinterpret_cast<const float*>(a.k_new) + nr;
       core.vnew_row = reinterpret_cast<const float*>(a.v_new) + nr;
       core.new_pos = pc.L - 1;
@@ -483,10 +484,11 @@ void piece_decode_kernel(const DecodeArgs a) {
     {
       const int hq = h * G + (n < G ? n : G - 1);
       const float* qrow =
-          reinterpret_cast<const float*>(a.q) + (int64_t)b * a.q_stride + (int64_t)hq * D;
+          reinterpret_cast<const float*>(a.q) + (int64_t)b * a.q_stride + (int64_t)hq * DR;
 #pragma unroll
-      for (int c = 0; c < F32Core<D, PAGE16>::NC; ++c) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(qrow + 16 * c + 4 * g);
+      for (int c = 0; c < F32Core<D, PAGE16, PAD>::NC; ++c) {
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (!PAD || 16 * c + 4 * g < DR) v = *reinterpret_cast<const f32x4*>(qrow + 16 * c + 4 * g);
         core.qv[c] = n < G ? v : f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
@@ -1429,12 +1431,17 @@ int launch_decode(const DecodeArgs& a, hipStream_t stream) {
   return FE_LAUNCH_STATUS();
 }
 
-// Padded head dims: 16-bit pools, unplanned, block sizes that are multiples of 16.
+// Padded head dims, unplanned: 16-bit pools with block sizes that are multiples
+// of 16, fp32 pools (D 64 / 128) at any block size.
 template <int D, class E>
 int launch_decode_padded(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid((a.target + 2 * a.B) * a.Hkv);
-  hipLaunchKernelGGL((piece_decode_kernel<D, true, false, E, true>), grid, dim3(kThreads),
-                     PieceLds<D>::bytes, stream, a);
+  if (a.BS % kTile == 0)
+    hipLaunchKernelGGL((piece_decode_kernel<D, true, false, E, true>), grid, dim3(kThreads),
+                       PieceLds<D>::bytes, stream, a);
+  else if constexpr (kIsF32<E>)
+    hipLaunchKernelGGL((piece_decode_kernel<D, false, false, E, true>), grid, dim3(kThreads),
+                       PieceLds<D>::bytes, stream, a);
   return FE_LAUNCH_STATUS();
 }
 
@@ -1596,9 +1603,13 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
   // other multiples of 8 below 256 (16-bit, unplanned, no shared prefix, pages
   // of 16k tokens): the piece kernel at the next of 64 / 128 / 256, the dims
   // past head_dim zeros in q and K and never stored
+  // (fp32: the fp32 engine at 64 / 128, any block size; padded to 128 only when
+  // head_dim fills 3/4 of it -- the engine runs one wave per SIMD there, and at
+  // D 80 (32/8) it measured 186.5 us against the generic kernel's 173.0)
   const int dpad = mfma_padded_head_dim(head_dim);
-  const bool padded = dpad != head_dim && !f32 && plan == nullptr && cascade == nullptr &&
-                      block_size % kTile == 0;
+  const bool padded = dpad != head_dim && plan == nullptr && cascade == nullptr &&
+                      (f32 ? dpad == 64 || (dpad == 128 && 4 * head_dim >= 3 * dpad)
+                           : block_size % kTile == 0);
   if ((head_dim != 64 && head_dim != 128 && !mfma256 && !padded) || G_v > kMaxGroup)
     return decode_generic(q, q_batch_stride, out, k_new, v_new, new_batch_stride, k_pool, v_pool,
                           num_blocks, block_tables, table_stride, context_lens, workspace,
@@ -1725,6 +1736,8 @@ int decode_impl(const void* q, int64_t q_batch_stride, void* out, const void* k_
     a.pre_lse = c.out_lse;
     a.pre_splits = c.splits;
   }
+  if (f32 && padded)
+    return dpad == 64 ? launch_decode_padded<64, F32>(a, s) : launch_decode_padded<128, F32>(a, s);
   if (f32) return head_dim == 64 ? launch_decode<64, F32>(a, s) : launch_decode<128, F32>(a, s);
   if (padded) {
     if (dpad == 64)

@@ -570,9 +570,13 @@ void prefill_kernel(const PrefillArgs a) {
 // whose context does not pass it), and the result is one prefix slot per
 // (row, query head): the normalised output in pre_o and its base-2 LSE in
 // pre_lse; the grid's last workgroup writes the suffix starts.
-template <int D, bool LIST, bool CASCADE = false>
+//
+// PAD: head_dim a.dr below D (a multiple of 8): q, the pools and the output laid
+// out by a.dr, the dims past it zeros in q, K and V and never stored.
+template <int D, bool LIST, bool CASCADE = false, bool PAD = false>
 __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs a) {
   constexpr int ROWS = kWaves * 16;
+  const int DR = PAD ? a.dr : D;
   if constexpr (CASCADE) {
     if (blockIdx.x == gridDim.x - 1) {
       write_suffix_starts(a, a.q_off);
@@ -597,14 +601,15 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs
   const bool valid = row < total_rows;
   const int rc = valid ? row : r_last;
 
-  F32Core<D, LIST> core;
+  F32Core<D, LIST, PAD> core;
   core.k_pool = reinterpret_cast<const float*>(a.k_pool);
   core.v_pool = reinterpret_cast<const float*>(a.v_pool);
   core.k_pool_w = nullptr;
   core.v_pool_w = nullptr;
   core.trow = a.tables + (int64_t)(CASCADE ? rb.q0 : rb.s) * a.W;
-  core.rs = a.Hkv * D;
-  core.hoff = h * D;
+  core.rs = a.Hkv * DR;
+  core.hoff = h * DR;
+  core.dr = DR;
   core.W = a.W;
   core.NB = a.NB;
   core.BS = a.BS;
@@ -622,10 +627,13 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs
   core.new_pos = -1;
   {
     const float* qrow = reinterpret_cast<const float*>(a.q) +
-                        (int64_t)(rb.q0 + rc / G) * a.q_stride + (int64_t)(h * G + rc % G) * D;
+                        (int64_t)(rb.q0 + rc / G) * a.q_stride + (int64_t)(h * G + rc % G) * DR;
 #pragma unroll
-    for (int c = 0; c < F32Core<D, LIST>::NC; ++c)
-      core.qv[c] = *reinterpret_cast<const f32x4*>(qrow + 16 * c + 4 * g);
+    for (int c = 0; c < F32Core<D, LIST, PAD>::NC; ++c) {
+      core.qv[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (!PAD || 16 * c + 4 * g < DR)
+        core.qv[c] = *reinterpret_cast<const f32x4*>(qrow + 16 * c + 4 * g);
+    }
   }
   core.init_acc();
   core.run(0, 1, (core.tok_end + kTile - 1) / kTile);
@@ -636,13 +644,14 @@ __global__ __launch_bounds__(kThreads) void prefill_f32_kernel(const PrefillArgs
     if constexpr (CASCADE) {
       float* orow = a.pre_o + r * D + 4 * g;
 #pragma unroll
-      for (int x = 0; x < F32Core<D, LIST>::NX; ++x)
+      for (int x = 0; x < F32Core<D, LIST, PAD>::NX; ++x)
         *reinterpret_cast<f32x4*>(orow + 16 * x) = core.o[x] * inv;
       if (g == 0) a.pre_lse[r] = l > 0.f ? core.m_run + log2f(l) : kNegInf;
     } else {
 #pragma unroll
-      for (int x = 0; x < F32Core<D, LIST>::NX; ++x)
-        store_out4<F32>(a.out, r * D + 4 * g + 16 * x, core.o[x] * inv);
+      for (int x = 0; x < F32Core<D, LIST, PAD>::NX; ++x)
+        if (!PAD || 4 * g + 16 * x < DR)
+          store_out4<F32>(a.out, r * DR + 4 * g + 16 * x, core.o[x] * inv);
     }
   }
 }
@@ -2172,8 +2181,9 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   const bool mfma256 = head_dim == 256 && !f32 && step_plan == nullptr;
   // other multiples of 8 below 256 in 16 bits (no plan): the tile kernel at the
   // next of 64 / 128 / 256, the dims past head_dim zeros
+  // (fp32: the fp32 engine at 64 / 128)
   const int dpad = mfma_padded_head_dim(head_dim);
-  const bool padded = dpad != head_dim && !f32 && step_plan == nullptr;
+  const bool padded = dpad != head_dim && step_plan == nullptr && (!f32 || dpad <= 128);
   if (head_dim != 64 && head_dim != 128 && !mfma256 && !padded)
     return prefill_generic(q, out, k_pool, v_pool, num_blocks, block_tables, table_stride,
                            q_offsets, context_lens, num_seqs, total_q, num_q_heads, kv_heads,
@@ -2209,13 +2219,22 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
     a.bs_log2 = bs_log2;
     a.NB = num_blocks;
     a.KS = 1;
+    a.dr = head_dim;
     a.scale_log2 = scale * kLog2e;
     const int64_t blocks = ((int64_t)total_q * a.G + kWaves * 16 - 1) / (kWaves * 16) + num_seqs;
     if (blocks * kv_heads >= ((int64_t)1 << 31)) return FE_ERR_UNSUPPORTED;
     const dim3 grid((unsigned)(blocks * kv_heads));
     const hipStream_t s = (hipStream_t)stream;
     const bool list = block_size % kTile == 0;  // tile rows held per lane
-    if (head_dim == 64 && list)
+    if (padded && dpad == 64 && list)
+      hipLaunchKernelGGL((prefill_f32_kernel<64, true, false, true>), grid, dim3(kThreads), 0, s, a);
+    else if (padded && dpad == 64)
+      hipLaunchKernelGGL((prefill_f32_kernel<64, false, false, true>), grid, dim3(kThreads), 0, s, a);
+    else if (padded && list)
+      hipLaunchKernelGGL((prefill_f32_kernel<128, true, false, true>), grid, dim3(kThreads), 0, s, a);
+    else if (padded)
+      hipLaunchKernelGGL((prefill_f32_kernel<128, false, false, true>), grid, dim3(kThreads), 0, s, a);
+    else if (head_dim == 64 && list)
       hipLaunchKernelGGL((prefill_f32_kernel<64, true>), grid, dim3(kThreads), 0, s, a);
     else if (head_dim == 64)
       hipLaunchKernelGGL((prefill_f32_kernel<64, false>), grid, dim3(kThreads), 0, s, a);

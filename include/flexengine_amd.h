@@ -33,7 +33,10 @@
  * at any other head_dim that is a multiple of 8 below 256 runs on the
  * matrix-core decode padded to the next of 64 / 128 / 256 (the dims past
  * head_dim are zeros, never read from the pool nor written to the output;
- * its workspace is sized at the padded head_dim).  Every other head_dim from 1 to 512, and decode groups of 17
+ * its workspace is sized at the padded head_dim), and so does the 16-bit
+ * prefill at any block size; fp32 runs padded on its own engine at 64 / 128
+ * (any block size): the decode at multiples of 8 up to 64 and from 96 to 120,
+ * the prefill at every multiple of 8 below 128.  Every other head_dim from 1 to 512, and decode groups of 17
  * to 128, run on a generic kernel (key splits of a row or tiles of prefill
  * tokens per workgroup, fp32 arithmetic) as long as group * head_dim <= 8192
  * (head_dim rounded up to a multiple of 8): same entry points, same results

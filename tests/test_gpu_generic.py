@@ -3,8 +3,10 @@ head -- the generic attention kernel; at head_dim 256 in 16 bits the matrix-core
 decode (groups <= 16) and prefill instantiated at 256; and groups above 16 with a
 divisor in 8..16 (24, 32, 48, 64 below) split into virtual KV heads on the matrix-core
 decode; and 16-bit decodes at other multiples of 8 below 256 over pages of 16k
-tokens, on the matrix-core decode padded to the next of 64 / 128 / 256 -- against
-the oracle, in fp16, bf16 and fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
+tokens, on the matrix-core decode padded to the next of 64 / 128 / 256 (fp32 up to 64
+and from 96 to 120 at any block size, on the fp32 engine padded to 64 / 128; the
+prefills alike, fp32 at every multiple of 8 below 128)
+-- against the oracle, in fp16, bf16 and fp32.  (The matrix-core prefill takes any group size: the group-24 / 32 cases at
 head_dim 64 / 128 below run there.)
 
 The reference's Triton decode takes any head_dim (BLOCK_D = next_power_of_2
@@ -69,6 +71,10 @@ SHAPES = [
     (96, 32, 1, 16, FP16),   # padded, and group 32 as two virtual KV heads
     (24, 4, 4, 16, FP16),
     (8, 4, 2, 16, BF16),
+    (48, 8, 2, 16, F32),     # fp32 multiples of 8 up to 64, and 96 / 104 / 112: the
+    (112, 16, 4, 8, F32),    # fp32 engine padded to 64 / 128 at any block size (the
+    (40, 32, 1, 16, F32),    # synthetic model's D 8 above too); group 32 as two
+    (80, 8, 2, 16, F32),     # virtual heads; D 80 stays on the generic kernel
     (36, 6, 2, 16, FP16),    # head dims off the 16-byte vector: element loads
     (6, 4, 1, 4, F32),
     (20, 4, 2, 32, BF16),
