@@ -473,12 +473,12 @@ def main(argv=None) -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "kernel": (f"piece_decode_kernel<128, true, true, {elem}> (fe_paged_decode_planned"
+            "kernel": (f"piece_decode_kernel<128, true, true, {elem}, false> (fe_paged_decode_planned"
                        f"{sfx}: page write + split-K attention + in-kernel LSE merge, one "
                        f"launch; achieved includes {-(-steps // LAYERS)} decode_plan_kernel "
                        f"launch(es) over the {steps} launches)")
                       if planned else
-                      f"piece_decode_kernel<128, true, false, {elem}> (fe_paged_decode{sfx}: "
+                      f"piece_decode_kernel<128, true, false, {elem}, false> (fe_paged_decode{sfx}: "
                       "page write + split-K attention + in-kernel LSE merge, one launch)",
             "us_per_launch": round(per_launch_ms * 1e3, 3),
             "us_per_launch_unplanned": None if other_us is None else round(other_us, 3),
