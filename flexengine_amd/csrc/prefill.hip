@@ -196,13 +196,13 @@ __device__ void write_suffix_starts(const PrefillArgs& a, Offs offs) {
 // m_run (base 2) and its sum l.  One split: normalise and store.  Several:
 // write this split's partial (device-coherent stores), draw the row block's
 // ticket; the last split merges all of them.
-template <int D, int RT, class E, bool PAD = false>
+template <int D, int RT, class E, bool PAD = false, int DC = D>
 __device__ __forceinline__ void finish_split(const PrefillArgs& a, const RowBlock& rb, int item,
                                              int h, int ks, int wr0, int r0, int r_last,
                                              const bool (&valid)[RT], const float (&m_run)[RT],
-                                             const float (&l)[RT], const f32x4 (&o)[RT][D / 16],
+                                             const float (&l)[RT], const f32x4 (&o)[RT][DC / 16],
                                              int* last) {
-  constexpr int NX = D / 16;
+  constexpr int NX = DC / 16;  // output tiles computed
   const int DR = PAD ? a.dr : D;  // output row length
   const int G = a.G;
   const int tid = threadIdx.x;
@@ -308,11 +308,17 @@ __device__ __forceinline__ void finish_split(const PrefillArgs& a, const RowBloc
 //
 // PAD: head_dim a.dr below D (a multiple of 8): q, the pools and the output are
 // laid out by a.dr; the dims past it are zeros in q, K and V (never loaded)
-// and never stored.
-template <int D, int RT, class E = Fp16, bool PAD = false>
+// and never stored.  DC (a multiple of 32, a.dr <= DC <= D): the dims the
+// products compute -- the K/V staging keeps D's layout, q.K runs DC / 32
+// k-chunks and P.V DC / 16 output tiles, so the all-zero ones drop out at
+// compile time.
+template <int D, int RT, class E = Fp16, bool PAD = false, int DC = D>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8)))
 void prefill_kernel(const PrefillArgs a) {
   using P = PCfg<D, RT>;
+  static_assert(DC % 32 == 0 && DC <= D && (PAD || DC == D), "computed dims");
+  constexpr int NCC = DC / 32;  // k-chunks of q.K computed
+  constexpr int NXC = DC / 16;  // output tiles computed
   const int DR = PAD ? a.dr : D;
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -349,7 +355,7 @@ void prefill_kernel(const PrefillArgs a) {
 
   // ---- this lane's rows: query vectors (B operand), last key each may see
   //      (its position) ----
-  f16x8 qv[RT][P::NC];
+  f16x8 qv[RT][NCC];
   int pos[RT];
   bool valid[RT];
 #pragma unroll
@@ -360,7 +366,7 @@ void prefill_kernel(const PrefillArgs a) {
     pos[rt] = valid[rt] ? cached + rc / G : -1;
     const f16* qrow = a.q + (int64_t)(rb.q0 + rc / G) * a.q_stride + (h * G + rc % G) * DR + 8 * g;
 #pragma unroll
-    for (int c = 0; c < P::NC; ++c) {
+    for (int c = 0; c < NCC; ++c) {
       const f16x8 v = !PAD || 32 * c + 8 * g < DR ? ld16(qrow + 32 * c) : f16x8{};
       qv[rt][c] = valid[rt] ? v : f16x8{};
     }
@@ -370,13 +376,13 @@ void prefill_kernel(const PrefillArgs a) {
   const int unmasked_blocks = (cached + min(wr0, r_last) / G + 1) / kBlockKeys;
 
   float m_run[RT], l_run[RT];
-  f32x4 o[RT][P::NX];
+  f32x4 o[RT][NXC];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     m_run[rt] = kNegInf;
     l_run[rt] = 0.f;
 #pragma unroll
-    for (int x = 0; x < P::NX; ++x) o[rt][x] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int x = 0; x < NXC; ++x) o[rt][x] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   // ---- K/V block staging: thread t loads 16-byte chunk t % CPR of key rows
@@ -454,7 +460,7 @@ void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) st[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < P::NC; ++c) {
+      for (int c = 0; c < NCC; ++c) {
         const f16x8 kv =
             *reinterpret_cast<const f16x8*>(kbase + (16 * kt + n) * P::KP + (32 * c + 8 * g) * 2);
 #pragma unroll
@@ -494,7 +500,7 @@ void prefill_kernel(const PrefillArgs a) {
         const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run[rt] - m_new);
         l_run[rt] *= alpha;
 #pragma unroll
-        for (int x = 0; x < P::NX; ++x) o[rt][x] *= alpha;
+        for (int x = 0; x < NXC; ++x) o[rt][x] *= alpha;
         m_run[rt] = m_new;
       }
       const float neg_m = m_run[rt] == kNegInf ? 0.f : -m_run[rt];
@@ -526,7 +532,7 @@ void prefill_kernel(const PrefillArgs a) {
     for (int ps = 0; ps < kPS; ++ps) {
       const unsigned char* vb = vbase + (32 * ps + 4 * g + (n >> 2)) * P::VP + (n & 3) * 8;
 #pragma unroll
-      for (int x = 0; x < P::NX; ++x) {
+      for (int x = 0; x < NXC; ++x) {
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) s16x4*)(vb + 32 * x));
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -550,7 +556,7 @@ void prefill_kernel(const PrefillArgs a) {
     lt[rt] += shfl_xor_f(lt[rt], 32);
   }
   __shared__ int last;
-  finish_split<D, RT, E, PAD>(a, rb, item, h, ks, wr0, r0, r_last, valid, m_run, lt, o, &last);
+  finish_split<D, RT, E, PAD, DC>(a, rb, item, h, ks, wr0, r0, r_last, valid, m_run, lt, o, &last);
 }
 
 // ---------------------------------------------------------------------------
@@ -2002,10 +2008,10 @@ inline int log2_exact(int x) {
   return l;
 }
 
-template <int D, int RT, class E = Fp16, bool PAD = false>
+template <int D, int RT, class E = Fp16, bool PAD = false, int DC = D>
 void launch_prefill(const PrefillArgs& a, int blocks, hipStream_t stream) {
   using P = PCfg<D, RT>;
-  hipLaunchKernelGGL((prefill_kernel<D, RT, E, PAD>), dim3(blocks * a.Hkv * a.KS),
+  hipLaunchKernelGGL((prefill_kernel<D, RT, E, PAD, DC>), dim3(blocks * a.Hkv * a.KS),
                      dim3(kThreads), 2 * P::STAGE, stream, a);
 }
 
@@ -2302,8 +2308,23 @@ int prefill_impl(const void* q, void* out, const void* k_pool, const void* v_poo
   } else if (dma) {
     if (head_dim == 64) launch_prefill_dma<64, Fp16>(a, s); else launch_prefill_dma<128, Fp16>(a, s);
   } else if (padded && dpad == 256) {
-    if (bf16) launch_prefill<256, 1, Bf16, true>(a, p.blocks, s);
-    else launch_prefill<256, 1, Fp16, true>(a, p.blocks, s);
+    // computed dims: 160 (head_dim 136-160), 192 (168-192), else all 256
+    if (head_dim <= 160) {
+      if (bf16) launch_prefill<256, 1, Bf16, true, 160>(a, p.blocks, s);
+      else launch_prefill<256, 1, Fp16, true, 160>(a, p.blocks, s);
+    } else if (head_dim <= 192) {
+      if (bf16) launch_prefill<256, 1, Bf16, true, 192>(a, p.blocks, s);
+      else launch_prefill<256, 1, Fp16, true, 192>(a, p.blocks, s);
+    } else {
+      if (bf16) launch_prefill<256, 1, Bf16, true>(a, p.blocks, s);
+      else launch_prefill<256, 1, Fp16, true>(a, p.blocks, s);
+    }
+  } else if (padded && dpad == 128 && head_dim <= 96) {
+    // head_dim 72-96: 96 computed dims of 128
+    if (bf16) p.rt == 2 ? launch_prefill<128, 2, Bf16, true, 96>(a, p.blocks, s)
+                        : launch_prefill<128, 1, Bf16, true, 96>(a, p.blocks, s);
+    else p.rt == 2 ? launch_prefill<128, 2, Fp16, true, 96>(a, p.blocks, s)
+                   : launch_prefill<128, 1, Fp16, true, 96>(a, p.blocks, s);
   } else if (padded) {
     const bool r2 = p.rt == 2;
     if (dpad == 64) {

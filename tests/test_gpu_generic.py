@@ -284,11 +284,13 @@ def test_generic_prefill_matches_oracle(shape):
     _close(out, exp, shape[4], f"prefill {_ids(shape)}")
 
 
-@pytest.mark.parametrize("shape", [(256, 32, 4, 16, FP16), (160, 32, 4, 16, BF16)], ids=_ids)
+@pytest.mark.parametrize("shape", [(256, 32, 4, 16, FP16), (160, 32, 4, 16, BF16),
+                                   (96, 32, 4, 16, FP16)], ids=_ids)
 def test_prefill_with_more_than_65536_rows_at_one_row_tile(shape):
     """2100 new tokens x 32 query heads = 67200 (token, head) rows, past the size at
     which the tile kernel's plan takes two row tiles per wave: at head_dim 256 (and
-    dims padded to it) the kernel has one, and its grid is sized for that."""
+    dims padded to it) the kernel has one, and its grid is sized for that; at 96
+    (padded to 128, 96 dims computed) the two-tile form runs."""
     n_new, cached = [2100, 3], [0, 50]
     q, offs, ctx, tables, kp, vp = _prefill_case(shape, 900 + shape[0], n_new, cached)
     out = ops.prefill_paged(q.to(DEV), kp.to(DEV), vp.to(DEV), tables.to(DEV), offs.to(DEV),
